@@ -1,0 +1,240 @@
+"""Benchmark: na2d 56x56 k=7 bf16 fused forward + backward on one MI355X.
+
+Workload: q, k, v, dO ~ N(0,1) bf16
+[B=4, 56, 56, heads=4, head_dim=32], kernel 7x7, non-causal, stride 1;
+dilation 1 is the timed step, dilation 4 is timed alongside and reported
+under "dilation4".  One step = forward (out + LSE) and backward
+(dq, dk, dv) through the public API, captured once in a HIP graph and
+replayed (eager timing is reported too).
+
+Printed JSON line (rank 0): metric/value/unit per the driver contract, with
+ * roofline: the dominant library call timed with HIP events on the stream
+   it runs on, algorithmic bytes / duration against 8 TB/s HBM;
+ * cpu_baseline: the CPU oracle (a restatement of the reference's pure
+   backend: gather neighbors, masked softmax, weighted sum; backward by
+   autograd) on a bounded sample, timed on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "natten-mlx_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+B, HH, WW, HEADS, D, K = 4, 56, 56, 4, 32, 7
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def algorithmic(n_valid: int):
+    """FLOPs and compulsory HBM bytes (valid neighbors only; LSE fp32)."""
+    qh = B * HH * WW * HEADS
+    t = B * HH * WW * HEADS * D * 2  # one bf16 tensor
+    lse = qh * 4
+    fwd_flops = qh * 4 * D * n_valid
+    bwd_flops = qh * 8 * D * n_valid
+    fwd_bytes = 4 * t + lse                 # q, k, v read; out written; lse written
+    bwd_bytes = 5 * t + lse + 3 * t         # q, k, v, out, dO, lse read; dq, dk, dv written
+    return fwd_flops, bwd_flops, fwd_bytes, bwd_bytes
+
+
+def make_inputs(device):
+    g = torch.Generator().manual_seed(0)
+    shape = (B, HH, WW, HEADS, D)
+    return [torch.randn(shape, generator=g).to(torch.bfloat16).to(device) for _ in range(4)]
+
+
+def run_gpu(args):
+    import natten_amd
+    from natten_amd._core import _lib, hip
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    q, k, v, do = make_inputs(dev)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+
+    def step(dil):
+        out = natten_amd.na2d(q, k, v, K, dilation=dil)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    results = {}
+    for dil in (1, 4):
+        for _ in range(args.warmup):
+            step(dil)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(dil)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+        graph_ms = None
+        graph_ok = None
+        if not args.no_graph:
+            try:
+                eager_ref = [g.clone() for g in step(dil)]
+                s = torch.cuda.Stream()
+                s.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(s):
+                    for _ in range(3):
+                        step(dil)
+                torch.cuda.current_stream().wait_stream(s)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    static_grads = step(dil)
+                graph_ok = True
+                for i in range(3):
+                    graph.replay()
+                    torch.cuda.synchronize()
+                    for a, b in zip(static_grads, eager_ref):
+                        graph_ok = graph_ok and torch.equal(a, b)
+                for _ in range(args.warmup):
+                    graph.replay()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    graph.replay()
+                torch.cuda.synchronize()
+                graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+                del graph
+            except Exception as exc:  # report, keep the eager number
+                print(f"[bench] graph capture unavailable: {exc}", file=sys.stderr, flush=True)
+                graph_ms, graph_ok = None, None
+
+        # per-call kernel durations with HIP events on torch's current stream
+        qd, kd, vd = q.detach(), k.detach(), v.detach()
+        ks, st, dl, ca = (K, K), (1, 1), (dil, dil), (False, False)
+        out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
+        n = max(args.steps, 20)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        fwd_t, bwd_t = 0.0, 0.0
+        for _ in range(n):
+            ev[0].record()
+            hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
+            ev[1].record()
+            hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca, None)
+            ev[2].record()
+            torch.cuda.synchronize()
+            fwd_t += ev[0].elapsed_time(ev[1])
+            bwd_t += ev[1].elapsed_time(ev[2])
+        results[dil] = dict(eager_ms=eager_ms, graph_ms=graph_ms, graph_ok=graph_ok,
+                            fwd_ms=fwd_t / n, bwd_ms=bwd_t / n)
+    return results
+
+
+def run_cpu_baseline():
+    """Oracle fwd+bwd in bf16 on a bounded sample: one of the B=4 images."""
+    from oracle import na as O
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    shape = (1, HH, WW, HEADS, D)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def once():
+        out = O.na_forward(q, k, v, K, 1, 1, False, None, compute_dtype=torch.bfloat16)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    once()  # warmup
+    times = []
+    deadline = time.perf_counter() + 20.0
+    while len(times) < 5 and (not times or time.perf_counter() < deadline):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    per_sample_s = times[len(times) // 2]
+    return per_sample_s * B, threads  # scaled to the full B=4 step
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(batch/head sharding needs no communication; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+
+    res = run_gpu(args)
+    fwd_f, bwd_f, fwd_b, bwd_b = algorithmic(K * K)
+    r1 = res[1]
+    step_ms = r1["graph_ms"] if r1["graph_ms"] is not None and r1["graph_ok"] else r1["eager_ms"]
+    total_flops = fwd_f + bwd_f
+    value = total_flops / (step_ms * 1e-3) / 1e12
+
+    # dominant call: the one with the larger event-timed duration
+    if r1["bwd_ms"] >= r1["fwd_ms"]:
+        dom, dom_ms, dom_bytes, dom_flops = "na_bwd", r1["bwd_ms"], bwd_b, bwd_f
+    else:
+        dom, dom_ms, dom_bytes, dom_flops = "na_fwd", r1["fwd_ms"], fwd_b, fwd_f
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                "call": dom, "call_ms": round(dom_ms, 5),
+                "mfma_frac": round(dom_flops / (dom_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 6)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu_s, threads = run_cpu_baseline()
+        cpu = {"value": round(total_flops / cpu_s / 1e12, 6), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": "oracle (pure-backend restatement) fwd+bwd in bf16 on 1 of the 4 "
+                         "images, median of <=5 runs, scaled x4 to the full step",
+               "ms_per_step": round(cpu_s * 1e3, 2)}
+
+    line = {
+        "metric": "na2d 56x56 k7 bf16 fwd+bwd ms & TFLOP/s; % MFMA/HBM roofline, 1 MI355X",
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), seed 0",
+        "config": {"workload": "na2d fused fwd+bwd, B=4 56x56 heads=4 head_dim=32 k=7 "
+                               "dilation=1 non-causal",
+                   "global_batch": B, "spatial": [HH, WW], "heads": HEADS, "head_dim": D,
+                   "kernel_size": K, "dilation": 1, "parallelism": "none (1 GPU)"},
+        "timing": {"graph_ms": r1["graph_ms"], "graph_replays_match_eager": r1["graph_ok"],
+                   "eager_ms": round(r1["eager_ms"], 5), "fwd_call_ms": round(r1["fwd_ms"], 5),
+                   "bwd_call_ms": round(r1["bwd_ms"], 5)},
+        "dilation4": {k2: (round(v2, 5) if isinstance(v2, float) else v2)
+                      for k2, v2 in res[4].items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,184 @@
+/*
+ * natten_amd.h — C ABI of the MI355X (gfx950) neighborhood-attention library
+ * (libnatten_amd.so).
+ *
+ * The library replaces the accelerated tiers behind natten-mlx's backend
+ * registry (reference: src/natten_mlx/_core/ops.py:14-135, the nanobind
+ * module src/natten_mlx/_core/_nanobind_ext.cpp:22-278 and the Metal
+ * kernels under src/natten_mlx/_core/nanobind/ and _core/_metal_sources.py).
+ * Every entry point works on caller-owned device buffers in the reference's
+ * spatial-first layout and never allocates or frees device memory:
+ *
+ *   query / out / dq          [B, X0, X1, X2, H,    D]   (rank < 3: leading X = 1)
+ *   key / value / dk / dv     [B, X0, X1, X2, H_kv, D]
+ *   extra key / value         [B, N_extra, H_kv, D]
+ *   logits / attn             [B, O0, O1, O2, H, K0*K1*K2]   O_a = ceil(X_a / stride_a)
+ *   lse / dlse                [B, O0, O1, O2, H]  float32
+ *
+ * All tensors are dense and contiguous.  Query head h reads key/value head
+ * h / (H / H_kv) (GQA/MQA without materialising the repeat, reference
+ * functional.py:29-68).  Launches are asynchronous on the caller's HIP stream
+ * (a hipStream_t passed as void*, NULL = default stream); nothing
+ * synchronises the device.  Return value: NA_OK or an NA_ERR_* code, with a
+ * thread-local message in na_last_error().  No C++ exception crosses the ABI.
+ */
+#ifndef NATTEN_AMD_H
+#define NATTEN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NA_ABI_VERSION 1
+
+enum na_dtype { NA_F32 = 0, NA_F16 = 1, NA_BF16 = 2 };
+
+enum na_status {
+  NA_OK = 0,
+  NA_ERR_INVALID = 1,     /* malformed parameters or shapes */
+  NA_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+  NA_ERR_LAUNCH = 3,      /* HIP launch / runtime failure */
+  NA_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+/* na_params.flags */
+enum na_flags {
+  /* Every query attends to every key of its sample (the FMHA fast path of
+   * functional.py:141-187, taken when the kernel covers the extent). */
+  NA_FLAG_DENSE = 1
+};
+
+/*
+ * Problem description shared by every entry point.  Per-axis arrays are
+ * given for rank axes in order (X0 = depth, X1 = height, X2 = width for
+ * rank 3; X0 = length for rank 1) and are normalised internally to three
+ * axes by prepending unit axes.  Mirrors the normalised tuples the
+ * reference backends receive (ops.py:49-135).
+ */
+typedef struct na_params {
+  int32_t rank;        /* 1, 2 or 3 */
+  int32_t batch;       /* B */
+  int32_t heads;       /* H (query heads) */
+  int32_t kv_heads;    /* H_kv, divides H */
+  int32_t head_dim;    /* D */
+  int32_t dtype;       /* enum na_dtype of q/k/v/out (and logits/attn) */
+  int32_t extent[3];   /* spatial size per axis (the padded maximum for varlen) */
+  int32_t kernel[3];   /* neighborhood size per axis */
+  int32_t dilation[3];
+  int32_t stride[3];
+  int32_t causal[3];   /* 0 / 1 per axis */
+  float scale;         /* logit scale (the caller resolves None -> D^-0.5) */
+  int32_t n_extra;     /* number of additional (global) key/value tokens */
+  int32_t flags;       /* enum na_flags */
+  /* Optional device pointer to int32 [batch, rank] per-sample extents
+   * (varlen, functional.py:697-828); NULL = every sample uses extent[]. */
+  const int32_t *sample_extent;
+} na_params;
+
+int na_abi_version(void);
+const char *na_last_error(void);
+
+/* ---- window math: host twins of the device helpers (bit-exact) --------- */
+/* utils/window.py:8-34 */
+int32_t na_window_start(int32_t index, int32_t length, int32_t kernel_size,
+                        int32_t neighborhood_size, int32_t dilation);
+/* utils/window.py:37-39 */
+int32_t na_window_end(int32_t start, int32_t length, int32_t kernel_size,
+                      int32_t dilation);
+/* utils/window.py:42-62 (also extras/allin1/reference_impl.py:32-45) */
+int32_t na_pb_start(int32_t index, int32_t length, int32_t kernel_size,
+                    int32_t neighborhood_size, int32_t dilation);
+/* dilation-partition form, extras/allin1/reference_impl.py:13-25 */
+int32_t na_window_start_partition(int32_t index, int32_t length,
+                                  int32_t kernel_size,
+                                  int32_t neighborhood_size, int32_t dilation);
+
+/*
+ * Device-computed neighbor table for checking the device helpers: writes
+ * the clipped linear key index (int32) and validity (uint8) of every
+ * (output position, kernel slot) pair, [O0, O1, O2, K0*K1*K2] each, exactly
+ * as pure.py:24-152 builds them.  Uses extent[], not sample_extent.
+ */
+int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
+                      void *stream);
+
+/* ---- fused neighborhood attention --------------------------------------- */
+/*
+ * out = softmax(scale * q k_nbr^T masked) v_nbr over each query's window
+ * (plus the n_extra additional tokens, joined into the same softmax, which
+ * equals the reference's merge_attentions composition, functional.py:277-292).
+ * lse (float32, natural log) may be NULL.  Replaces na{1,2,3}d_forward
+ * (ops.py:49-58; pure.py:155-255; fast_metal.py:2524-2763) and the
+ * varlen forward (autograd/na1d.py:76-80; pure.py:497-688).  Queries beyond
+ * a sample's extent get out = 0 and lse = 0.
+ */
+int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
+           const void *extra_k, const void *extra_v, void *out, float *lse,
+           void *stream);
+
+/* Bytes of device workspace na_bwd needs for these parameters. */
+size_t na_bwd_workspace_bytes(const na_params *p);
+
+/*
+ * Gradients of the fused op given out, lse (from na_fwd) and dout; dlse
+ * (gradient w.r.t. the returned lse, float32) may be NULL.  Writes dq, dk,
+ * dv in full (zero where nothing contributes: non-strided query positions,
+ * varlen padding) and, when n_extra > 0 and the pointers are non-NULL, the
+ * additional-token gradients.  Deterministic: no atomics.  Replaces
+ * na{1,2,3}d_backward (ops.py:100-110) and the fused SIMD backward that the
+ * VJP calls directly (autograd/na2d.py:34-53; fast_metal.py:2390-2521).
+ */
+int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
+           const void *extra_k, const void *extra_v, const void *out,
+           const float *lse, const void *dout, const float *dlse, void *dq,
+           void *dk, void *dv, void *d_extra_k, void *d_extra_v,
+           void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- split operators ----------------------------------------------------- */
+/* logits = scale * <q, k_nbr>, -inf for invalid slots; ops.py:61-80,
+ * pure.py:258-283,320-359,404-449.  logits in p->dtype. */
+int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,
+              void *stream);
+/* out = sum over valid slots attn * v_nbr; pure.py:286-317,362-401,452-494. */
+int na_av_fwd(const na_params *p, const void *attn, const void *v, void *out,
+              void *stream);
+/* (dq, dk) of na_qk_fwd; ops.py:112-131, pure.py:739-808. */
+int na_qk_bwd(const na_params *p, const void *q, const void *k,
+              const void *dlogits, void *dq, void *dk, void *stream);
+/* (dattn, dv) of na_av_fwd; ops.py:116-135, pure.py:750-808. */
+int na_av_bwd(const na_params *p, const void *attn, const void *v,
+              const void *dout, void *dattn, void *dv, void *stream);
+
+/* ---- DiNAT all-in-one 1D operators (extras/allin1) ----------------------- */
+/*
+ * logits[b,i,h,k] = <q[b,i,h] * scale, key[b, n_i + k*dilation, h]>
+ *                   + rpb[h, pb_i + k]        (-inf outside the window)
+ * q, key: [B, L, H, D] in `dtype`; rpb: float32 [H, 2K-1] or NULL (zeros);
+ * logits: float32 [B, L, H, K].  has_scale = 0 skips the scaling, matching
+ * scale=None.  Replaces extras/allin1/__init__.py:40-79 and
+ * functional_metal.py:1921-1976.
+ */
+int na1d_qk_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
+                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
+                    float scale, int32_t has_scale, int32_t dtype,
+                    const void *q, const void *key, const float *rpb,
+                    float *logits, void *stream);
+/*
+ * out[b,i,h,:] = sum_k attn[b,i,h,k] * value[b, n_i + k*dilation, h, :]
+ * attn: float32 [B, L, H, K]; value [B, L, H, D] in `dtype`;
+ * out: float32 [B, L, H, D].  Replaces extras/allin1/__init__.py:82-109 and
+ * functional_metal.py:1979-2033.
+ */
+int na1d_av_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
+                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
+                    int32_t dtype, const float *attn, const void *value,
+                    float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NATTEN_AMD_H */

@@ -1,0 +1,302 @@
+// na_api.hip — the exported C ABI (include/natten_amd.h): parameter
+// validation, problem normalisation and kernel selection.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "na_common.h"
+#include "na_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int launch_status(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(NA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  g_error.clear();
+  return NA_OK;
+}
+
+constexpr int kMaxHeadDim = 1024;
+
+// Normalise the public parameters to the three-axis device problem.
+int make_prob(const na_params *p, na::Prob *P, bool allow_varlen) {
+  if (p == nullptr) return fail(NA_ERR_INVALID, "params is NULL");
+  if (p->rank < 1 || p->rank > 3)
+    return fail(NA_ERR_INVALID, "rank must be 1, 2 or 3, got %d", p->rank);
+  if (p->batch < 0 || p->heads < 1 || p->kv_heads < 1 || p->head_dim < 1)
+    return fail(NA_ERR_INVALID,
+                "batch/heads/kv_heads/head_dim must be positive "
+                "(got %d/%d/%d/%d)",
+                p->batch, p->heads, p->kv_heads, p->head_dim);
+  if (p->heads % p->kv_heads != 0)
+    return fail(NA_ERR_INVALID,
+                "heads (%d) must be divisible by kv_heads (%d)", p->heads,
+                p->kv_heads);
+  if (p->dtype != NA_F32 && p->dtype != NA_F16 && p->dtype != NA_BF16)
+    return fail(NA_ERR_INVALID, "unknown dtype %d", p->dtype);
+  if (p->n_extra < 0)
+    return fail(NA_ERR_INVALID, "n_extra must be >= 0, got %d", p->n_extra);
+  if (!allow_varlen && p->sample_extent != nullptr)
+    return fail(NA_ERR_UNSUPPORTED,
+                "per-sample extents are only supported by na_fwd/na_bwd");
+  if ((p->head_dim % 8 != 0 && p->head_dim > 128) ||
+      p->head_dim > kMaxHeadDim)
+    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported",
+                p->head_dim);
+  const bool dense = (p->flags & NA_FLAG_DENSE) != 0;
+  P->rank = p->rank;
+  P->B = p->batch;
+  P->H = p->heads;
+  P->Hkv = p->kv_heads;
+  P->rep = p->heads / p->kv_heads;
+  P->D = p->head_dim;
+  P->scale = p->scale;
+  P->n_extra = p->n_extra;
+  P->dense = dense ? 1 : 0;
+  P->sample_extent = p->sample_extent;
+  P->kprod = 1;
+  const int lead = 3 - p->rank;
+  for (int a = 0; a < 3; ++a) {
+    na::Axis &x = P->ax[a];
+    if (a < lead) {
+      x.L = 1;
+      x.K = 1;
+      x.d = 1;
+      x.s = 1;
+      x.causal = 0;
+    } else {
+      const int i = a - lead;
+      x.L = p->extent[i];
+      x.K = p->kernel[i];
+      x.d = p->dilation[i];
+      x.s = p->stride[i];
+      x.causal = p->causal[i] ? 1 : 0;
+      if (x.L < 1)
+        return fail(NA_ERR_INVALID, "extent[%d] must be positive, got %d", i,
+                    x.L);
+      if (x.K < 1 || x.d < 1 || x.s < 1)
+        return fail(NA_ERR_INVALID,
+                    "kernel/dilation/stride[%d] must be positive "
+                    "(got %d/%d/%d)",
+                    i, x.K, x.d, x.s);
+      if (!dense && x.K > x.L)
+        return fail(NA_ERR_INVALID, "kernel_size[%d]=%d exceeds extent %d", i,
+                    x.K, x.L);
+      if (dense && (x.s != 1 || x.causal))
+        return fail(NA_ERR_INVALID,
+                    "dense attention requires stride 1 and no causal mask");
+    }
+    x.O = (x.L + x.s - 1) / x.s;
+    P->kprod *= x.K;
+  }
+  return NA_OK;
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+size_t delta_bytes(const na::Prob &P) {
+  return align256(sizeof(float) * (size_t)P.B * P.ax[0].O * P.ax[1].O *
+                  P.ax[2].O * P.H);
+}
+
+}  // namespace
+
+extern "C" {
+
+int na_abi_version(void) { return NA_ABI_VERSION; }
+
+const char *na_last_error(void) { return g_error.c_str(); }
+
+int32_t na_window_start(int32_t index, int32_t length, int32_t kernel_size,
+                        int32_t neighborhood_size, int32_t dilation) {
+  return na::window_start(index, length, kernel_size, neighborhood_size,
+                          dilation);
+}
+
+int32_t na_window_end(int32_t start, int32_t length, int32_t kernel_size,
+                      int32_t dilation) {
+  return na::window_end(start, length, kernel_size, dilation);
+}
+
+int32_t na_pb_start(int32_t index, int32_t length, int32_t kernel_size,
+                    int32_t neighborhood_size, int32_t dilation) {
+  return na::pb_start(index, length, kernel_size, neighborhood_size, dilation);
+}
+
+int32_t na_window_start_partition(int32_t index, int32_t length,
+                                  int32_t kernel_size,
+                                  int32_t neighborhood_size,
+                                  int32_t dilation) {
+  return na::window_start_partition(index, length, kernel_size,
+                                    neighborhood_size, dilation);
+}
+
+int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
+                      void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, false);
+  if (rc != NA_OK) return rc;
+  if (P.dense) return fail(NA_ERR_INVALID, "neighbor table of a dense problem");
+  if (index == nullptr || valid == nullptr)
+    return fail(NA_ERR_INVALID, "index/valid must be non-NULL");
+  na::table(P, index, valid, as_stream(stream));
+  return launch_status("na_neighbor_table");
+}
+
+int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
+           const void *extra_k, const void *extra_v, void *out, float *lse,
+           void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, true);
+  if (rc != NA_OK) return rc;
+  if (P.B == 0) return NA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+    return fail(NA_ERR_INVALID, "q/k/v/out must be non-NULL");
+  if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
+    return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
+  na::valu_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
+               as_stream(stream));
+  return launch_status("na_fwd");
+}
+
+size_t na_bwd_workspace_bytes(const na_params *p) {
+  na::Prob P;
+  if (make_prob(p, &P, true) != NA_OK) return 0;
+  return delta_bytes(P);
+}
+
+int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
+           const void *extra_k, const void *extra_v, const void *out,
+           const float *lse, const void *dout, const float *dlse, void *dq,
+           void *dk, void *dv, void *d_extra_k, void *d_extra_v,
+           void *workspace, size_t workspace_bytes, void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, true);
+  if (rc != NA_OK) return rc;
+  if (P.B == 0) return NA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
+      lse == nullptr || dout == nullptr || dq == nullptr || dk == nullptr ||
+      dv == nullptr)
+    return fail(NA_ERR_INVALID,
+                "q/k/v/out/lse/dout/dq/dk/dv must be non-NULL");
+  if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
+    return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
+  if (workspace == nullptr || workspace_bytes < delta_bytes(P))
+    return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                delta_bytes(P), workspace == nullptr ? (size_t)0 : workspace_bytes);
+  float *delta = static_cast<float *>(workspace);
+  na::valu_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
+               dq, dk, dv, d_extra_k, d_extra_v, delta, as_stream(stream));
+  return launch_status("na_bwd");
+}
+
+int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,
+              void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, false);
+  if (rc != NA_OK) return rc;
+  if (P.dense) return fail(NA_ERR_INVALID, "split ops take no dense flag");
+  if (P.B == 0) return NA_OK;
+  if (q == nullptr || k == nullptr || logits == nullptr)
+    return fail(NA_ERR_INVALID, "q/k/logits must be non-NULL");
+  na::valu_qk(P, p->dtype, q, k, logits, as_stream(stream));
+  return launch_status("na_qk_fwd");
+}
+
+int na_av_fwd(const na_params *p, const void *attn, const void *v, void *out,
+              void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, false);
+  if (rc != NA_OK) return rc;
+  if (P.dense) return fail(NA_ERR_INVALID, "split ops take no dense flag");
+  if (P.B == 0) return NA_OK;
+  if (attn == nullptr || v == nullptr || out == nullptr)
+    return fail(NA_ERR_INVALID, "attn/v/out must be non-NULL");
+  na::valu_av(P, p->dtype, attn, v, out, as_stream(stream));
+  return launch_status("na_av_fwd");
+}
+
+int na_qk_bwd(const na_params *p, const void *q, const void *k,
+              const void *dlogits, void *dq, void *dk, void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, false);
+  if (rc != NA_OK) return rc;
+  if (P.dense) return fail(NA_ERR_INVALID, "split ops take no dense flag");
+  if (P.B == 0) return NA_OK;
+  if (q == nullptr || k == nullptr || dlogits == nullptr || dq == nullptr ||
+      dk == nullptr)
+    return fail(NA_ERR_INVALID, "q/k/dlogits/dq/dk must be non-NULL");
+  na::valu_qk_bwd(P, p->dtype, q, k, dlogits, dq, dk, as_stream(stream));
+  return launch_status("na_qk_bwd");
+}
+
+int na_av_bwd(const na_params *p, const void *attn, const void *v,
+              const void *dout, void *dattn, void *dv, void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, false);
+  if (rc != NA_OK) return rc;
+  if (P.dense) return fail(NA_ERR_INVALID, "split ops take no dense flag");
+  if (P.B == 0) return NA_OK;
+  if (attn == nullptr || v == nullptr || dout == nullptr || dattn == nullptr ||
+      dv == nullptr)
+    return fail(NA_ERR_INVALID, "attn/v/dout/dattn/dv must be non-NULL");
+  na::valu_av_bwd(P, p->dtype, attn, v, dout, dattn, dv, as_stream(stream));
+  return launch_status("na_av_bwd");
+}
+
+int na1d_qk_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
+                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
+                    float scale, int32_t has_scale, int32_t dtype,
+                    const void *q, const void *key, const float *rpb,
+                    float *logits, void *stream) {
+  if (batch < 0 || length < 1 || heads < 1 || head_dim < 1 ||
+      kernel_size < 1 || dilation < 1)
+    return fail(NA_ERR_INVALID, "invalid 1D QK+RPB shape");
+  if (head_dim > kMaxHeadDim || (head_dim % 8 != 0 && head_dim > 128))
+    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported", head_dim);
+  if (dtype != NA_F32 && dtype != NA_F16 && dtype != NA_BF16)
+    return fail(NA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (batch == 0) return NA_OK;
+  if (q == nullptr || key == nullptr || logits == nullptr)
+    return fail(NA_ERR_INVALID, "q/key/logits must be non-NULL");
+  na::valu_qk_rpb(batch, length, heads, head_dim, kernel_size, dilation, scale,
+                  has_scale, dtype, q, key, rpb, logits, as_stream(stream));
+  return launch_status("na1d_qk_rpb_fwd");
+}
+
+int na1d_av_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
+                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
+                    int32_t dtype, const float *attn, const void *value,
+                    float *out, void *stream) {
+  if (batch < 0 || length < 1 || heads < 1 || head_dim < 1 ||
+      kernel_size < 1 || dilation < 1)
+    return fail(NA_ERR_INVALID, "invalid 1D AV shape");
+  if (head_dim > kMaxHeadDim || (head_dim % 8 != 0 && head_dim > 128))
+    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported", head_dim);
+  if (dtype != NA_F32 && dtype != NA_F16 && dtype != NA_BF16)
+    return fail(NA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (batch == 0) return NA_OK;
+  if (attn == nullptr || value == nullptr || out == nullptr)
+    return fail(NA_ERR_INVALID, "attn/value/out must be non-NULL");
+  na::valu_av_rpb(batch, length, heads, head_dim, kernel_size, dilation,
+                  dtype, attn, value, out, as_stream(stream));
+  return launch_status("na1d_av_rpb_fwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,36 @@
+// na_launch.h — internal launchers behind the C ABI (not exported).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "na_common.h"
+
+namespace na {
+
+// Generic vector-ALU kernels (na_valu.hip): every dtype / head_dim.
+void valu_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st);
+void valu_bwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, const void *out,
+              const float *lse, const void *dout, const float *dlse, void *dq,
+              void *dk, void *dv, void *dek, void *dev, float *delta,
+              hipStream_t st);
+void valu_qk(const Prob &P, int dtype, const void *q, const void *k,
+             void *logits, hipStream_t st);
+void valu_av(const Prob &P, int dtype, const void *attn, const void *v,
+             void *out, hipStream_t st);
+void valu_qk_bwd(const Prob &P, int dtype, const void *q, const void *k,
+                 const void *dl, void *dq, void *dk, hipStream_t st);
+void valu_av_bwd(const Prob &P, int dtype, const void *attn, const void *v,
+                 const void *dout, void *dattn, void *dv, hipStream_t st);
+void valu_qk_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
+                 int32_t dil, float scale, int32_t has_scale, int dtype,
+                 const void *q, const void *key, const float *rpb,
+                 float *logits, hipStream_t st);
+void valu_av_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
+                 int32_t dil, int dtype, const float *attn, const void *v,
+                 float *out, hipStream_t st);
+void table(const Prob &P, int32_t *index, uint8_t *valid, hipStream_t st);
+
+}  // namespace na

@@ -1,0 +1,151 @@
+"""ctypes binding of libnatten_amd.so (the C ABI in include/natten_amd.h).
+
+The library is built in-tree by ``natten-mlx_amd/build_lib.py``.  It must be
+loaded after ``import torch`` so that it shares torch's HIP runtime (both
+link ``libamdhip64.so.7``) and therefore torch's streams and allocations.
+Nothing here falls back to another implementation: a missing library or a
+failing call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libnatten_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
+
+NA_F32, NA_F16, NA_BF16 = 0, 1, 2
+NA_FLAG_DENSE = 1
+ABI_VERSION = 1
+
+_STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "launch failure",
+           4: "workspace"}
+
+_I32x3 = ctypes.c_int32 * 3
+
+
+class NaParams(ctypes.Structure):
+    """Mirror of ``na_params`` (include/natten_amd.h)."""
+
+    _fields_ = [
+        ("rank", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("extent", _I32x3),
+        ("kernel", _I32x3),
+        ("dilation", _I32x3),
+        ("stride", _I32x3),
+        ("causal", _I32x3),
+        ("scale", ctypes.c_float),
+        ("n_extra", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("sample_extent", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.POINTER(NaParams)
+_V = ctypes.c_void_p
+_I = ctypes.c_int32
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "na_abi_version": (ctypes.c_int, []),
+    "na_last_error": (ctypes.c_char_p, []),
+    "na_window_start": (_I, [_I, _I, _I, _I, _I]),
+    "na_window_end": (_I, [_I, _I, _I, _I]),
+    "na_pb_start": (_I, [_I, _I, _I, _I, _I]),
+    "na_window_start_partition": (_I, [_I, _I, _I, _I, _I]),
+    "na_neighbor_table": (ctypes.c_int, [_P, _V, _V, _V]),
+    "na_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V, _V, _V]),
+    "na_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
+    "na_bwd": (ctypes.c_int, [_P] + [_V] * 15 + [ctypes.c_size_t, _V]),
+    "na_qk_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V]),
+    "na_av_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V]),
+    "na_qk_bwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V]),
+    "na_av_bwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V]),
+    "na1d_qk_rpb_fwd": (ctypes.c_int, [_I] * 6 + [ctypes.c_float, _I, _I, _V, _V, _V, _V, _V]),
+    "na1d_av_rpb_fwd": (ctypes.c_int, [_I] * 7 + [_V, _V, _V, _V]),
+}
+
+_lib = None
+_lock = threading.Lock()
+_load_error: str | None = None
+
+
+def load():
+    """Load (once) and return the library; raise if it is unavailable."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            _load_error = (f"{LIB_NAME} is not built (expected at {LIB_PATH}); "
+                           "run `python natten-mlx_amd/build_lib.py`")
+            raise RuntimeError(_load_error)
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.na_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_NAME} ABI {lib.na_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+    except Exception:
+        return False
+    return True
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().na_last_error().decode(errors="replace")
+        raise RuntimeError(f"natten_amd {what} failed ({_STATUS.get(rc, rc)}): {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return NA_F32
+    if dt == torch.float16:
+        return NA_F16
+    if dt == torch.bfloat16:
+        return NA_BF16
+    raise TypeError(f"natten_amd supports float32/float16/bfloat16 tensors, got {dt}")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def make_params(rank: int, batch: int, heads: int, kv_heads: int, head_dim: int, dtype: int,
+                extent, kernel, dilation, stride, causal, scale: float, n_extra: int = 0,
+                flags: int = 0, sample_extent: torch.Tensor | None = None) -> NaParams:
+    p = NaParams()
+    p.rank, p.batch, p.heads, p.kv_heads, p.head_dim, p.dtype = (
+        rank, batch, heads, kv_heads, head_dim, dtype)
+    for arr, vals in ((p.extent, extent), (p.kernel, kernel), (p.dilation, dilation),
+                      (p.stride, stride), (p.causal, causal)):
+        for i in range(3):
+            arr[i] = int(vals[i]) if i < len(vals) else 1
+    p.scale = float(scale)
+    p.n_extra = int(n_extra)
+    p.flags = int(flags)
+    p.sample_extent = None if sample_extent is None else sample_extent.data_ptr()
+    return p

@@ -1,0 +1,311 @@
+"""The ``hip`` backend: natten-mlx's backend-module interface on PyTorch-ROCm
+tensors, executed by libnatten_amd.so.
+
+It exposes the eighteen entry points every reference backend module has
+(``src/natten_mlx/_core/ops.py:49-135``: ``na{1,2,3}d_forward``,
+``na{1,2,3}d_backward``, ``na{1,2,3}d_{qk,av}_{forward,backward}``) with the
+same argument order and meaning (normalised tuples; ``scale`` may be None),
+plus the hooks the autograd layer calls directly (reference
+``autograd/na2d.py:34-53`` calls ``fast_metal.na2d_fused_simd_backward``
+with the forward output; ``autograd/na1d.py:76-80`` calls the varlen
+forward).  Tensors must live on a HIP device; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+
+def is_available() -> bool:
+    return torch.cuda.is_available() and _lib.available()
+
+
+def _require_device(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "natten_amd's hip backend runs on MI355X (HIP) tensors only; got a tensor on "
+                f"{t.device}. There is no CPU implementation.")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors are on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _c(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.contiguous()
+
+
+def _scale(scale, head_dim: int) -> float:
+    return head_dim ** -0.5 if scale is None else float(scale)
+
+
+def _params(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_causal, scale,
+            n_extra: int = 0, dense: bool = False,
+            sample_extent: Optional[torch.Tensor] = None) -> _lib.NaParams:
+    rank = q.dim() - 3
+    return _lib.make_params(
+        rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
+        tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
+        tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra,
+        _lib.NA_FLAG_DENSE if dense else 0, sample_extent)
+
+
+def _out_spatial(spatial: Sequence[int], stride: Sequence[int]) -> tuple[int, ...]:
+    return tuple((s + st - 1) // st for s, st in zip(spatial, stride))
+
+
+# ---------------------------------------------------------------------------
+# fused op (with LSE, additional tokens, varlen and the dense FMHA mode)
+
+def fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale,
+                  extra_k=None, extra_v=None, sample_extent=None, dense=False,
+                  want_lse=True):
+    """Returns ``(out, lse)``; lse is float32 ``[B, *O, H]`` (or None)."""
+    _require_device(q, k, v, extra_k, extra_v, sample_extent)
+    q, k, v, extra_k, extra_v = map(_c, (q, k, v, extra_k, extra_v))
+    lib = _lib.load()
+    n_extra = 0 if extra_k is None else extra_k.shape[1]
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                sample_extent)
+    osp = _out_spatial(q.shape[1:-2], stride)
+    B, H, D = q.shape[0], q.shape[-2], q.shape[-1]
+    out = torch.empty((B, *osp, H, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, *osp, H), dtype=torch.float32, device=q.device) if want_lse else None
+    _lib.check(lib.na_fwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(extra_k),
+                          _lib.ptr(extra_v), _lib.ptr(out), _lib.ptr(lse), _lib.stream_of(q)),
+               "na_fwd")
+    return out, lse
+
+
+def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, dilation,
+                   is_causal, scale, extra_k=None, extra_v=None, sample_extent=None,
+                   dense=False):
+    """Returns ``(dq, dk, dv, d_extra_k, d_extra_v)``."""
+    _require_device(q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v)
+    q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v = map(
+        _c, (q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v))
+    if grad_out.dtype != q.dtype:
+        grad_out = grad_out.to(q.dtype)
+    if grad_lse is not None and grad_lse.dtype != torch.float32:
+        grad_lse = grad_lse.float()
+    lib = _lib.load()
+    n_extra = 0 if extra_k is None else extra_k.shape[1]
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                sample_extent)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dek = torch.empty_like(extra_k) if n_extra else None
+    dev = torch.empty_like(extra_v) if n_extra else None
+    ws_bytes = int(lib.na_bwd_workspace_bytes(p))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.na_bwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(extra_k),
+                          _lib.ptr(extra_v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(grad_out),
+                          _lib.ptr(grad_lse), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+                          _lib.ptr(dek), _lib.ptr(dev), _lib.ptr(ws), ws_bytes,
+                          _lib.stream_of(q)), "na_bwd")
+    return dq, dk, dv, dek, dev
+
+
+# ---------------------------------------------------------------------------
+# split ops
+
+def qk_forward(q, k, kernel_size, stride, dilation, is_causal, scale):
+    _require_device(q, k)
+    q, k = _c(q), _c(k)
+    if k.dtype != q.dtype:
+        k = k.to(q.dtype)
+    lib = _lib.load()
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale)
+    osp = _out_spatial(q.shape[1:-2], stride)
+    kprod = 1
+    for x in kernel_size:
+        kprod *= int(x)
+    logits = torch.empty((q.shape[0], *osp, q.shape[-2], kprod), dtype=q.dtype, device=q.device)
+    _lib.check(lib.na_qk_fwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(logits), _lib.stream_of(q)),
+               "na_qk_fwd")
+    return logits
+
+
+def _av_params(attn, v, kernel_size, stride, dilation, is_causal):
+    rank = v.dim() - 3
+    return _lib.make_params(
+        rank, v.shape[0], attn.shape[-2], v.shape[-2], v.shape[-1], _lib.dtype_code(v.dtype),
+        tuple(v.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
+        tuple(int(bool(c)) for c in is_causal), 1.0)
+
+
+def _check_attn_shape(attn, v, kernel_size, stride):
+    osp = _out_spatial(v.shape[1:-2], stride)
+    kprod = 1
+    for x in kernel_size:
+        kprod *= int(x)
+    if tuple(attn.shape[1:-2]) != osp or attn.shape[-1] != kprod or attn.shape[0] != v.shape[0]:
+        raise ValueError(
+            f"attn shape {tuple(attn.shape)} must be [B, *ceil(input/stride), heads, {kprod}] "
+            f"for value shape {tuple(v.shape)}")
+
+
+def av_forward(attn, v, kernel_size, stride, dilation, is_causal):
+    _require_device(attn, v)
+    _check_attn_shape(attn, v, kernel_size, stride)
+    dt = torch.promote_types(attn.dtype, v.dtype)
+    attn, v = _c(attn.to(dt)), _c(v.to(dt))
+    lib = _lib.load()
+    p = _av_params(attn, v, kernel_size, stride, dilation, is_causal)
+    out = torch.empty((*attn.shape[:-1], v.shape[-1]), dtype=dt, device=v.device)
+    _lib.check(lib.na_av_fwd(p, _lib.ptr(attn), _lib.ptr(v), _lib.ptr(out), _lib.stream_of(v)),
+               "na_av_fwd")
+    return out
+
+
+def qk_backward(q, k, grad_attn, kernel_size, stride, dilation, is_causal, scale):
+    _require_device(q, k, grad_attn)
+    q, k = _c(q), _c(k)
+    kd = k.dtype
+    if k.dtype != q.dtype:
+        k = k.to(q.dtype)
+    g = _c(grad_attn.to(q.dtype))
+    lib = _lib.load()
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    _lib.check(lib.na_qk_bwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(g), _lib.ptr(dq),
+                             _lib.ptr(dk), _lib.stream_of(q)), "na_qk_bwd")
+    return dq, dk.to(kd)
+
+
+def av_backward(attn, v, grad_out, kernel_size, stride, dilation, is_causal):
+    _require_device(attn, v, grad_out)
+    dt = torch.promote_types(attn.dtype, v.dtype)
+    ad, vd = attn.dtype, v.dtype
+    attn, v = _c(attn.to(dt)), _c(v.to(dt))
+    g = _c(grad_out.to(dt))
+    lib = _lib.load()
+    p = _av_params(attn, v, kernel_size, stride, dilation, is_causal)
+    dattn = torch.empty_like(attn)
+    dv = torch.empty_like(v)
+    _lib.check(lib.na_av_bwd(p, _lib.ptr(attn), _lib.ptr(v), _lib.ptr(g), _lib.ptr(dattn),
+                             _lib.ptr(dv), _lib.stream_of(v)), "na_av_bwd")
+    return dattn.to(ad), dv.to(vd)
+
+
+# ---------------------------------------------------------------------------
+# the reference backend-module interface (ops.py:49-135)
+
+def na1d_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    return fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale,
+                         want_lse=False)[0]
+
+
+na2d_forward = na1d_forward
+na3d_forward = na1d_forward
+
+
+def na1d_backward(q, k, v, grad_out, kernel_size, stride, dilation, is_causal, scale):
+    out, lse = fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale)
+    dq, dk, dv, _, _ = fused_backward(q, k, v, out, lse, grad_out, None, kernel_size, stride,
+                                      dilation, is_causal, scale)
+    return dq, dk, dv
+
+
+na2d_backward = na1d_backward
+na3d_backward = na1d_backward
+
+
+def na1d_qk_forward(q, k, kernel_size, stride, dilation, is_causal, scale):
+    return qk_forward(q, k, kernel_size, stride, dilation, is_causal, scale)
+
+
+na2d_qk_forward = na1d_qk_forward
+na3d_qk_forward = na1d_qk_forward
+
+
+def na1d_av_forward(attn, v, kernel_size, stride, dilation, is_causal):
+    return av_forward(attn, v, kernel_size, stride, dilation, is_causal)
+
+
+na2d_av_forward = na1d_av_forward
+na3d_av_forward = na1d_av_forward
+
+
+def na1d_qk_backward(q, k, grad_attn, kernel_size, stride, dilation, is_causal, scale):
+    return qk_backward(q, k, grad_attn, kernel_size, stride, dilation, is_causal, scale)
+
+
+na2d_qk_backward = na1d_qk_backward
+na3d_qk_backward = na1d_qk_backward
+
+
+def na1d_av_backward(attn, v, grad_out, kernel_size, stride, dilation, is_causal):
+    return av_backward(attn, v, grad_out, kernel_size, stride, dilation, is_causal)
+
+
+na2d_av_backward = na1d_av_backward
+na3d_av_backward = na1d_av_backward
+
+
+def na1d_fused_backward(q, k, v, grad_out, out, lse, kernel_size, stride, dilation, is_causal,
+                        scale, grad_lse=None):
+    """Backward from a saved forward (the role of the reference's
+    ``fast_metal.na{n}d_fused_simd_backward(q, k, v, dO, out, ...)``)."""
+    dq, dk, dv, _, _ = fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride,
+                                      dilation, is_causal, scale)
+    return dq, dk, dv
+
+
+na2d_fused_backward = na1d_fused_backward
+na3d_fused_backward = na1d_fused_backward
+
+
+def varlen_forward(q, k, v, sample_extent, kernel_size, dilation, scale):
+    """Varlen fused forward (reference ``fast_metal.na1d_varlen_forward``)."""
+    rank = q.dim() - 3
+    return fused_forward(q, k, v, kernel_size, (1,) * rank, dilation, (False,) * rank, scale,
+                         sample_extent=sample_extent)
+
+
+# ---------------------------------------------------------------------------
+# DiNAT allin1 1D
+
+def qk_rpb_1d(q, k, rpb, kernel_size, dilation, scale):
+    _require_device(q, k, rpb)
+    q, k = _c(q), _c(k)
+    if k.dtype != q.dtype:
+        k = k.to(q.dtype)
+    B, L, H, D = q.shape
+    rp = None if rpb is None else _c(rpb.to(torch.float32))
+    if rp is not None and tuple(rp.shape) != (H, 2 * kernel_size - 1):
+        raise ValueError(f"rpb must have shape [{H}, {2 * kernel_size - 1}], got {tuple(rp.shape)}")
+    out = torch.empty((B, L, H, kernel_size), dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    _lib.check(lib.na1d_qk_rpb_fwd(B, L, H, D, kernel_size, dilation,
+                                   1.0 if scale is None else float(scale),
+                                   0 if scale is None else 1, _lib.dtype_code(q.dtype),
+                                   _lib.ptr(q), _lib.ptr(k), _lib.ptr(rp), _lib.ptr(out),
+                                   _lib.stream_of(q)), "na1d_qk_rpb_fwd")
+    return out
+
+
+def av_rpb_1d(attn, v, kernel_size, dilation):
+    _require_device(attn, v)
+    a = _c(attn.to(torch.float32))
+    v = _c(v)
+    B, L, H, D = v.shape
+    if tuple(a.shape) != (B, L, H, kernel_size):
+        raise ValueError(f"attn must have shape {(B, L, H, kernel_size)}, got {tuple(a.shape)}")
+    out = torch.empty((B, L, H, D), dtype=torch.float32, device=v.device)
+    lib = _lib.load()
+    _lib.check(lib.na1d_av_rpb_fwd(B, L, H, D, kernel_size, dilation, _lib.dtype_code(v.dtype),
+                                   _lib.ptr(a), _lib.ptr(v), _lib.ptr(out), _lib.stream_of(v)),
+               "na1d_av_rpb_fwd")
+    return out

@@ -1,0 +1,98 @@
+"""Autograd for the fused op (reference ``autograd/na{1,2,3}d.py``).
+
+One Function covers every rank, GQA, additional tokens, varlen and the
+dense (FMHA) mode.  Its forward returns ``(out, lse)``; the backward takes
+gradients for both (the LSE gradient enters as ``delta - dlse``), so a loss
+that uses the returned LSE differentiates correctly
+(reference ``tests/test_new_features.py:1177-1192``).
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple, Optional
+
+import torch
+
+from .._core import ops
+
+
+class FusedSpec(NamedTuple):
+    kernel_size: tuple
+    stride: tuple
+    dilation: tuple
+    is_causal: tuple
+    scale: Optional[float]
+    dense: bool = False
+
+
+class _FusedNA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, extra_k, extra_v, sample_extent, spec: FusedSpec):
+        be = ops.backend_module()
+        out, lse = be.fused_forward(q, k, v, spec.kernel_size, spec.stride, spec.dilation,
+                                    spec.is_causal, spec.scale, extra_k, extra_v,
+                                    sample_extent, spec.dense)
+        ctx.save_for_backward(q, k, v, extra_k, extra_v, out, lse, sample_extent)
+        ctx.spec = spec
+        ctx.set_materialize_grads(False)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_lse):
+        q, k, v, extra_k, extra_v, out, lse, sample_extent = ctx.saved_tensors
+        spec = ctx.spec
+        if grad_out is None:
+            grad_out = torch.zeros_like(out)
+        be = ops.backend_module()
+        dq, dk, dv, dek, dev = be.fused_backward(
+            q, k, v, out, lse, grad_out, grad_lse, spec.kernel_size, spec.stride, spec.dilation,
+            spec.is_causal, spec.scale, extra_k, extra_v, sample_extent, spec.dense)
+        return dq, dk, dv, dek, dev, None, None
+
+
+def na_fused_with_grad(q, k, v, spec: FusedSpec, extra_k=None, extra_v=None,
+                       sample_extent=None):
+    """Differentiable fused op; returns ``(out, lse_float32)``."""
+    return _FusedNA.apply(q, k, v, extra_k, extra_v, sample_extent, spec)
+
+
+def _plain(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    spec = FusedSpec(tuple(kernel_size), tuple(stride), tuple(dilation),
+                     tuple(bool(c) for c in is_causal), scale)
+    return na_fused_with_grad(q, k, v, spec)[0]
+
+
+def na1d_with_grad(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    """Autograd-capable 1D NA (reference ``autograd/na1d.py:56-63``)."""
+    return _plain(q, k, v, kernel_size, stride, dilation, is_causal, scale)
+
+
+def na2d_with_grad(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    """Autograd-capable 2D NA (reference ``autograd/na2d.py:59-64``)."""
+    return _plain(q, k, v, kernel_size, stride, dilation, is_causal, scale)
+
+
+def na3d_with_grad(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    """Autograd-capable 3D NA (reference ``autograd/na3d.py``)."""
+    return _plain(q, k, v, kernel_size, stride, dilation, is_causal, scale)
+
+
+def _varlen(q, k, v, sizes, kernel_size, dilation, scale):
+    rank = q.dim() - 3
+    se = sizes.to(device=q.device, dtype=torch.int32).reshape(q.shape[0], rank).contiguous()
+    spec = FusedSpec(tuple(kernel_size), (1,) * rank, tuple(dilation), (False,) * rank, scale)
+    return na_fused_with_grad(q, k, v, spec, sample_extent=se)[0]
+
+
+def na1d_varlen_with_grad(q, k, v, seq_lens, kernel_size, dilation, scale):
+    """Reference ``autograd/na1d.py:73-103``; the backward is the same
+    fused HIP backward (the reference runs pure per-sample autodiff)."""
+    return _varlen(q, k, v, seq_lens, kernel_size, dilation, scale)
+
+
+def na2d_varlen_with_grad(q, k, v, spatial_sizes, kernel_size, dilation, scale):
+    return _varlen(q, k, v, spatial_sizes, kernel_size, dilation, scale)
+
+
+def na3d_varlen_with_grad(q, k, v, spatial_sizes, kernel_size, dilation, scale):
+    return _varlen(q, k, v, spatial_sizes, kernel_size, dilation, scale)

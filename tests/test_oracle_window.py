@@ -1,0 +1,99 @@
+"""Pins the oracle's window arithmetic (oracle/window.py) to the reference's
+known answers and to properties the definition fixes independently."""
+
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import brute
+from oracle import window as W
+
+
+def test_reference_kats():
+    # reference tests/test_shift_semantics.py:53-64
+    assert W.window_start(31, 32, 3, 1, 1) == 29
+    assert W.pb_start(31, 32, 3, 1, 1) == 0
+
+
+def test_phase_bounds_and_pb_range():
+    # reference tests/test_shift_semantics.py:11-50 (L=64, K=7, d=4)
+    L, K, d = 64, 7, 4
+    for i in range(L):
+        s = W.window_start(i, L, K, K // 2, d)
+        e = W.window_end(s, L, K, d)
+        assert 0 <= s < L and 0 < e <= L
+        for k in range(K):
+            if s + k * d < e:
+                assert (s + k * d) % d == i % d
+        pb = W.pb_start(i, L, K, K // 2, d)
+        assert all(0 <= pb + k <= 2 * K - 2 for k in range(K))
+
+
+def _domain(max_len=60):
+    for L in range(1, max_len):
+        for K in range(1, L + 1, 2):
+            for d in range(1, L // K + 1):
+                yield L, K, d
+
+
+def test_dilation1_closed_form():
+    # d = 1, odd K: the window is the K-run centred on i, clamped into [0, L)
+    for L in range(1, 80):
+        for K in range(1, L + 1, 2):
+            for i in range(L):
+                assert W.window_start(i, L, K, K // 2, 1) == min(max(i - K // 2, 0), L - K)
+
+
+def test_legacy_equals_partition_form():
+    for L, K, d in _domain(70):
+        for i in range(L):
+            assert W.window_start(i, L, K, K // 2, d) == W.window_start_partition(i, L, K, K // 2, d)
+
+
+def test_pb_start_is_relative_offset():
+    # bias row of slot k == (key - query) / d + K - 1
+    for L, K, d in _domain(50):
+        for i in range(L):
+            s = W.window_start(i, L, K, K // 2, d)
+            pb = W.pb_start(i, L, K, K // 2, d)
+            for k in range(K):
+                key = s + k * d
+                assert (key - i) % d == 0
+                assert pb + k == (key - i) // d + K - 1
+
+
+def test_noncausal_full_window():
+    # with d*K <= L every slot of a non-causal window is a valid key
+    for L, K, d in _domain(50):
+        idx, valid = W.axis_indices(np.arange(L), L, K, d, False)
+        assert valid.all()
+        assert (idx == W.axis_indices(np.arange(L), L, K, d, False)[0]).all()
+
+
+def test_causal_axis():
+    L, K, d = 20, 4, 3
+    idx, valid = W.axis_indices(np.arange(L), L, K, d, True)
+    # the last slot is the query itself; the first query sees only itself
+    assert (idx[:, -1] == np.arange(L)).all() and valid[:, -1].all()
+    assert valid[0].sum() == 1
+    for i in range(L):
+        assert valid[i].sum() == min(K, i // d + 1)
+
+
+@pytest.mark.parametrize("spatial,ks,dil,caus,st", [
+    ((9,), (3,), (2,), (False,), (1,)),
+    ((7, 6), (3, 2), (2, 1), (True, False), (2, 1)),
+    ((4, 5, 6), (3, 3, 2), (1, 1, 2), (False, True, False), (1, 2, 3)),
+])
+def test_neighbor_table_matches_axis_loops(spatial, ks, dil, caus, st):
+    lin, valid = W.neighbor_table(spatial, ks, dil, caus, st)
+    outs = [range((s + t - 1) // t) for s, t in zip(spatial, st)]
+    for o in itertools.product(*outs):
+        axes = [brute.axis_keys(o[a] * st[a], spatial[a], ks[a], dil[a], caus[a])
+                for a in range(len(spatial))]
+        for n, combo in enumerate(itertools.product(*axes)):
+            ok = all(c is not None for c in combo)
+            assert valid[o][n] == ok
+            if ok:
+                assert lin[o][n] == np.ravel_multi_index(combo, spatial)
