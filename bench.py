@@ -114,25 +114,57 @@ def run_gpu(args):
                 print(f"[bench] graph capture unavailable: {exc}", file=sys.stderr, flush=True)
                 graph_ms, graph_ok = None, None
 
-        # per-call kernel durations with HIP events on torch's current stream
+        # per-call kernel durations: HIP events around `reps` back-to-back
+        # calls of one library entry point on torch's current stream (the
+        # stream the library launches on), replayed from a HIP graph so host
+        # overhead does not leave the GPU idle between launches
         qd, kd, vd = q.detach(), k.detach(), v.detach()
         ks, st, dl, ca = (K, K), (1, 1), (dil, dil), (False, False)
         out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
-        n = max(args.steps, 20)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        fwd_t, bwd_t = 0.0, 0.0
-        for _ in range(n):
-            ev[0].record()
-            hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
-            ev[1].record()
-            hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca, None)
-            ev[2].record()
-            torch.cuda.synchronize()
-            fwd_t += ev[0].elapsed_time(ev[1])
-            bwd_t += ev[1].elapsed_time(ev[2])
+        fwd_ms = time_calls(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None),
+                            args.steps)
+        bwd_ms = time_calls(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st,
+                                                       dl, ca, None), args.steps)
         results[dil] = dict(eager_ms=eager_ms, graph_ms=graph_ms, graph_ok=graph_ok,
-                            fwd_ms=fwd_t / n, bwd_ms=bwd_t / n)
+                            fwd_ms=fwd_ms, bwd_ms=bwd_ms)
     return results
+
+
+def time_calls(fn, steps: int, reps: int = 20) -> float:
+    """Average device time (ms) of one call of ``fn``: events bracket a
+    graph replay of ``reps`` back-to-back calls (eager loop if capture
+    fails), repeated ``steps`` times."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph = None
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+    except Exception as exc:
+        print(f"[bench] call-timing capture unavailable: {exc}", file=sys.stderr, flush=True)
+        graph = None
+    total = 0.0
+    n = max(steps // 4, 5)
+    for _ in range(n):
+        start.record()
+        if graph is not None:
+            graph.replay()
+        else:
+            for _ in range(reps):
+                fn()
+        end.record()
+        torch.cuda.synchronize()
+        total += start.elapsed_time(end)
+    return total / (n * reps)
 
 
 def run_cpu_baseline():
@@ -153,14 +185,14 @@ def run_cpu_baseline():
 
     once()  # warmup
     times = []
-    deadline = time.perf_counter() + 20.0
-    while len(times) < 5 and (not times or time.perf_counter() < deadline):
+    deadline = time.perf_counter() + 12.0
+    while len(times) < 3 or (len(times) < 40 and time.perf_counter() < deadline):
         t0 = time.perf_counter()
         once()
         times.append(time.perf_counter() - t0)
     times.sort()
     per_sample_s = times[len(times) // 2]
-    return per_sample_s * B, threads  # scaled to the full B=4 step
+    return per_sample_s * B, threads, len(times)  # scaled to the full B=4 step
 
 
 def main(argv=None):
@@ -200,11 +232,11 @@ def main(argv=None):
 
     cpu = None
     if not args.no_cpu:
-        cpu_s, threads = run_cpu_baseline()
+        cpu_s, threads, runs = run_cpu_baseline()
         cpu = {"value": round(total_flops / cpu_s / 1e12, 6), "unit": "TFLOP/s",
                "cores": threads, "kind": "port",
-               "sample": "oracle (pure-backend restatement) fwd+bwd in bf16 on 1 of the 4 "
-                         "images, median of <=5 runs, scaled x4 to the full step",
+               "sample": f"oracle (pure-backend restatement) fwd+bwd in bf16 on 1 of the 4 "
+                         f"images, median of {runs} runs (~12 s), scaled x4 to the full step",
                "ms_per_step": round(cpu_s * 1e3, 2)}
 
     line = {

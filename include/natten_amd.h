@@ -48,7 +48,10 @@ enum na_status {
 enum na_flags {
   /* Every query attends to every key of its sample (the FMHA fast path of
    * functional.py:141-187, taken when the kernel covers the extent). */
-  NA_FLAG_DENSE = 1
+  NA_FLAG_DENSE = 1,
+  /* Run the generic vector-ALU kernels even where the matrix-core kernels
+   * apply (for A/B comparison of the two implementations). */
+  NA_FLAG_GENERIC = 2
 };
 
 /*
@@ -104,6 +107,16 @@ int32_t na_window_start_partition(int32_t index, int32_t length,
  */
 int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
                       void *stream);
+
+/*
+ * Diagnostic with no counterpart in the reference: multiplies two fixed
+ * small-integer matrices (A 32x16, B 16x32) with one matrix-core
+ * instruction in `dtype` (NA_BF16 / NA_F16) using the operand and result
+ * lane layouts the kernels assume, and writes C = A.B as float32 [32][32]
+ * row-major into `out` (device).  A[m][k] = (m + 2k) % 7 - 3,
+ * B[k][n] = (3k + n) % 5 - 2.
+ */
+int na_mfma_selftest(int32_t dtype, float *out, void *stream);
 
 /* ---- fused neighborhood attention --------------------------------------- */
 /*

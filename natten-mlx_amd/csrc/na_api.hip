@@ -99,6 +99,10 @@ int make_prob(const na_params *p, na::Prob *P, bool allow_varlen) {
       if (dense && (x.s != 1 || x.causal))
         return fail(NA_ERR_INVALID,
                     "dense attention requires stride 1 and no causal mask");
+      if (dense) {  // every key of the sample: no window, no dilation phases
+        x.K = x.L;
+        x.d = 1;
+      }
     }
     x.O = (x.L + x.s - 1) / x.s;
     P->kprod *= x.K;
@@ -107,6 +111,10 @@ int make_prob(const na_params *p, na::Prob *P, bool allow_varlen) {
 }
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool use_mfma(const na_params *p, const na::Prob &P) {
+  return (p->flags & NA_FLAG_GENERIC) == 0 && na::mfma_eligible(P, p->dtype);
+}
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -147,6 +155,14 @@ int32_t na_window_start_partition(int32_t index, int32_t length,
                                     neighborhood_size, dilation);
 }
 
+int na_mfma_selftest(int32_t dtype, float *out, void *stream) {
+  if (dtype != NA_BF16 && dtype != NA_F16)
+    return fail(NA_ERR_INVALID, "selftest dtype must be bf16 or fp16");
+  if (out == nullptr) return fail(NA_ERR_INVALID, "out must be non-NULL");
+  na::mfma_selftest(dtype, out, as_stream(stream));
+  return launch_status("na_mfma_selftest");
+}
+
 int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
                       void *stream) {
   na::Prob P;
@@ -170,8 +186,12 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
     return fail(NA_ERR_INVALID, "q/k/v/out must be non-NULL");
   if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
     return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
-  na::valu_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
-               as_stream(stream));
+  if (use_mfma(p, P))
+    na::mfma_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
+                 as_stream(stream));
+  else
+    na::valu_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
+                 as_stream(stream));
   return launch_status("na_fwd");
 }
 
@@ -201,8 +221,19 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
     return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
                 delta_bytes(P), workspace == nullptr ? (size_t)0 : workspace_bytes);
   float *delta = static_cast<float *>(workspace);
-  na::valu_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
-               dq, dk, dv, d_extra_k, d_extra_v, delta, as_stream(stream));
+  const hipStream_t st = as_stream(stream);
+  if (use_mfma(p, P)) {
+    na::mfma_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
+                 dq, dk, dv, st);
+    if (P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr) {
+      na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+      na::valu_dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout,
+                      d_extra_k, d_extra_v, st);
+    }
+  } else {
+    na::valu_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
+                 dq, dk, dv, d_extra_k, d_extra_v, delta, st);
+  }
   return launch_status("na_bwd");
 }
 

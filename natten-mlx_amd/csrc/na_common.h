@@ -134,6 +134,14 @@ struct Prob {
   const int32_t *sample_extent;  // [B, rank] or nullptr
 };
 
+// Tiling of the MFMA kernels: 32-query (or 32-key) tiles of T0 x T1 x T2
+// sub-grid points (powers of two), nt[a] tiles per dilation phase.
+struct Tiling {
+  int32_t T[3], lgT[3], nt[3];
+  int32_t n_q, n_k;   // query tiles, key tiles
+  int32_t n_launch;   // workgroups launched (multiple of 8)
+};
+
 // Extents of sample b (varlen aware).
 __device__ __forceinline__ void sample_extents(const Prob &P, int32_t b,
                                                int32_t L[3], int32_t O[3]) {

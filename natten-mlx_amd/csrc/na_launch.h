@@ -33,4 +33,23 @@ void valu_av_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
                  float *out, hipStream_t st);
 void table(const Prob &P, int32_t *index, uint8_t *valid, hipStream_t st);
 
+// Matrix-core kernels (na_mfma.hip): bf16/fp16, head_dim 32/64/128,
+// stride 1, odd kernel size on every non-causal axis.
+bool mfma_eligible(const Prob &P, int dtype);
+void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st);
+void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, const void *out,
+              const float *lse, const void *dout, const float *dlse, void *dq,
+              void *dk, void *dv, hipStream_t st);
+void mfma_selftest(int dtype, float *out, hipStream_t st);
+
+// Generic pieces reused around the MFMA backward.
+void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
+                const float *dlse, float *delta, hipStream_t st);
+void valu_dextra(const Prob &P, int dtype, const void *q, const void *ek,
+                 const void *ev, const float *lse, const float *delta,
+                 const void *dout, void *dek, void *dev, hipStream_t st);
+
 }  // namespace na

@@ -1,0 +1,881 @@
+// na_mfma.hip — matrix-core (gfx950 MFMA) kernels for the fused op.
+//
+// Tiling.  With dilation d an axis splits into d independent phases
+// (positions r, r+d, r+2d, ...), each an undilated neighborhood problem on
+// its "sub-grid".  A wave owns a tile of 32 queries: a T0 x T1 x T2 box
+// (powers of two) of one phase.  The union of their windows is again a box
+// on the same sub-grid, enumerated row-major with the innermost extent
+// padded to a power of two P2 >= 8, so the coordinates of a chunk of 32
+// keys follow from shifts and wave-uniform divisions.
+//
+// Forward, per chunk of 32 keys (mfma_f32_32x32x16, fp32 accumulate):
+//   S^T[key][q] = K_chunk . Q^T          (A = K rows, B = Q rows: global)
+//   online softmax per query column: a lane owns 16 scores of one query,
+//   the other 16 sit in lane ^ 32, so one cross-lane max per chunk
+//   O^T[d][q] += V^T[d][key] . P^T        (A = V^T from LDS, B = P regs)
+// The 16 scores a lane holds (keys 8i + 4h + j) feed the next MFMA's B
+// operand directly when its k index is permuted the same way on the A side.
+//
+// Backward is one launch with two roles, deterministic and atomic-free:
+//   dQ tiles   (as forward)  dS^T = P^T (dP^T - delta),  dQ^T += K^T . dS^T
+//   dK/dV tiles (32 keys)    over the queries whose windows contain them
+//                            (inverse neighborhood, a box per axis):
+//                            dV^T += dO^T . P,  dK^T += Q^T . dS
+// delta = rowsum(dO * O) - dlse is recomputed per query from O and dO.
+#include <cmath>
+
+#include "na_common.h"
+#include "na_launch.h"
+
+namespace na {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mf;
+template <>
+struct Mf<bf16_t> {
+  typedef __bf16 e;
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mf<f16_t> {
+  typedef _Float16 e;
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename Mf<T>::v8 ld8(const T *p) {
+  return *reinterpret_cast<const typename Mf<T>::v8 *>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mf<T>::v8 zero8() {
+  typename Mf<T>::v8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (typename Mf<T>::e)0.f;
+  return z;
+}
+
+// B operand from 8 fp32 scores (the lane's keys 8i+4h+j for i = 2b, 2b+1).
+template <typename T>
+__device__ __forceinline__ typename Mf<T>::v8 pack8(const float *x) {
+  typename Mf<T>::v8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (typename Mf<T>::e)x[i];
+  return r;
+}
+
+// A operand from an LDS row of a transposed chunk: elements 4h..4h+3 and
+// 8+4h..8+4h+3 of the 16-wide k-block starting at `row`.
+template <typename T>
+__device__ __forceinline__ typename Mf<T>::v8 lds_a(const typename Mf<T>::e *row,
+                                                  int h) {
+  typedef typename Mf<T>::v4 v4;
+  const v4 lo = *reinterpret_cast<const v4 *>(row + 4 * h);
+  const v4 hi = *reinterpret_cast<const v4 *>(row + 8 + 4 * h);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+constexpr int kRow = 36;  // LDS row stride (elements) of a transposed chunk
+
+__device__ __forceinline__ int xcd_tile(int bid, int n_launch) {
+  // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a
+  // contiguous range of tiles so neighbouring tiles share its L2.
+  return (bid & 7) * (n_launch >> 3) + (bid >> 3);
+}
+
+__device__ __forceinline__ int ceil_log2(int x) {
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+// Window of sub-grid query i (phase r) on axis a, as sub-grid [lo, hi).
+__device__ __forceinline__ void sub_window(const Prob &P, int a, int L, int r,
+                                           int i, int &lo, int &hi) {
+  const Axis &x = P.ax[a];
+  if (P.dense) {
+    lo = 0;
+    hi = L;
+    return;
+  }
+  const AxisWin w = axis_window(r + x.d * i, L, x.K, x.d, x.causal);
+  lo = (w.lo - r) / x.d;
+  hi = (w.hi - r + x.d - 1) / x.d;
+}
+
+// Sub-grid queries [qlo, qhi] whose windows contain sub-grid key j.
+__device__ __forceinline__ void sub_inverse(const Prob &P, int a, int L, int r,
+                                            int Lr, int j, int &qlo,
+                                            int &qhi) {
+  const Axis &x = P.ax[a];
+  if (P.dense) {
+    qlo = 0;
+    qhi = Lr - 1;
+    return;
+  }
+  if (x.causal) {
+    qlo = j;
+    qhi = min(j + x.K - 1, Lr - 1);
+    return;
+  }
+  if (x.d * x.K <= L) {  // clamped windows: start = clamp(i - K/2, 0, Lr - K)
+    const int nh = x.K / 2;
+    qlo = j <= x.K - 1 ? 0 : j - nh;
+    qhi = j >= Lr - x.K ? Lr - 1 : j + nh;
+    return;
+  }
+  // general odd K: window bounds are non-decreasing in i
+  int a0 = 0, b0 = Lr, lo, hi;
+  while (a0 < b0) {
+    const int mid = (a0 + b0) >> 1;
+    sub_window(P, a, L, r, mid, lo, hi);
+    if (hi > j) b0 = mid; else a0 = mid + 1;
+  }
+  qlo = a0;
+  a0 = 0;
+  b0 = Lr;
+  while (a0 < b0) {
+    const int mid = (a0 + b0) >> 1;
+    sub_window(P, a, L, r, mid, lo, hi);
+    if (lo > j) b0 = mid; else a0 = mid + 1;
+  }
+  qhi = a0 - 1;
+}
+
+// Per-wave tile context: phase, sub-grid origin and valid counts per axis.
+struct TileCtx {
+  int b, head;
+  int r[3], i0[3], nv[3], nt[3];  // nv: valid in sample, nt: valid in tensor
+  int L[3];                       // sample extents
+};
+
+__device__ __forceinline__ TileCtx decode_tile(const Prob &P, const Tiling &Tl,
+                                               int id, int Hn) {
+  TileCtx c;
+  int g[3];
+#pragma unroll
+  for (int a = 2; a >= 0; --a) {
+    const int G = P.ax[a].d * Tl.nt[a];
+    g[a] = id % G;
+    id /= G;
+  }
+  c.head = id % Hn;
+  c.b = id / Hn;
+  int O[3];
+  sample_extents(P, c.b, c.L, O);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const Axis &x = P.ax[a];
+    c.r[a] = g[a] / Tl.nt[a];
+    c.i0[a] = (g[a] % Tl.nt[a]) * Tl.T[a];
+    const int Ls = c.L[a] > c.r[a] ? (c.L[a] - 1 - c.r[a]) / x.d + 1 : 0;
+    const int Lt = x.L > c.r[a] ? (x.L - 1 - c.r[a]) / x.d + 1 : 0;
+    c.nv[a] = max(0, min(Ls - c.i0[a], Tl.T[a]));
+    c.nt[a] = max(0, min(Lt - c.i0[a], Tl.T[a]));
+  }
+  return c;
+}
+
+// Coordinates of slot n (0..31) inside a T0 x T1 x T2 tile.
+__device__ __forceinline__ void tile_slot(const Tiling &Tl, int n, int u[3]) {
+  u[2] = n & (Tl.T[2] - 1);
+  u[1] = (n >> Tl.lgT[2]) & (Tl.T[1] - 1);
+  u[0] = n >> (Tl.lgT[2] + Tl.lgT[1]);
+}
+
+// A row-major box of sub-grid points, innermost extent padded to 2^lgP.
+struct Box {
+  int lo[3], E[3];
+  int lgP;     // padding of the innermost axis (30: the box is one row)
+  int slots;   // padded number of points
+};
+
+__device__ __forceinline__ void box_init(Box &bx) {
+  const int rows = bx.E[0] * bx.E[1];
+  if (rows == 1) {
+    bx.lgP = 30;
+    bx.slots = bx.E[2];
+  } else {
+    bx.lgP = max(3, ceil_log2(bx.E[2]));
+    bx.slots = rows << bx.lgP;
+  }
+}
+
+// Box coordinates of padded slot g; false when g is padding.
+__device__ __forceinline__ bool box_point(const Box &bx, int g, int e[3]) {
+  const int x = g & ((1 << bx.lgP) - 1);
+  const int R = g >> bx.lgP;
+  e[2] = x;
+  e[1] = R % bx.E[1];
+  e[0] = R / bx.E[1];
+  return x < bx.E[2] && e[0] < bx.E[0];
+}
+
+// Per-chunk mask helper: for the 4 groups i of a lane's 16 elements
+// (slots 32c + 8i + 4h + j), the row of group i is wave-uniform; the
+// element is inside [wlo, wlo + ww) on every axis iff rowok(i) and
+// its innermost coordinate xb(i) + 4h + j is.
+__device__ __forceinline__ void chunk_mask(const Box &bx, int c, int h,
+                                           const int wlo[3], const int ww[3],
+                                           bool ok[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = 32 * c + 8 * i;
+    const int R = g >> bx.lgP;
+    const int xb = g & ((1 << bx.lgP) - 1);
+    const int e1 = R % bx.E[1];
+    const int e0 = R / bx.E[1];
+    const bool rowok = (unsigned)(e1 - wlo[1]) < (unsigned)ww[1] &&
+                       (unsigned)(e0 - wlo[0]) < (unsigned)ww[0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      ok[4 * i + j] =
+          rowok && (unsigned)(xb + 4 * h + j - wlo[2]) < (unsigned)ww[2];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Layout self-check: C = A . B for fixed small-integer A (32x16), B (16x32),
+// using the operand and result layouts every kernel here assumes.
+template <typename T>
+__global__ void __launch_bounds__(64) k_selftest(float *out) {
+  typedef typename Mf<T>::v8 v8;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  v8 a, bv;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = 8 * h + e;
+    a[e] = (typename Mf<T>::e)(float)(((n + 2 * k) % 7) - 3);   // A[m=n][k]
+    bv[e] = (typename Mf<T>::e)(float)(((3 * k + n) % 5) - 2);  // B[k][n]
+  }
+  const f32x16 c = Mf<T>::mma(a, bv, zero16());
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+    out[m * 32 + n] = c[r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward.
+template <typename T, int D>
+__global__ void __launch_bounds__(64)
+    k_mfwd(Prob P, Tiling Tl, const T *__restrict__ q, const T *__restrict__ k,
+           const T *__restrict__ v, const T *__restrict__ ek,
+           const T *__restrict__ ev, T *__restrict__ out,
+           float *__restrict__ lse) {
+  typedef Mf<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::e E;
+  constexpr int NK = D / 16;  // k-steps over head_dim
+  constexpr int NC = D / 32;  // 32-row output tiles over head_dim
+  __shared__ E vt[D * kRow];
+
+  const int tile = xcd_tile(blockIdx.x, Tl.n_launch);
+  if (tile >= Tl.n_q) return;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const TileCtx tc = decode_tile(P, Tl, tile, P.H);
+  const int hk = tc.head / P.rep;
+  const float sl2 = P.scale * kLog2e;
+
+  int u[3];
+  tile_slot(Tl, n, u);
+  const bool q_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
+  const bool q_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
+  const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
+  int pos[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
+  const int64_t qrow =
+      (tok_in(P, tc.b, pos[0], pos[1], pos[2]) * P.H + tc.head) * D;
+
+  Box bx;
+  int wlo[3], ww[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+    if (any) {
+      sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
+      sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
+    }
+    bx.lo[a] = lo0;
+    bx.E[a] = any ? hi1 - lo0 : 1;
+    int lo = 0, hi = 0;
+    if (q_valid) sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
+    wlo[a] = lo - bx.lo[a];
+    ww[a] = q_valid ? hi - lo : 0;
+  }
+  box_init(bx);
+  const int nbox = any ? (bx.slots + 31) >> 5 : 0;
+  const int nchunk = nbox + (any ? (P.n_extra + 31) >> 5 : 0);
+
+  v8 qf[NK];
+#pragma unroll
+  for (int t = 0; t < NK; ++t)
+    qf[t] = q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+
+  f32x16 o[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) o[c] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  for (int c = 0; c < nchunk; ++c) {
+    const bool extra = c >= nbox;
+    // key this lane loads (slot n of the chunk)
+    bool kv;
+    const T *kp, *vp;
+    if (!extra) {
+      int e[3];
+      kv = box_point(bx, 32 * c + n, e);
+      int kpos[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+        kpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
+      const int64_t row =
+          (tok_in(P, tc.b, kpos[0], kpos[1], kpos[2]) * P.Hkv + hk) * D;
+      kp = k + row;
+      vp = v + row;
+    } else {
+      const int ne = 32 * (c - nbox) + n;
+      kv = ne < P.n_extra;
+      const int64_t row =
+          (((int64_t)tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
+      kp = ek + row;
+      vp = ev + row;
+    }
+    v8 kf[NK], vf[NK];
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      kf[t] = kv ? ld8(kp + 16 * t + 8 * h) : zero8<T>();
+      vf[t] = kv ? ld8(vp + 16 * t + 8 * h) : zero8<T>();
+    }
+    f32x16 s = zero16();
+#pragma unroll
+    for (int t = 0; t < NK; ++t) s = M::mma(kf[t], qf[t], s);
+
+    bool ok[16];
+    if (!extra) {
+      chunk_mask(bx, c, h, wlo, ww, ok);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        ok[e] = q_valid &&
+                32 * (c - nbox) + 8 * (e >> 2) + 4 * h + (e & 3) < P.n_extra;
+    }
+    float sv[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sv[e] = ok[e] ? s[e] * sl2 : -INFINITY;
+      mx = fmaxf(mx, sv[e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = exp2f(m - mu);
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sv[e] = exp2f(sv[e] - mu);
+      ps += sv[e];
+    }
+    l = fmaf(l, alpha, ps);
+    m = mn;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[cc][e] *= alpha;
+
+    // V^T chunk to LDS: vt[d][key]
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NK; ++t)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[(16 * t + 8 * h + e) * kRow + n] = vf[t][e];
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const v8 bp = pack8<T>(sv + 8 * kb);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+        o[cc] = M::mma(lds_a<T>(vt + (32 * cc + n) * kRow + 16 * kb, h), bp,
+                       o[cc]);
+    }
+  }
+
+  const float lt = l + __shfl_xor(l, 32);
+  const float inv = (q_valid && lt > 0.f) ? 1.f / lt : 0.f;
+  if (q_tensor) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        typename M::v4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = (E)(o[cc][4 * i + j] * inv);
+        *reinterpret_cast<typename M::v4 *>(out + qrow + 32 * cc + 8 * i + 4 * h) = w;
+      }
+    if (lse != nullptr && h == 0)
+      lse[qrow / D] = q_valid ? (m + __log2f(lt)) * kLn2 : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: blocks [0, n_q) are dQ tiles, [n_q, n_q + n_k) dK/dV tiles.
+template <typename T, int D>
+__global__ void __launch_bounds__(64)
+    k_mbwd(Prob P, Tiling Tl, const T *__restrict__ q, const T *__restrict__ k,
+           const T *__restrict__ v, const T *__restrict__ ek,
+           const T *__restrict__ ev, const T *__restrict__ out,
+           const float *__restrict__ lse, const T *__restrict__ dout,
+           const float *__restrict__ dlse, T *__restrict__ dq,
+           T *__restrict__ dk, T *__restrict__ dv) {
+  typedef Mf<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::e E;
+  constexpr int NK = D / 16;
+  constexpr int NC = D / 32;
+  __shared__ E ta[D * kRow];  // transposed chunk (K in dQ tiles, Q in dK/dV)
+  __shared__ E tb[D * kRow];  // transposed dO chunk (dK/dV tiles)
+  __shared__ float s_lse[32], s_del[32];
+
+  const int tile = xcd_tile(blockIdx.x, Tl.n_launch);
+  if (tile >= Tl.n_q + Tl.n_k) return;
+  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const float sl2 = P.scale * kLog2e;
+
+  if (tile < Tl.n_q) {
+    // ------------------------------- dQ role -------------------------------
+    const TileCtx tc = decode_tile(P, Tl, tile, P.H);
+    const int hk = tc.head / P.rep;
+    int u[3];
+    tile_slot(Tl, n, u);
+    const bool q_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
+    const bool q_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
+    const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
+    int pos[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
+    const int64_t qtok = tok_in(P, tc.b, pos[0], pos[1], pos[2]);
+    const int64_t qrow = (qtok * P.H + tc.head) * D;
+
+    Box bx;
+    int wlo[3], ww[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+      if (any) {
+        sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
+        sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
+      }
+      bx.lo[a] = lo0;
+      bx.E[a] = any ? hi1 - lo0 : 1;
+      int lo = 0, hi = 0;
+      if (q_valid) sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
+      wlo[a] = lo - bx.lo[a];
+      ww[a] = q_valid ? hi - lo : 0;
+    }
+    box_init(bx);
+    const int nbox = any ? (bx.slots + 31) >> 5 : 0;
+    const int nchunk = nbox + (any ? (P.n_extra + 31) >> 5 : 0);
+
+    v8 qf[NK], df[NK];
+    float dl = 0.f;
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      qf[t] = q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+      df[t] = q_valid ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
+      const v8 of = q_valid ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dl = fmaf((float)df[t][e], (float)of[e], dl);
+    }
+    dl += __shfl_xor(dl, 32);
+    const int64_t lrow = qtok * P.H + tc.head;
+    if (q_valid && dlse != nullptr) dl -= dlse[lrow];
+    const float lse2 = q_valid ? lse[lrow] * kLog2e : 0.f;
+
+    f32x16 acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = zero16();
+
+    for (int c = 0; c < nchunk; ++c) {
+      const bool extra = c >= nbox;
+      bool kv;
+      const T *kp, *vp;
+      if (!extra) {
+        int e[3];
+        kv = box_point(bx, 32 * c + n, e);
+        int kpos[3];
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+          kpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
+        const int64_t row =
+            (tok_in(P, tc.b, kpos[0], kpos[1], kpos[2]) * P.Hkv + hk) * D;
+        kp = k + row;
+        vp = v + row;
+      } else {
+        const int ne = 32 * (c - nbox) + n;
+        kv = ne < P.n_extra;
+        const int64_t row =
+            (((int64_t)tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
+        kp = ek + row;
+        vp = ev + row;
+      }
+      v8 kf[NK], vf[NK];
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        kf[t] = kv ? ld8(kp + 16 * t + 8 * h) : zero8<T>();
+        vf[t] = kv ? ld8(vp + 16 * t + 8 * h) : zero8<T>();
+      }
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        s = M::mma(kf[t], qf[t], s);
+        dp = M::mma(vf[t], df[t], dp);
+      }
+      bool ok[16];
+      if (!extra) {
+        chunk_mask(bx, c, h, wlo, ww, ok);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          ok[e] = q_valid &&
+                  32 * (c - nbox) + 8 * (e >> 2) + 4 * h + (e & 3) < P.n_extra;
+      }
+      float ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = ok[e] ? exp2f(fmaf(s[e], sl2, -lse2)) : 0.f;
+        ds[e] = p * (dp[e] - dl);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < NK; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ta[(16 * t + 8 * h + e) * kRow + n] = kf[t][e];
+      __syncthreads();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc)
+          acc[cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
+                           bs, acc[cc]);
+      }
+    }
+    if (q_tensor) {
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          typename M::v4 w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            w[j] = (E)(q_valid ? acc[cc][4 * i + j] * P.scale : 0.f);
+          *reinterpret_cast<typename M::v4 *>(dq + qrow + 32 * cc + 8 * i + 4 * h) = w;
+        }
+    }
+    return;
+  }
+
+  // ------------------------------ dK/dV role -------------------------------
+  const TileCtx tc = decode_tile(P, Tl, tile - Tl.n_q, P.Hkv);
+  const int hk = tc.head;
+  int u[3];
+  tile_slot(Tl, n, u);
+  const bool k_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
+  const bool k_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
+  const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
+  int pos[3], Lr[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
+    Lr[a] = tc.L[a] > tc.r[a] ? (tc.L[a] - 1 - tc.r[a]) / P.ax[a].d + 1 : 0;
+  }
+  const int64_t krow =
+      (tok_in(P, tc.b, pos[0], pos[1], pos[2]) * P.Hkv + hk) * D;
+
+  // query box = union of the tile keys' inverse neighborhoods
+  Box bx;
+  int wlo[3], ww[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+    if (any) {
+      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a], lo0, hi0);
+      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + tc.nv[a] - 1, lo1,
+                  hi1);
+    }
+    bx.lo[a] = lo0;
+    bx.E[a] = any ? max(hi1 - lo0 + 1, 1) : 1;
+    int lo = 0, hi = -1;
+    if (k_valid)
+      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + u[a], lo, hi);
+    wlo[a] = lo - bx.lo[a];
+    ww[a] = k_valid ? max(hi - lo + 1, 0) : 0;
+  }
+  box_init(bx);
+  const int nchunk = any ? (bx.slots + 31) >> 5 : 0;
+
+  v8 kf[NK], vf[NK];
+#pragma unroll
+  for (int t = 0; t < NK; ++t) {
+    kf[t] = k_valid ? ld8(k + krow + 16 * t + 8 * h) : zero8<T>();
+    vf[t] = k_valid ? ld8(v + krow + 16 * t + 8 * h) : zero8<T>();
+  }
+  f32x16 adk[NC], adv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    adk[c] = zero16();
+    adv[c] = zero16();
+  }
+
+  for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
+    for (int c = 0; c < nchunk; ++c) {
+      int e[3];
+      const bool qv = box_point(bx, 32 * c + n, e);
+      int qpos[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+        qpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
+      const int64_t qtok = tok_in(P, tc.b, qpos[0], qpos[1], qpos[2]);
+      const int64_t qrow = (qtok * P.H + hq) * D;
+      v8 qa[NK], da[NK];
+      float dl = 0.f;
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        qa[t] = qv ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+        da[t] = qv ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
+        const v8 of = qv ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
+      }
+      dl += __shfl_xor(dl, 32);
+      const int64_t lrow = qtok * P.H + hq;
+      if (qv && dlse != nullptr) dl -= dlse[lrow];
+      const float l2 = qv ? lse[lrow] * kLog2e : 0.f;
+
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < NK; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
+          tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+        }
+      if (h == 0) {
+        s_lse[n] = l2;
+        s_del[n] = dl;
+      }
+      __syncthreads();
+
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        s = M::mma(qa[t], kf[t], s);
+        dp = M::mma(da[t], vf[t], dp);
+      }
+      bool ok[16];
+      chunk_mask(bx, c, h, wlo, ww, ok);
+      float p[16], ds[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
+        const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e2 = 4 * i + j;
+          p[e2] = ok[e2] ? exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
+          ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const v8 bp = pack8<T>(p + 8 * kb);
+        const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          adv[cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h), bp,
+                           adv[cc]);
+          adk[cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h), bs,
+                           adk[cc]);
+        }
+      }
+    }
+  }
+  if (k_tensor) {
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        typename M::v4 wk, wv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wk[j] = (E)(k_valid ? adk[cc][4 * i + j] * P.scale : 0.f);
+          wv[j] = (E)(k_valid ? adv[cc][4 * i + j] : 0.f);
+        }
+        *reinterpret_cast<typename M::v4 *>(dk + krow + 32 * cc + 8 * i + 4 * h) = wk;
+        *reinterpret_cast<typename M::v4 *>(dv + krow + 32 * cc + 8 * i + 4 * h) = wv;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: eligibility, tile choice, launch.
+
+int ilog2(int x) {
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+// Estimated 32-wide chunk count of a tiling (the work the kernels do).
+double tiling_cost(const Prob &P, const int T[3]) {
+  double tiles = 1.0, rows = 1.0;
+  int e2 = 1;
+  for (int a = 0; a < 3; ++a) {
+    const Axis &x = P.ax[a];
+    const int Lr = (x.L + x.d - 1) / x.d;
+    const int nt = (Lr + T[a] - 1) / T[a];
+    tiles *= (double)x.d * nt;
+    const int e = P.dense ? Lr : min(min(T[a], Lr) + x.K - 1, Lr);
+    if (a < 2) rows *= e; else e2 = e;
+  }
+  double slots = rows == 1.0 ? e2 : rows * (double)(1 << max(3, ilog2(e2)));
+  const double chunks = std::ceil(slots / 32.0) + std::ceil(P.n_extra / 32.0);
+  return tiles * chunks;
+}
+
+Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv) {
+  Tiling best{};
+  double best_cost = 1e300;
+  for (int l0 = 0; l0 <= 5; ++l0)
+    for (int l1 = 0; l0 + l1 <= 5; ++l1) {
+      const int l2 = 5 - l0 - l1;
+      const int T[3] = {1 << l0, 1 << l1, 1 << l2};
+      bool ok = true;
+      for (int a = 0; a < 3; ++a)
+        if (P.ax[a].L == 1 && T[a] != 1) ok = false;
+      if (!ok) continue;
+      const double cost = tiling_cost(P, T);
+      if (cost < best_cost) {
+        best_cost = cost;
+        for (int a = 0; a < 3; ++a) best.T[a] = T[a];
+      }
+    }
+  if (best_cost == 1e300) {  // every axis is a unit axis except fewer than 32 points
+    best.T[0] = best.T[1] = 1;
+    best.T[2] = 32;
+  }
+  int grid = 1;
+  for (int a = 0; a < 3; ++a) {
+    best.lgT[a] = ilog2(best.T[a]);
+    const Axis &x = P.ax[a];
+    const int Lr = (x.L + x.d - 1) / x.d;
+    best.nt[a] = (Lr + best.T[a] - 1) / best.T[a];
+    grid *= x.d * best.nt[a];
+  }
+  best.n_q = P.B * heads_q * grid;
+  best.n_k = P.B * heads_kv * grid;
+  return best;
+}
+
+}  // namespace
+
+bool mfma_eligible(const Prob &P, int dtype) {
+  if (dtype != NA_BF16 && dtype != NA_F16) return false;
+  if (P.D != 32 && P.D != 64 && P.D != 128) return false;
+  for (int a = 0; a < 3; ++a) {
+    const Axis &x = P.ax[a];
+    if (x.s != 1) return false;
+    if (!P.dense && !x.causal && (x.K % 2) == 0) return false;
+  }
+  return true;
+}
+
+#define NA_MFMA_D(D_, BODY)      \
+  do {                           \
+    if ((D_) == 32) {            \
+      BODY(32);                  \
+    } else if ((D_) == 64) {     \
+      BODY(64);                  \
+    } else {                     \
+      BODY(128);                 \
+    }                            \
+  } while (0)
+
+void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st) {
+  Tiling Tl = choose_tiling(P, P.H, P.Hkv);
+  Tl.n_launch = (Tl.n_q + 7) & ~7;
+  if (Tl.n_q == 0) return;
+#define FWD_(DD)                                                             \
+  if (dtype == NA_BF16)                                                      \
+    hipLaunchKernelGGL((k_mfwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,  \
+                       st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,      \
+                       (const bf16_t *)v, (const bf16_t *)ek,                \
+                       (const bf16_t *)ev, (bf16_t *)out, lse);              \
+  else                                                                       \
+    hipLaunchKernelGGL((k_mfwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,   \
+                       st, P, Tl, (const f16_t *)q, (const f16_t *)k,        \
+                       (const f16_t *)v, (const f16_t *)ek,                  \
+                       (const f16_t *)ev, (f16_t *)out, lse)
+  NA_MFMA_D(P.D, FWD_);
+#undef FWD_
+}
+
+void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, const void *out,
+              const float *lse, const void *dout, const float *dlse, void *dq,
+              void *dk, void *dv, hipStream_t st) {
+  Tiling Tl = choose_tiling(P, P.H, P.Hkv);
+  Tl.n_launch = (Tl.n_q + Tl.n_k + 7) & ~7;
+  if (Tl.n_q + Tl.n_k == 0) return;
+#define BWD_(DD)                                                               \
+  if (dtype == NA_BF16)                                                        \
+    hipLaunchKernelGGL((k_mbwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,    \
+                       st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,        \
+                       (const bf16_t *)v, (const bf16_t *)ek,                  \
+                       (const bf16_t *)ev, (const bf16_t *)out, lse,           \
+                       (const bf16_t *)dout, dlse, (bf16_t *)dq, (bf16_t *)dk, \
+                       (bf16_t *)dv);                                          \
+  else                                                                         \
+    hipLaunchKernelGGL((k_mbwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,     \
+                       st, P, Tl, (const f16_t *)q, (const f16_t *)k,          \
+                       (const f16_t *)v, (const f16_t *)ek,                    \
+                       (const f16_t *)ev, (const f16_t *)out, lse,             \
+                       (const f16_t *)dout, dlse, (f16_t *)dq, (f16_t *)dk,    \
+                       (f16_t *)dv)
+  NA_MFMA_D(P.D, BWD_);
+#undef BWD_
+}
+
+void mfma_selftest(int dtype, float *out, hipStream_t st) {
+  if (dtype == NA_BF16)
+    hipLaunchKernelGGL(k_selftest<bf16_t>, dim3(1), dim3(64), 0, st, out);
+  else
+    hipLaunchKernelGGL(k_selftest<f16_t>, dim3(1), dim3(64), 0, st, out);
+}
+
+}  // namespace na

@@ -816,6 +816,34 @@ void bwd_t(const Prob &P, const void *q, const void *k, const void *v,
 }
 
 template <typename T>
+void delta_t(const Prob &P, const void *out, const void *dout, const float *dlse,
+             float *delta, hipStream_t st) {
+  const Shape s = pick_shape<T>(P.D);
+  const int64_t n = (int64_t)P.B * P.ax[0].O * P.ax[1].O * P.ax[2].O * P.H;
+#define L_(TT, V, N)                                                         \
+  hipLaunchKernelGGL((k_delta<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
+                     st, P, (const TT *)out, (const TT *)dout, dlse, delta,  \
+                     s.G, s.lgG, n)
+  NA_VALU_DISPATCH(T, s, L_);
+#undef L_
+}
+
+template <typename T>
+void dextra_t(const Prob &P, const void *q, const void *ek, const void *ev,
+              const float *lse, const float *delta, const void *dout, void *dek,
+              void *dev, hipStream_t st) {
+  const Shape s = pick_shape<T>(P.D);
+  const int64_t n = (int64_t)P.B * P.n_extra * P.Hkv;
+#define L_(TT, V, N)                                                          \
+  hipLaunchKernelGGL((k_dextra<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
+                     st, P, (const TT *)q, (const TT *)ek, (const TT *)ev,    \
+                     lse, delta, (const TT *)dout, (TT *)dek, (TT *)dev, s.G, \
+                     s.lgG, n)
+  NA_VALU_DISPATCH(T, s, L_);
+#undef L_
+}
+
+template <typename T>
 void qk_t(const Prob &P, const void *q, const void *k, void *logits,
           hipStream_t st) {
   const Shape s = pick_shape<T>(P.D);
@@ -932,6 +960,17 @@ void valu_bwd(const Prob &P, int dtype, const void *q, const void *k,
               hipStream_t st) {
   NA_BY_DTYPE(dtype, bwd_t, P, q, k, v, ek, ev, out, lse, dout, dlse, dq, dk,
               dv, dek, dev, delta, st);
+}
+
+void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
+                const float *dlse, float *delta, hipStream_t st) {
+  NA_BY_DTYPE(dtype, delta_t, P, out, dout, dlse, delta, st);
+}
+
+void valu_dextra(const Prob &P, int dtype, const void *q, const void *ek,
+                 const void *ev, const float *lse, const float *delta,
+                 const void *dout, void *dek, void *dev, hipStream_t st) {
+  NA_BY_DTYPE(dtype, dextra_t, P, q, ek, ev, lse, delta, dout, dek, dev, st);
 }
 
 void valu_qk(const Prob &P, int dtype, const void *q, const void *k,

@@ -13,11 +13,29 @@ forward).  Tensors must live on a HIP device; there is no CPU path.
 
 from __future__ import annotations
 
+import contextlib
+import os
 from typing import Optional, Sequence
 
 import torch
 
 from . import _lib
+
+# NATTEN_AMD_GENERIC=1 (or the generic_kernels() context) runs the fused op on
+# the generic vector-ALU kernels even where the matrix-core kernels apply.
+_force_generic = os.environ.get("NATTEN_AMD_GENERIC", "0") == "1"
+
+
+@contextlib.contextmanager
+def generic_kernels(enabled: bool = True):
+    """Temporarily route the fused op to the generic kernels."""
+    global _force_generic
+    prev = _force_generic
+    _force_generic = enabled
+    try:
+        yield
+    finally:
+        _force_generic = prev
 
 
 def is_available() -> bool:
@@ -56,7 +74,8 @@ def _params(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_
         rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
         tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
         tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra,
-        _lib.NA_FLAG_DENSE if dense else 0, sample_extent)
+        (_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0),
+        sample_extent)
 
 
 def _out_spatial(spatial: Sequence[int], stride: Sequence[int]) -> tuple[int, ...]:
