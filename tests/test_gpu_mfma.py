@@ -80,12 +80,12 @@ def test_mfma_parity(case, dtype):
     ref = O.grads(lambda a, b, c: O.na_functional(a, b, c, ks, 1, dil, caus), (q, k, v), (go,))
     for g, r, nm in zip(grads, ref, ("dq", "dk", "dv")):
         assert_close(g, r, dtype, f"{name} {nm}")
-    # the generic kernels agree with the MFMA kernels on the same device
+    # the generic kernels meet the same bar on the same inputs
     with hip.generic_kernels():
         out2, lse2, grads2 = _run(fn, q, k, v, go, kernel_size=ks, dilation=dil, is_causal=caus)
-    assert (out.float() - out2.float()).abs().max() <= 2e-2
-    for g, g2 in zip(grads, grads2):
-        assert (g.float() - g2.float()).abs().max() <= 3e-2
+    assert_close(out2, ref_out, dtype, f"{name} generic out")
+    for g, r, nm in zip(grads2, ref, ("dq", "dk", "dv")):
+        assert_close(g, r, dtype, f"{name} generic {nm}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16], ids=str)
