@@ -275,9 +275,19 @@ __global__ void __launch_bounds__(64) k_selftest(float *out) {
 }
 
 // ---------------------------------------------------------------------------
+// A workgroup of W waves owns one tile; wave w walks chunks w, w + W, ...
+// with its own LDS transpose buffer, and the partial results are combined
+// in LDS in wave order at the end (deterministic).  Inside the chunk loop a
+// wave only synchronises with itself.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS ops done
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Forward.
 template <typename T, int D>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
     k_mfwd(Prob P, Tiling Tl, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, T *__restrict__ out,
@@ -287,11 +297,13 @@ __global__ void __launch_bounds__(64)
   typedef typename M::e E;
   constexpr int NK = D / 16;  // k-steps over head_dim
   constexpr int NC = D / 32;  // 32-row output tiles over head_dim
-  __shared__ E vt[D * kRow];
+  extern __shared__ __align__(16) char smem[];
 
   const int tile = xcd_tile(blockIdx.x, Tl.n_launch);
   if (tile >= Tl.n_q) return;
-  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
+  E *vt = reinterpret_cast<E *>(smem) + w * D * kRow;
   const TileCtx tc = decode_tile(P, Tl, tile, P.H);
   const int hk = tc.head / P.rep;
   const float sl2 = P.scale * kLog2e;
@@ -337,7 +349,7 @@ __global__ void __launch_bounds__(64)
   for (int c = 0; c < NC; ++c) o[c] = zero16();
   float m = -INFINITY, l = 0.f;
 
-  for (int c = 0; c < nchunk; ++c) {
+  for (int c = w; c < nchunk; c += W) {
     const bool extra = c >= nbox;
     // key this lane loads (slot n of the chunk)
     bool kv;
@@ -404,13 +416,13 @@ __global__ void __launch_bounds__(64)
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[cc][e] *= alpha;
 
-    // V^T chunk to LDS: vt[d][key]
-    __syncthreads();
+    // V^T chunk to this wave's LDS buffer: vt[d][key]
+    wave_lds_sync();
 #pragma unroll
     for (int t = 0; t < NK; ++t)
 #pragma unroll
       for (int e = 0; e < 8; ++e) vt[(16 * t + 8 * h + e) * kRow + n] = vf[t][e];
-    __syncthreads();
+    wave_lds_sync();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const v8 bp = pack8<T>(sv + 8 * kb);
@@ -421,27 +433,96 @@ __global__ void __launch_bounds__(64)
     }
   }
 
-  const float lt = l + __shfl_xor(l, 32);
+  float lt = l + __shfl_xor(l, 32);
+  if (W > 1) {
+    // waves 1..W-1 hand (m, l, O^T) to wave 0, which merges them in order
+    float *cb = reinterpret_cast<float *>(smem);
+    __syncthreads();  // the combine area overlaps the transpose buffers
+    if (w > 0) {
+      float *mine = cb + (w - 1) * (D * 32 + 64);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          mine[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] = o[cc][e];
+      if (h == 0) {
+        mine[D * 32 + n] = m;
+        mine[D * 32 + 32 + n] = lt;
+      }
+    }
+    __syncthreads();
+    if (w > 0) return;
+    for (int w2 = 1; w2 < W; ++w2) {
+      const float *src = cb + (w2 - 1) * (D * 32 + 64);
+      const float m2 = src[D * 32 + n];
+      const float l2 = src[D * 32 + 32 + n];
+      const float mn = fmaxf(m, m2);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float a0 = exp2f(m - mu), a2 = exp2f(m2 - mu);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          o[cc][e] = o[cc][e] * a0 +
+                     src[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] * a2;
+      lt = lt * a0 + l2 * a2;
+      m = mn;
+    }
+  }
   const float inv = (q_valid && lt > 0.f) ? 1.f / lt : 0.f;
   if (q_tensor) {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        typename M::v4 w;
+        typename M::v4 wv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = (E)(o[cc][4 * i + j] * inv);
-        *reinterpret_cast<typename M::v4 *>(out + qrow + 32 * cc + 8 * i + 4 * h) = w;
+        for (int j = 0; j < 4; ++j) wv[j] = (E)(o[cc][4 * i + j] * inv);
+        *reinterpret_cast<typename M::v4 *>(out + qrow + 32 * cc + 8 * i + 4 * h) = wv;
       }
     if (lse != nullptr && h == 0)
       lse[qrow / D] = q_valid ? (m + __log2f(lt)) * kLn2 : 0.f;
   }
 }
 
+// Sum partial f32x16 accumulators of waves 1..W-1 into wave 0 (in wave
+// order).  Returns false for the waves that are done.
+template <int NC, int NA>
+__device__ __forceinline__ bool combine_sum(char *smem, int W, int w, int n,
+                                            int h, f32x16 (*acc)[NC]) {
+  if (W == 1) return true;
+  float *cb = reinterpret_cast<float *>(smem);
+  constexpr int PER = NA * NC * 16 * 64;  // floats per wave
+  __syncthreads();
+  if (w > 0) {
+    float *mine = cb + (w - 1) * PER;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          mine[((a * NC + cc) * 16 + e) * 64 + h * 32 + n] = acc[a][cc][e];
+  }
+  __syncthreads();
+  if (w > 0) return false;
+  for (int w2 = 1; w2 < W; ++w2) {
+    const float *src = cb + (w2 - 1) * PER;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          acc[a][cc][e] += src[((a * NC + cc) * 16 + e) * 64 + h * 32 + n];
+  }
+  return true;
+}
+
 // ---------------------------------------------------------------------------
 // Backward: blocks [0, n_q) are dQ tiles, [n_q, n_q + n_k) dK/dV tiles.
 template <typename T, int D>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
     k_mbwd(Prob P, Tiling Tl, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, const T *__restrict__ out,
@@ -453,13 +534,18 @@ __global__ void __launch_bounds__(64)
   typedef typename M::e E;
   constexpr int NK = D / 16;
   constexpr int NC = D / 32;
-  __shared__ E ta[D * kRow];  // transposed chunk (K in dQ tiles, Q in dK/dV)
-  __shared__ E tb[D * kRow];  // transposed dO chunk (dK/dV tiles)
-  __shared__ float s_lse[32], s_del[32];
+  extern __shared__ __align__(16) char smem[];
 
   const int tile = xcd_tile(blockIdx.x, Tl.n_launch);
   if (tile >= Tl.n_q + Tl.n_k) return;
-  const int lane = threadIdx.x, n = lane & 31, h = lane >> 5;
+  const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
+  // per-wave scratch: two transposed chunks + per-query lse / delta
+  char *mys = smem + w * (2 * D * kRow * (int)sizeof(E) + 256);
+  E *ta = reinterpret_cast<E *>(mys);                 // K^T (dQ) or Q^T (dK/dV)
+  E *tb = ta + D * kRow;                              // dO^T (dK/dV)
+  float *s_lse = reinterpret_cast<float *>(tb + D * kRow);
+  float *s_del = s_lse + 32;
   const float sl2 = P.scale * kLog2e;
 
   if (tile < Tl.n_q) {
@@ -512,11 +598,11 @@ __global__ void __launch_bounds__(64)
     if (q_valid && dlse != nullptr) dl -= dlse[lrow];
     const float lse2 = q_valid ? lse[lrow] * kLog2e : 0.f;
 
-    f32x16 acc[NC];
+    f32x16 acc[1][NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = zero16();
+    for (int c = 0; c < NC; ++c) acc[0][c] = zero16();
 
-    for (int c = 0; c < nchunk; ++c) {
+    for (int c = w; c < nchunk; c += W) {
       const bool extra = c >= nbox;
       bool kv;
       const T *kp, *vp;
@@ -566,31 +652,32 @@ __global__ void __launch_bounds__(64)
         const float p = ok[e] ? exp2f(fmaf(s[e], sl2, -lse2)) : 0.f;
         ds[e] = p * (dp[e] - dl);
       }
-      __syncthreads();
+      wave_lds_sync();
 #pragma unroll
       for (int t = 0; t < NK; ++t)
 #pragma unroll
         for (int e = 0; e < 8; ++e) ta[(16 * t + 8 * h + e) * kRow + n] = kf[t][e];
-      __syncthreads();
+      wave_lds_sync();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const v8 bs = pack8<T>(ds + 8 * kb);
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc)
-          acc[cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
-                           bs, acc[cc]);
+          acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
+                              bs, acc[0][cc]);
       }
     }
+    if (!combine_sum<NC, 1>(smem, W, w, n, h, acc)) return;
     if (q_tensor) {
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          typename M::v4 w;
+          typename M::v4 wv;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            w[j] = (E)(q_valid ? acc[cc][4 * i + j] * P.scale : 0.f);
-          *reinterpret_cast<typename M::v4 *>(dq + qrow + 32 * cc + 8 * i + 4 * h) = w;
+            wv[j] = (E)(q_valid ? acc[0][cc][4 * i + j] * P.scale : 0.f);
+          *reinterpret_cast<typename M::v4 *>(dq + qrow + 32 * cc + 8 * i + 4 * h) = wv;
         }
     }
     return;
@@ -641,88 +728,90 @@ __global__ void __launch_bounds__(64)
     kf[t] = k_valid ? ld8(k + krow + 16 * t + 8 * h) : zero8<T>();
     vf[t] = k_valid ? ld8(v + krow + 16 * t + 8 * h) : zero8<T>();
   }
-  f32x16 adk[NC], adv[NC];
+  f32x16 acc[2][NC];  // [0] = dK^T, [1] = dV^T
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    adk[c] = zero16();
-    adv[c] = zero16();
+    acc[0][c] = zero16();
+    acc[1][c] = zero16();
   }
 
-  for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
-    for (int c = 0; c < nchunk; ++c) {
-      int e[3];
-      const bool qv = box_point(bx, 32 * c + n, e);
-      int qpos[3];
+  const int nwork = P.rep * nchunk;
+  for (int it = w; it < nwork; it += W) {
+    const int hq = hk * P.rep + it / nchunk;
+    const int c = it % nchunk;
+    int e[3];
+    const bool qv = box_point(bx, 32 * c + n, e);
+    int qpos[3];
 #pragma unroll
-      for (int a = 0; a < 3; ++a)
-        qpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
-      const int64_t qtok = tok_in(P, tc.b, qpos[0], qpos[1], qpos[2]);
-      const int64_t qrow = (qtok * P.H + hq) * D;
-      v8 qa[NK], da[NK];
-      float dl = 0.f;
+    for (int a = 0; a < 3; ++a)
+      qpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
+    const int64_t qtok = tok_in(P, tc.b, qpos[0], qpos[1], qpos[2]);
+    const int64_t qrow = (qtok * P.H + hq) * D;
+    v8 qa[NK], da[NK];
+    float dl = 0.f;
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        qa[t] = qv ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
-        da[t] = qv ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
-        const v8 of = qv ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
+    for (int t = 0; t < NK; ++t) {
+      qa[t] = qv ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+      da[t] = qv ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
+      const v8 of = qv ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
-      }
-      dl += __shfl_xor(dl, 32);
-      const int64_t lrow = qtok * P.H + hq;
-      if (qv && dlse != nullptr) dl -= dlse[lrow];
-      const float l2 = qv ? lse[lrow] * kLog2e : 0.f;
+      for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
+    }
+    dl += __shfl_xor(dl, 32);
+    const int64_t lrow = qtok * P.H + hq;
+    if (qv && dlse != nullptr) dl -= dlse[lrow];
+    const float l2 = qv ? lse[lrow] * kLog2e : 0.f;
 
-      __syncthreads();
+    wave_lds_sync();
 #pragma unroll
-      for (int t = 0; t < NK; ++t)
+    for (int t = 0; t < NK; ++t)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
-          tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
-        }
-      if (h == 0) {
-        s_lse[n] = l2;
-        s_del[n] = dl;
+      for (int i = 0; i < 8; ++i) {
+        ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
+        tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
       }
-      __syncthreads();
+    if (h == 0) {
+      s_lse[n] = l2;
+      s_del[n] = dl;
+    }
+    wave_lds_sync();
 
-      f32x16 s = zero16(), dp = zero16();
+    f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        s = M::mma(qa[t], kf[t], s);
-        dp = M::mma(da[t], vf[t], dp);
+    for (int t = 0; t < NK; ++t) {
+      s = M::mma(qa[t], kf[t], s);
+      dp = M::mma(da[t], vf[t], dp);
+    }
+    bool ok[16];
+    chunk_mask(bx, c, h, wlo, ww, ok);
+    float p[16], ds[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
+      const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e2 = 4 * i + j;
+        p[e2] = ok[e2] ? exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
+        ds[e2] = p[e2] * (dp[e2] - dv4[j]);
       }
-      bool ok[16];
-      chunk_mask(bx, c, h, wlo, ww, ok);
-      float p[16], ds[16];
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
-        const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+    for (int kb = 0; kb < 2; ++kb) {
+      const v8 bp = pack8<T>(p + 8 * kb);
+      const v8 bs = pack8<T>(ds + 8 * kb);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e2 = 4 * i + j;
-          p[e2] = ok[e2] ? exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
-          ds[e2] = p[e2] * (dp[e2] - dv4[j]);
-        }
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const v8 bp = pack8<T>(p + 8 * kb);
-        const v8 bs = pack8<T>(ds + 8 * kb);
-#pragma unroll
-        for (int cc = 0; cc < NC; ++cc) {
-          adv[cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h), bp,
-                           adv[cc]);
-          adk[cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h), bs,
-                           adk[cc]);
-        }
+      for (int cc = 0; cc < NC; ++cc) {
+        acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h), bp,
+                            acc[1][cc]);
+        acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h), bs,
+                            acc[0][cc]);
       }
     }
   }
+  if (!combine_sum<NC, 2>(smem, W, w, n, h, acc)) return;
   if (k_tensor) {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
@@ -731,8 +820,8 @@ __global__ void __launch_bounds__(64)
         typename M::v4 wk, wv;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          wk[j] = (E)(k_valid ? adk[cc][4 * i + j] * P.scale : 0.f);
-          wv[j] = (E)(k_valid ? adv[cc][4 * i + j] : 0.f);
+          wk[j] = (E)(k_valid ? acc[0][cc][4 * i + j] * P.scale : 0.f);
+          wv[j] = (E)(k_valid ? acc[1][cc][4 * i + j] : 0.f);
         }
         *reinterpret_cast<typename M::v4 *>(dk + krow + 32 * cc + 8 * i + 4 * h) = wk;
         *reinterpret_cast<typename M::v4 *>(dv + krow + 32 * cc + 8 * i + 4 * h) = wv;
@@ -749,8 +838,12 @@ int ilog2(int x) {
   return l;
 }
 
-// Estimated 32-wide chunk count of a tiling (the work the kernels do).
-double tiling_cost(const Prob &P, const int T[3]) {
+// Estimated 32-wide chunks per tile and tile count of a tiling.
+struct TileCost {
+  double tiles, chunks;
+};
+
+TileCost tiling_cost(const Prob &P, const int T[3]) {
   double tiles = 1.0, rows = 1.0;
   int e2 = 1;
   for (int a = 0; a < 3; ++a) {
@@ -761,12 +854,12 @@ double tiling_cost(const Prob &P, const int T[3]) {
     const int e = P.dense ? Lr : min(min(T[a], Lr) + x.K - 1, Lr);
     if (a < 2) rows *= e; else e2 = e;
   }
-  double slots = rows == 1.0 ? e2 : rows * (double)(1 << max(3, ilog2(e2)));
-  const double chunks = std::ceil(slots / 32.0) + std::ceil(P.n_extra / 32.0);
-  return tiles * chunks;
+  const double slots =
+      rows == 1.0 ? e2 : rows * (double)(1 << max(3, ilog2(e2)));
+  return {tiles, std::ceil(slots / 32.0) + std::ceil(P.n_extra / 32.0)};
 }
 
-Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv) {
+Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv, double *chunks) {
   Tiling best{};
   double best_cost = 1e300;
   for (int l0 = 0; l0 <= 5; ++l0)
@@ -777,16 +870,13 @@ Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv) {
       for (int a = 0; a < 3; ++a)
         if (P.ax[a].L == 1 && T[a] != 1) ok = false;
       if (!ok) continue;
-      const double cost = tiling_cost(P, T);
-      if (cost < best_cost) {
-        best_cost = cost;
+      const TileCost c = tiling_cost(P, T);
+      if (c.tiles * c.chunks < best_cost) {
+        best_cost = c.tiles * c.chunks;
+        *chunks = c.chunks;
         for (int a = 0; a < 3; ++a) best.T[a] = T[a];
       }
     }
-  if (best_cost == 1e300) {  // every axis is a unit axis except fewer than 32 points
-    best.T[0] = best.T[1] = 1;
-    best.T[2] = 32;
-  }
   int grid = 1;
   for (int a = 0; a < 3; ++a) {
     best.lgT[a] = ilog2(best.T[a]);
@@ -798,6 +888,25 @@ Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv) {
   best.n_q = P.B * heads_q * grid;
   best.n_k = P.B * heads_kv * grid;
   return best;
+}
+
+// Waves per tile: about two chunks each, at most 4 (2 for the backward at
+// head_dim 128, to stay within 64 KB of LDS).
+int waves_for(double chunks, int cap) {
+  const int w = (int)std::ceil(chunks / 2.0);
+  return max(1, min(w, cap));
+}
+
+size_t fwd_lds(int D, int W, int esize) {
+  const size_t tr = (size_t)W * D * kRow * esize;
+  const size_t cb = (size_t)(W - 1) * (D * 32 + 64) * sizeof(float);
+  return tr > cb ? tr : cb;
+}
+
+size_t bwd_lds(int D, int W, int esize) {
+  const size_t tr = (size_t)W * (2 * D * kRow * esize + 256);
+  const size_t cb = (size_t)(W - 1) * 2 * (D / 32) * 16 * 64 * sizeof(float);
+  return tr > cb ? tr : cb;
 }
 
 }  // namespace
@@ -827,18 +936,21 @@ bool mfma_eligible(const Prob &P, int dtype) {
 void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,
               float *lse, hipStream_t st) {
-  Tiling Tl = choose_tiling(P, P.H, P.Hkv);
+  double chunks = 1.0;
+  Tiling Tl = choose_tiling(P, P.H, P.Hkv, &chunks);
   Tl.n_launch = (Tl.n_q + 7) & ~7;
   if (Tl.n_q == 0) return;
+  const int W = waves_for(chunks, 4);
+  const size_t lds = fwd_lds(P.D, W, 2);
 #define FWD_(DD)                                                             \
   if (dtype == NA_BF16)                                                      \
-    hipLaunchKernelGGL((k_mfwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,  \
-                       st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,      \
+    hipLaunchKernelGGL((k_mfwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64 * W), \
+                       lds, st, P, Tl, (const bf16_t *)q, (const bf16_t *)k, \
                        (const bf16_t *)v, (const bf16_t *)ek,                \
                        (const bf16_t *)ev, (bf16_t *)out, lse);              \
   else                                                                       \
-    hipLaunchKernelGGL((k_mfwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,   \
-                       st, P, Tl, (const f16_t *)q, (const f16_t *)k,        \
+    hipLaunchKernelGGL((k_mfwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64 * W),  \
+                       lds, st, P, Tl, (const f16_t *)q, (const f16_t *)k,   \
                        (const f16_t *)v, (const f16_t *)ek,                  \
                        (const f16_t *)ev, (f16_t *)out, lse)
   NA_MFMA_D(P.D, FWD_);
@@ -849,20 +961,23 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, const void *out,
               const float *lse, const void *dout, const float *dlse, void *dq,
               void *dk, void *dv, hipStream_t st) {
-  Tiling Tl = choose_tiling(P, P.H, P.Hkv);
+  double chunks = 1.0;
+  Tiling Tl = choose_tiling(P, P.H, P.Hkv, &chunks);
   Tl.n_launch = (Tl.n_q + Tl.n_k + 7) & ~7;
   if (Tl.n_q + Tl.n_k == 0) return;
+  const int W = waves_for(chunks * P.rep, P.D >= 128 ? 2 : 4);
+  const size_t lds = bwd_lds(P.D, W, 2);
 #define BWD_(DD)                                                               \
   if (dtype == NA_BF16)                                                        \
-    hipLaunchKernelGGL((k_mbwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,    \
-                       st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,        \
+    hipLaunchKernelGGL((k_mbwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64 * W),   \
+                       lds, st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,   \
                        (const bf16_t *)v, (const bf16_t *)ek,                  \
                        (const bf16_t *)ev, (const bf16_t *)out, lse,           \
                        (const bf16_t *)dout, dlse, (bf16_t *)dq, (bf16_t *)dk, \
                        (bf16_t *)dv);                                          \
   else                                                                         \
-    hipLaunchKernelGGL((k_mbwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64), 0,     \
-                       st, P, Tl, (const f16_t *)q, (const f16_t *)k,          \
+    hipLaunchKernelGGL((k_mbwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64 * W),    \
+                       lds, st, P, Tl, (const f16_t *)q, (const f16_t *)k,     \
                        (const f16_t *)v, (const f16_t *)ek,                    \
                        (const f16_t *)ev, (const f16_t *)out, lse,             \
                        (const f16_t *)dout, dlse, (f16_t *)dq, (f16_t *)dk,    \
