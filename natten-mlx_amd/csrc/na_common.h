@@ -134,12 +134,37 @@ struct Prob {
   const int32_t *sample_extent;  // [B, rank] or nullptr
 };
 
+// Division by a divisor fixed at launch (round-up multiply method of
+// Granlund and Montgomery): q = (mulhi(n, mul) + n) >> shift, exact for
+// 0 <= n < 2^31 and 1 <= d < 2^31.
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  FastDiv f;
+  f.d = d;
+  f.shift = l;
+  f.mul = (uint32_t)(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
 // Tiling of the MFMA kernels: 32-query (or 32-key) tiles of T0 x T1 x T2
 // sub-grid points (powers of two), nt[a] tiles per dilation phase.
 struct Tiling {
   int32_t T[3], lgT[3], nt[3];
   int32_t n_q, n_k;   // query tiles, key tiles
   int32_t n_launch;   // workgroups launched (multiple of 8)
+  FastDiv fG[3];      // per-axis tile-grid extent d * nt
+  FastDiv fnt[3];     // per-axis tiles per phase
+  FastDiv fd[3];      // per-axis dilation
+  FastDiv fH, fHk;    // query heads, key/value heads
 };
 
 // Extents of sample b (varlen aware).

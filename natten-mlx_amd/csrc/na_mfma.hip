@@ -108,23 +108,30 @@ __device__ __forceinline__ int ceil_log2(int x) {
 }
 
 // Window of sub-grid query i (phase r) on axis a, as sub-grid [lo, hi).
-__device__ __forceinline__ void sub_window(const Prob &P, int a, int L, int r,
-                                           int i, int &lo, int &hi) {
+__device__ __forceinline__ void sub_window(const Prob &P, const Tiling &Tl,
+                                           int a, int L, int r, int i, int &lo,
+                                           int &hi) {
   const Axis &x = P.ax[a];
   if (P.dense) {
     lo = 0;
     hi = L;
     return;
   }
+  if (x.d == 1) {
+    const AxisWin w = axis_window(i, L, x.K, 1, x.causal);
+    lo = w.lo;
+    hi = w.hi;
+    return;
+  }
   const AxisWin w = axis_window(r + x.d * i, L, x.K, x.d, x.causal);
-  lo = (w.lo - r) / x.d;
-  hi = (w.hi - r + x.d - 1) / x.d;
+  lo = (int)fdiv((uint32_t)(w.lo - r), Tl.fd[a]);
+  hi = (int)fdiv((uint32_t)(w.hi - r + x.d - 1), Tl.fd[a]);
 }
 
 // Sub-grid queries [qlo, qhi] whose windows contain sub-grid key j.
-__device__ __forceinline__ void sub_inverse(const Prob &P, int a, int L, int r,
-                                            int Lr, int j, int &qlo,
-                                            int &qhi) {
+__device__ __forceinline__ void sub_inverse(const Prob &P, const Tiling &Tl,
+                                            int a, int L, int r, int Lr, int j,
+                                            int &qlo, int &qhi) {
   const Axis &x = P.ax[a];
   if (P.dense) {
     qlo = 0;
@@ -146,7 +153,7 @@ __device__ __forceinline__ void sub_inverse(const Prob &P, int a, int L, int r,
   int a0 = 0, b0 = Lr, lo, hi;
   while (a0 < b0) {
     const int mid = (a0 + b0) >> 1;
-    sub_window(P, a, L, r, mid, lo, hi);
+    sub_window(P, Tl, a, L, r, mid, lo, hi);
     if (hi > j) b0 = mid; else a0 = mid + 1;
   }
   qlo = a0;
@@ -154,7 +161,7 @@ __device__ __forceinline__ void sub_inverse(const Prob &P, int a, int L, int r,
   b0 = Lr;
   while (a0 < b0) {
     const int mid = (a0 + b0) >> 1;
-    sub_window(P, a, L, r, mid, lo, hi);
+    sub_window(P, Tl, a, L, r, mid, lo, hi);
     if (lo > j) b0 = mid; else a0 = mid + 1;
   }
   qhi = a0 - 1;
@@ -168,26 +175,35 @@ struct TileCtx {
 };
 
 __device__ __forceinline__ TileCtx decode_tile(const Prob &P, const Tiling &Tl,
-                                               int id, int Hn) {
+                                               int id, const FastDiv &fHn) {
   TileCtx c;
   int g[3];
+  uint32_t rest = (uint32_t)id;
 #pragma unroll
   for (int a = 2; a >= 0; --a) {
-    const int G = P.ax[a].d * Tl.nt[a];
-    g[a] = id % G;
-    id /= G;
+    const uint32_t qd = fdiv(rest, Tl.fG[a]);
+    g[a] = (int)(rest - qd * Tl.fG[a].d);
+    rest = qd;
   }
-  c.head = id % Hn;
-  c.b = id / Hn;
+  const uint32_t bq = fdiv(rest, fHn);
+  c.head = (int)(rest - bq * fHn.d);
+  c.b = (int)bq;
   int O[3];
   sample_extents(P, c.b, c.L, O);
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     const Axis &x = P.ax[a];
-    c.r[a] = g[a] / Tl.nt[a];
-    c.i0[a] = (g[a] % Tl.nt[a]) * Tl.T[a];
-    const int Ls = c.L[a] > c.r[a] ? (c.L[a] - 1 - c.r[a]) / x.d + 1 : 0;
-    const int Lt = x.L > c.r[a] ? (x.L - 1 - c.r[a]) / x.d + 1 : 0;
+    const uint32_t rr = fdiv((uint32_t)g[a], Tl.fnt[a]);
+    c.r[a] = (int)rr;
+    c.i0[a] = (g[a] - (int)rr * Tl.nt[a]) * Tl.T[a];
+    int Ls, Lt;
+    if (x.d == 1) {
+      Ls = c.L[a];
+      Lt = x.L;
+    } else {
+      Ls = c.L[a] > c.r[a] ? (int)fdiv((uint32_t)(c.L[a] - 1 - c.r[a]), Tl.fd[a]) + 1 : 0;
+      Lt = x.L > c.r[a] ? (int)fdiv((uint32_t)(x.L - 1 - c.r[a]), Tl.fd[a]) + 1 : 0;
+    }
     c.nv[a] = max(0, min(Ls - c.i0[a], Tl.T[a]));
     c.nt[a] = max(0, min(Lt - c.i0[a], Tl.T[a]));
   }
@@ -219,30 +235,52 @@ __device__ __forceinline__ void box_init(Box &bx) {
   }
 }
 
-// Box coordinates of padded slot g; false when g is padding.
-__device__ __forceinline__ bool box_point(const Box &bx, int g, int e[3]) {
-  const int x = g & ((1 << bx.lgP) - 1);
-  const int R = g >> bx.lgP;
-  e[2] = x;
-  e[1] = R % bx.E[1];
-  e[0] = R / bx.E[1];
-  return x < bx.E[2] && e[0] < bx.E[0];
+// Row coordinates (e0, e1) of padded-box row R, advanced incrementally so
+// the chunk loop never divides: rows only move forward by a few per chunk.
+struct RowCursor {
+  int R, e0, e1;
+};
+
+__device__ __forceinline__ void row_step(int &e0, int &e1, int dr, int E1) {
+  e1 += dr;
+  while (e1 >= E1) {
+    e1 -= E1;
+    ++e0;
+  }
+}
+
+// Move the cursor to the first row of the chunk starting at slot g0.
+__device__ __forceinline__ void cursor_seek(RowCursor &rc, const Box &bx,
+                                            int g0) {
+  const int R = g0 >> bx.lgP;
+  row_step(rc.e0, rc.e1, R - rc.R, bx.E[1]);
+  rc.R = R;
+}
+
+// Box coordinates of padded slot g0 + n; false when it is padding.
+__device__ __forceinline__ bool box_point(const Box &bx, const RowCursor &rc,
+                                          int g0, int n, int e[3]) {
+  const int g = g0 + n;
+  e[2] = g & ((1 << bx.lgP) - 1);
+  e[0] = rc.e0;
+  e[1] = rc.e1;
+  row_step(e[0], e[1], (g >> bx.lgP) - rc.R, bx.E[1]);
+  return e[2] < bx.E[2] && e[0] < bx.E[0];
 }
 
 // Per-chunk mask helper: for the 4 groups i of a lane's 16 elements
-// (slots 32c + 8i + 4h + j), the row of group i is wave-uniform; the
+// (slots g0 + 8i + 4h + j), the row of group i is wave-uniform; the
 // element is inside [wlo, wlo + ww) on every axis iff rowok(i) and
 // its innermost coordinate xb(i) + 4h + j is.
-__device__ __forceinline__ void chunk_mask(const Box &bx, int c, int h,
-                                           const int wlo[3], const int ww[3],
-                                           bool ok[16]) {
+__device__ __forceinline__ void chunk_mask(const Box &bx, const RowCursor &rc,
+                                           int g0, int h, const int wlo[3],
+                                           const int ww[3], bool ok[16]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int g = 32 * c + 8 * i;
-    const int R = g >> bx.lgP;
+    const int g = g0 + 8 * i;
     const int xb = g & ((1 << bx.lgP) - 1);
-    const int e1 = R % bx.E[1];
-    const int e0 = R / bx.E[1];
+    int e0 = rc.e0, e1 = rc.e1;
+    row_step(e0, e1, (g >> bx.lgP) - rc.R, bx.E[1]);
     const bool rowok = (unsigned)(e1 - wlo[1]) < (unsigned)ww[1] &&
                        (unsigned)(e0 - wlo[0]) < (unsigned)ww[0];
 #pragma unroll
@@ -304,7 +342,7 @@ __global__ void __launch_bounds__(256)
   const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
   E *vt = reinterpret_cast<E *>(smem) + w * D * kRow;
-  const TileCtx tc = decode_tile(P, Tl, tile, P.H);
+  const TileCtx tc = decode_tile(P, Tl, tile, Tl.fH);
   const int hk = tc.head / P.rep;
   const float sl2 = P.scale * kLog2e;
 
@@ -325,13 +363,13 @@ __global__ void __launch_bounds__(256)
   for (int a = 0; a < 3; ++a) {
     int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
     if (any) {
-      sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
-      sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
+      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
+      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
     }
     bx.lo[a] = lo0;
     bx.E[a] = any ? hi1 - lo0 : 1;
     int lo = 0, hi = 0;
-    if (q_valid) sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
+    if (q_valid) sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
     wlo[a] = lo - bx.lo[a];
     ww[a] = q_valid ? hi - lo : 0;
   }
@@ -349,14 +387,16 @@ __global__ void __launch_bounds__(256)
   for (int c = 0; c < NC; ++c) o[c] = zero16();
   float m = -INFINITY, l = 0.f;
 
+  RowCursor rc{0, 0, 0};
   for (int c = w; c < nchunk; c += W) {
     const bool extra = c >= nbox;
+    if (!extra) cursor_seek(rc, bx, 32 * c);
     // key this lane loads (slot n of the chunk)
     bool kv;
     const T *kp, *vp;
     if (!extra) {
       int e[3];
-      kv = box_point(bx, 32 * c + n, e);
+      kv = box_point(bx, rc, 32 * c, n, e);
       int kpos[3];
 #pragma unroll
       for (int a = 0; a < 3; ++a)
@@ -385,7 +425,7 @@ __global__ void __launch_bounds__(256)
 
     bool ok[16];
     if (!extra) {
-      chunk_mask(bx, c, h, wlo, ww, ok);
+      chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
     } else {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
@@ -550,7 +590,7 @@ __global__ void __launch_bounds__(256)
 
   if (tile < Tl.n_q) {
     // ------------------------------- dQ role -------------------------------
-    const TileCtx tc = decode_tile(P, Tl, tile, P.H);
+    const TileCtx tc = decode_tile(P, Tl, tile, Tl.fH);
     const int hk = tc.head / P.rep;
     int u[3];
     tile_slot(Tl, n, u);
@@ -569,13 +609,13 @@ __global__ void __launch_bounds__(256)
     for (int a = 0; a < 3; ++a) {
       int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
       if (any) {
-        sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
-        sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
+        sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
+        sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
       }
       bx.lo[a] = lo0;
       bx.E[a] = any ? hi1 - lo0 : 1;
       int lo = 0, hi = 0;
-      if (q_valid) sub_window(P, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
+      if (q_valid) sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
       wlo[a] = lo - bx.lo[a];
       ww[a] = q_valid ? hi - lo : 0;
     }
@@ -602,13 +642,15 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[0][c] = zero16();
 
+    RowCursor rc{0, 0, 0};
     for (int c = w; c < nchunk; c += W) {
       const bool extra = c >= nbox;
+      if (!extra) cursor_seek(rc, bx, 32 * c);
       bool kv;
       const T *kp, *vp;
       if (!extra) {
         int e[3];
-        kv = box_point(bx, 32 * c + n, e);
+        kv = box_point(bx, rc, 32 * c, n, e);
         int kpos[3];
 #pragma unroll
         for (int a = 0; a < 3; ++a)
@@ -639,7 +681,7 @@ __global__ void __launch_bounds__(256)
       }
       bool ok[16];
       if (!extra) {
-        chunk_mask(bx, c, h, wlo, ww, ok);
+        chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
       } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e)
@@ -684,7 +726,7 @@ __global__ void __launch_bounds__(256)
   }
 
   // ------------------------------ dK/dV role -------------------------------
-  const TileCtx tc = decode_tile(P, Tl, tile - Tl.n_q, P.Hkv);
+  const TileCtx tc = decode_tile(P, Tl, tile - Tl.n_q, Tl.fHk);
   const int hk = tc.head;
   int u[3];
   tile_slot(Tl, n, u);
@@ -707,15 +749,15 @@ __global__ void __launch_bounds__(256)
   for (int a = 0; a < 3; ++a) {
     int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
     if (any) {
-      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a], lo0, hi0);
-      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + tc.nv[a] - 1, lo1,
+      sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a], lo0, hi0);
+      sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + tc.nv[a] - 1, lo1,
                   hi1);
     }
     bx.lo[a] = lo0;
     bx.E[a] = any ? max(hi1 - lo0 + 1, 1) : 1;
     int lo = 0, hi = -1;
     if (k_valid)
-      sub_inverse(P, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + u[a], lo, hi);
+      sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + u[a], lo, hi);
     wlo[a] = lo - bx.lo[a];
     ww[a] = k_valid ? max(hi - lo + 1, 0) : 0;
   }
@@ -735,12 +777,12 @@ __global__ void __launch_bounds__(256)
     acc[1][c] = zero16();
   }
 
-  const int nwork = P.rep * nchunk;
-  for (int it = w; it < nwork; it += W) {
-    const int hq = hk * P.rep + it / nchunk;
-    const int c = it % nchunk;
+  for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
+  RowCursor rc{0, 0, 0};
+  for (int c = w; c < nchunk; c += W) {
+    cursor_seek(rc, bx, 32 * c);
     int e[3];
-    const bool qv = box_point(bx, 32 * c + n, e);
+    const bool qv = box_point(bx, rc, 32 * c, n, e);
     int qpos[3];
 #pragma unroll
     for (int a = 0; a < 3; ++a)
@@ -783,7 +825,7 @@ __global__ void __launch_bounds__(256)
       dp = M::mma(da[t], vf[t], dp);
     }
     bool ok[16];
-    chunk_mask(bx, c, h, wlo, ww, ok);
+    chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
     float p[16], ds[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -810,6 +852,7 @@ __global__ void __launch_bounds__(256)
                             acc[0][cc]);
       }
     }
+  }
   }
   if (!combine_sum<NC, 2>(smem, W, w, n, h, acc)) return;
   if (k_tensor) {
@@ -887,13 +930,20 @@ Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv, double *chunks) {
   }
   best.n_q = P.B * heads_q * grid;
   best.n_k = P.B * heads_kv * grid;
+  for (int a = 0; a < 3; ++a) {
+    best.fG[a] = make_fastdiv((uint32_t)(P.ax[a].d * best.nt[a]));
+    best.fnt[a] = make_fastdiv((uint32_t)best.nt[a]);
+    best.fd[a] = make_fastdiv((uint32_t)P.ax[a].d);
+  }
+  best.fH = make_fastdiv((uint32_t)heads_q);
+  best.fHk = make_fastdiv((uint32_t)heads_kv);
   return best;
 }
 
-// Waves per tile: about two chunks each, at most 4 (2 for the backward at
+// Waves per tile: one per ~6 chunks, at most `cap` (2 for the backward at
 // head_dim 128, to stay within 64 KB of LDS).
 int waves_for(double chunks, int cap) {
-  const int w = (int)std::ceil(chunks / 2.0);
+  const int w = (int)std::ceil(chunks / 6.0);
   return max(1, min(w, cap));
 }
 
