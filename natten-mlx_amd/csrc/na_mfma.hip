@@ -235,58 +235,79 @@ __device__ __forceinline__ void box_init(Box &bx) {
   }
 }
 
+__device__ __forceinline__ int uni(int x) {
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
 // Row coordinates (e0, e1) of padded-box row R, advanced incrementally so
-// the chunk loop never divides: rows only move forward by a few per chunk.
+// the chunk loop never divides; the cursor is wave-uniform.
 struct RowCursor {
   int R, e0, e1;
 };
 
-__device__ __forceinline__ void row_step(int &e0, int &e1, int dr, int E1) {
-  e1 += dr;
-  while (e1 >= E1) {
-    e1 -= E1;
-    ++e0;
+// Advance (e0, e1) by dr rows, 0 <= dr <= 3 (a chunk spans at most 4
+// rows), without branches: e1 + dr wraps at most three times.
+__device__ __forceinline__ void row_add(int &e0, int &e1, int dr, int E1) {
+  const int x = e1 + dr;
+  const int wraps = (int)(x >= E1) + (int)(x >= 2 * E1) + (int)(x >= 3 * E1);
+  e1 = x - wraps * E1;
+  e0 += wraps;
+}
+
+// First row of a 32-slot chunk (wave-uniform).
+struct ChunkRows {
+  int R0, e0, e1;
+};
+
+// Move the cursor to the chunk starting at slot g0 (rows only advance).
+__device__ __forceinline__ ChunkRows chunk_rows(RowCursor &rc, const Box &bx,
+                                                int g0) {
+  const int R = uni(g0 >> bx.lgP);
+  while (rc.R + 3 < R) {
+    row_add(rc.e0, rc.e1, 3, bx.E[1]);
+    rc.R += 3;
   }
-}
-
-// Move the cursor to the first row of the chunk starting at slot g0.
-__device__ __forceinline__ void cursor_seek(RowCursor &rc, const Box &bx,
-                                            int g0) {
-  const int R = g0 >> bx.lgP;
-  row_step(rc.e0, rc.e1, R - rc.R, bx.E[1]);
+  row_add(rc.e0, rc.e1, R - rc.R, bx.E[1]);
   rc.R = R;
+  rc.e0 = uni(rc.e0);
+  rc.e1 = uni(rc.e1);
+  return ChunkRows{R, rc.e0, rc.e1};
 }
 
-// Box coordinates of padded slot g0 + n; false when it is padding.
-__device__ __forceinline__ bool box_point(const Box &bx, const RowCursor &rc,
+// Box coordinates of padded slot g0 + n, clamped into the box; returns
+// false when the slot is padding (its clamped point is a real box point).
+__device__ __forceinline__ bool box_point(const Box &bx, const ChunkRows &cr,
                                           int g0, int n, int e[3]) {
   const int g = g0 + n;
   e[2] = g & ((1 << bx.lgP) - 1);
-  e[0] = rc.e0;
-  e[1] = rc.e1;
-  row_step(e[0], e[1], (g >> bx.lgP) - rc.R, bx.E[1]);
-  return e[2] < bx.E[2] && e[0] < bx.E[0];
+  e[0] = cr.e0;
+  e[1] = cr.e1;
+  row_add(e[0], e[1], (g >> bx.lgP) - cr.R0, bx.E[1]);
+  const bool inside = (e[2] < bx.E[2]) & (e[0] < bx.E[0]);
+  e[2] = min(e[2], bx.E[2] - 1);
+  e[0] = min(e[0], bx.E[0] - 1);
+  return inside;
 }
 
 // Per-chunk mask helper: for the 4 groups i of a lane's 16 elements
 // (slots g0 + 8i + 4h + j), the row of group i is wave-uniform; the
 // element is inside [wlo, wlo + ww) on every axis iff rowok(i) and
 // its innermost coordinate xb(i) + 4h + j is.
-__device__ __forceinline__ void chunk_mask(const Box &bx, const RowCursor &rc,
+__device__ __forceinline__ void chunk_mask(const Box &bx, const ChunkRows &cr,
                                            int g0, int h, const int wlo[3],
                                            const int ww[3], bool ok[16]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int g = g0 + 8 * i;
     const int xb = g & ((1 << bx.lgP) - 1);
-    int e0 = rc.e0, e1 = rc.e1;
-    row_step(e0, e1, (g >> bx.lgP) - rc.R, bx.E[1]);
-    const bool rowok = (unsigned)(e1 - wlo[1]) < (unsigned)ww[1] &&
-                       (unsigned)(e0 - wlo[0]) < (unsigned)ww[0];
+    int e0 = cr.e0, e1 = cr.e1;
+    row_add(e0, e1, uni((g >> bx.lgP) - cr.R0), bx.E[1]);
+    const bool rowok = ((unsigned)(e1 - wlo[1]) < (unsigned)ww[1]) &
+                       ((unsigned)(e0 - wlo[0]) < (unsigned)ww[0]);
+    const int x0 = xb + 4 * h - wlo[2];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      ok[4 * i + j] =
-          rowok && (unsigned)(xb + 4 * h + j - wlo[2]) < (unsigned)ww[2];
+      ok[4 * i + j] = rowok & ((unsigned)(x0 + j) < (unsigned)ww[2]);
   }
 }
 
@@ -315,12 +336,166 @@ __global__ void __launch_bounds__(64) k_selftest(float *out) {
 // ---------------------------------------------------------------------------
 // A workgroup of W waves owns one tile; wave w walks chunks w, w + W, ...
 // with its own LDS transpose buffer, and the partial results are combined
-// in LDS in wave order at the end (deterministic).  Inside the chunk loop a
+// in LDS in wave order at the end (deterministic).  Inside the chunk loops a
 // wave only synchronises with itself.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS ops done
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
+}
+
+// Element offset of box point e: base + e0*S0 + e1*S1 + e2*S2 (wave-uniform
+// base and strides, so the chunk loops carry four scalars for addressing).
+struct BoxAddr {
+  int64_t base;
+  int S[3];
+};
+
+// Box of sub-grid points of phase tc.r, origin bx.lo, rows of `heads`
+// heads: token strides along each axis times the dilation.
+__device__ __forceinline__ BoxAddr box_addr(const Prob &P, const TileCtx &tc,
+                                            const Box &bx, int head,
+                                            int heads) {
+  BoxAddr ba;
+  int p[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) p[a] = tc.r[a] + P.ax[a].d * bx.lo[a];
+  const int row = heads * P.D;
+  ba.base = tok_in(P, tc.b, p[0], p[1], p[2]) * row + (int64_t)head * P.D;
+  ba.S[2] = uni(P.ax[2].d * row);
+  ba.S[1] = uni(P.ax[1].d * P.ax[2].L * row);
+  ba.S[0] = uni(P.ax[0].d * P.ax[1].L * P.ax[2].L * row);
+  return ba;
+}
+
+__device__ __forceinline__ int box_off(const BoxAddr &ba, const int e[3]) {
+  return e[0] * ba.S[0] + e[1] * ba.S[1] + e[2] * ba.S[2];
+}
+
+// First global chunk index >= lo that wave w of W owns (c == w mod W).
+__device__ __forceinline__ int first_owned(int lo, int w, int W) {
+  return lo + (((w - lo) % W) + W) % W;
+}
+
+// Online-softmax state of one query column (the lane pair n, n + 32).
+template <int NC>
+struct Softmax {
+  f32x16 o[NC];
+  float m, l;
+};
+
+// One 32-key chunk of the forward: S^T = K.Q^T, masked online softmax,
+// O^T += V^T.P^T (V^T staged through this wave's LDS buffer).
+template <typename T, int D>
+__device__ __forceinline__ void fwd_chunk(Softmax<D / 32> &st,
+                                          const typename Mf<T>::v8 *qf,
+                                          const T *kp, const T *vp,
+                                          const bool ok[16], float sl2,
+                                          typename Mf<T>::e *vt, int n, int h) {
+  typedef Mf<T> M;
+  typedef typename M::v8 v8;
+  constexpr int NK = D / 16, NC = D / 32;
+  v8 kf[NK], vf[NK];
+#pragma unroll
+  for (int t = 0; t < NK; ++t) {
+    kf[t] = ld8(kp + 16 * t + 8 * h);
+    vf[t] = ld8(vp + 16 * t + 8 * h);
+  }
+  f32x16 s = zero16();
+#pragma unroll
+  for (int t = 0; t < NK; ++t) s = M::mma(kf[t], qf[t], s);
+  float sv[16];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    sv[e] = ok[e] ? s[e] * sl2 : -INFINITY;
+    mx = fmaxf(mx, sv[e]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mn = fmaxf(st.m, mx);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - mu);
+  float ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    sv[e] = __builtin_amdgcn_exp2f(sv[e] - mu);
+    ps += sv[e];
+  }
+  st.l = fmaf(st.l, alpha, ps);
+  st.m = mn;
+#pragma unroll
+  for (int cc = 0; cc < NC; ++cc)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st.o[cc][e] *= alpha;
+  wave_lds_sync();
+#pragma unroll
+  for (int t = 0; t < NK; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vt[(16 * t + 8 * h + e) * kRow + n] = vf[t][e];
+  wave_lds_sync();
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const v8 bp = pack8<T>(sv + 8 * kb);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+      st.o[cc] = M::mma(lds_a<T>(vt + (32 * cc + n) * kRow + 16 * kb, h), bp,
+                        st.o[cc]);
+  }
+}
+
+// Query-tile setup shared by the forward and the dQ role: the lane's
+// query, its window relative to the tile's key box, and the box itself.
+struct QTile {
+  TileCtx tc;
+  bool q_valid, q_tensor, any;
+  int64_t qtok;
+  Box bx;
+  int wlo[3], ww[3];
+  int nbox, nextra;
+};
+
+__device__ __forceinline__ QTile query_tile(const Prob &P, const Tiling &Tl,
+                                            int tile, int n) {
+  QTile Q;
+  Q.tc = decode_tile(P, Tl, tile, Tl.fH);
+  const TileCtx &tc = Q.tc;
+  int u[3];
+  tile_slot(Tl, n, u);
+  Q.q_tensor = (u[0] < tc.nt[0]) & (u[1] < tc.nt[1]) & (u[2] < tc.nt[2]);
+  Q.q_valid = (u[0] < tc.nv[0]) & (u[1] < tc.nv[1]) & (u[2] < tc.nv[2]);
+  Q.any = (tc.nv[0] > 0) & (tc.nv[1] > 0) & (tc.nv[2] > 0);
+  int pos[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
+  Q.qtok = tok_in(P, tc.b, pos[0], pos[1], pos[2]);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
+    if (Q.any) {
+      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
+      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
+    }
+    Q.bx.lo[a] = uni(lo0);
+    Q.bx.E[a] = uni(Q.any ? hi1 - lo0 : 1);
+    int lo = 0, hi = 0;
+    if (Q.q_valid)
+      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
+    Q.wlo[a] = lo - Q.bx.lo[a];
+    Q.ww[a] = Q.q_valid ? hi - lo : 0;
+  }
+  box_init(Q.bx);
+  Q.bx.lgP = uni(Q.bx.lgP);
+  Q.nbox = uni(Q.any ? (Q.bx.slots + 31) >> 5 : 0);
+  Q.nextra = uni(Q.any ? (P.n_extra + 31) >> 5 : 0);
+  return Q;
+}
+
+// Mask of a chunk of additional tokens (global chunk index c >= nbox).
+__device__ __forceinline__ void extra_mask(bool q_valid, int first, int n_extra,
+                                           int h, bool ok[16]) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    ok[e] = q_valid & (first + 8 * (e >> 2) + 4 * h + (e & 3) < n_extra);
 }
 
 // Forward.
@@ -342,138 +517,45 @@ __global__ void __launch_bounds__(256)
   const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
   E *vt = reinterpret_cast<E *>(smem) + w * D * kRow;
-  const TileCtx tc = decode_tile(P, Tl, tile, Tl.fH);
-  const int hk = tc.head / P.rep;
+  const QTile Q = query_tile(P, Tl, tile, n);
+  const int hk = Q.tc.head / P.rep;
   const float sl2 = P.scale * kLog2e;
-
-  int u[3];
-  tile_slot(Tl, n, u);
-  const bool q_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
-  const bool q_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
-  const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
-  int pos[3];
-#pragma unroll
-  for (int a = 0; a < 3; ++a) pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
-  const int64_t qrow =
-      (tok_in(P, tc.b, pos[0], pos[1], pos[2]) * P.H + tc.head) * D;
-
-  Box bx;
-  int wlo[3], ww[3];
-#pragma unroll
-  for (int a = 0; a < 3; ++a) {
-    int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
-    if (any) {
-      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
-      sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
-    }
-    bx.lo[a] = lo0;
-    bx.E[a] = any ? hi1 - lo0 : 1;
-    int lo = 0, hi = 0;
-    if (q_valid) sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
-    wlo[a] = lo - bx.lo[a];
-    ww[a] = q_valid ? hi - lo : 0;
-  }
-  box_init(bx);
-  const int nbox = any ? (bx.slots + 31) >> 5 : 0;
-  const int nchunk = nbox + (any ? (P.n_extra + 31) >> 5 : 0);
+  const int64_t qrow = (Q.qtok * P.H + Q.tc.head) * D;
 
   v8 qf[NK];
 #pragma unroll
   for (int t = 0; t < NK; ++t)
-    qf[t] = q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+    qf[t] = Q.q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
 
-  f32x16 o[NC];
+  Softmax<NC> st;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) o[c] = zero16();
-  float m = -INFINITY, l = 0.f;
+  for (int c = 0; c < NC; ++c) st.o[c] = zero16();
+  st.m = -INFINITY;
+  st.l = 0.f;
 
+  const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
   RowCursor rc{0, 0, 0};
-  for (int c = w; c < nchunk; c += W) {
-    const bool extra = c >= nbox;
-    if (!extra) cursor_seek(rc, bx, 32 * c);
-    // key this lane loads (slot n of the chunk)
-    bool kv;
-    const T *kp, *vp;
-    if (!extra) {
-      int e[3];
-      kv = box_point(bx, rc, 32 * c, n, e);
-      int kpos[3];
-#pragma unroll
-      for (int a = 0; a < 3; ++a)
-        kpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
-      const int64_t row =
-          (tok_in(P, tc.b, kpos[0], kpos[1], kpos[2]) * P.Hkv + hk) * D;
-      kp = k + row;
-      vp = v + row;
-    } else {
-      const int ne = 32 * (c - nbox) + n;
-      kv = ne < P.n_extra;
-      const int64_t row =
-          (((int64_t)tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
-      kp = ek + row;
-      vp = ev + row;
-    }
-    v8 kf[NK], vf[NK];
-#pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      kf[t] = kv ? ld8(kp + 16 * t + 8 * h) : zero8<T>();
-      vf[t] = kv ? ld8(vp + 16 * t + 8 * h) : zero8<T>();
-    }
-    f32x16 s = zero16();
-#pragma unroll
-    for (int t = 0; t < NK; ++t) s = M::mma(kf[t], qf[t], s);
-
+  for (int c = w; c < Q.nbox; c += W) {
+    const ChunkRows cr = chunk_rows(rc, Q.bx, 32 * c);
+    int e[3];
+    box_point(Q.bx, cr, 32 * c, n, e);
+    const int off = box_off(ka, e);
     bool ok[16];
-    if (!extra) {
-      chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        ok[e] = q_valid &&
-                32 * (c - nbox) + 8 * (e >> 2) + 4 * h + (e & 3) < P.n_extra;
-    }
-    float sv[16];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      sv[e] = ok[e] ? s[e] * sl2 : -INFINITY;
-      mx = fmaxf(mx, sv[e]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx);
-    const float mu = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp2f(m - mu);
-    float ps = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      sv[e] = exp2f(sv[e] - mu);
-      ps += sv[e];
-    }
-    l = fmaf(l, alpha, ps);
-    m = mn;
-#pragma unroll
-    for (int cc = 0; cc < NC; ++cc)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[cc][e] *= alpha;
-
-    // V^T chunk to this wave's LDS buffer: vt[d][key]
-    wave_lds_sync();
-#pragma unroll
-    for (int t = 0; t < NK; ++t)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(16 * t + 8 * h + e) * kRow + n] = vf[t][e];
-    wave_lds_sync();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const v8 bp = pack8<T>(sv + 8 * kb);
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc)
-        o[cc] = M::mma(lds_a<T>(vt + (32 * cc + n) * kRow + 16 * kb, h), bp,
-                       o[cc]);
-    }
+    chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
+    fwd_chunk<T, D>(st, qf, k + ka.base + off, v + ka.base + off, ok, sl2, vt,
+                    n, h);
+  }
+  for (int c = first_owned(Q.nbox, w, W); c < Q.nbox + Q.nextra; c += W) {
+    const int first = 32 * (c - Q.nbox);
+    const int ne = min(first + n, P.n_extra - 1);
+    const int64_t row = (((int64_t)Q.tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
+    bool ok[16];
+    extra_mask(Q.q_valid, first, P.n_extra, h, ok);
+    fwd_chunk<T, D>(st, qf, ek + row, ev + row, ok, sl2, vt, n, h);
   }
 
-  float lt = l + __shfl_xor(l, 32);
+  float lt = st.l + __shfl_xor(st.l, 32);
+  float m = st.m;
   if (W > 1) {
     // waves 1..W-1 hand (m, l, O^T) to wave 0, which merges them in order
     float *cb = reinterpret_cast<float *>(smem);
@@ -484,7 +566,7 @@ __global__ void __launch_bounds__(256)
       for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          mine[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] = o[cc][e];
+          mine[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] = st.o[cc][e];
       if (h == 0) {
         mine[D * 32 + n] = m;
         mine[D * 32 + 32 + n] = lt;
@@ -498,30 +580,31 @@ __global__ void __launch_bounds__(256)
       const float l2 = src[D * 32 + 32 + n];
       const float mn = fmaxf(m, m2);
       const float mu = mn == -INFINITY ? 0.f : mn;
-      const float a0 = exp2f(m - mu), a2 = exp2f(m2 - mu);
+      const float a0 = __builtin_amdgcn_exp2f(m - mu);
+      const float a2 = __builtin_amdgcn_exp2f(m2 - mu);
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          o[cc][e] = o[cc][e] * a0 +
-                     src[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] * a2;
+          st.o[cc][e] = st.o[cc][e] * a0 +
+                        src[(32 * cc + 8 * (e >> 2) + 4 * h + (e & 3)) * 32 + n] * a2;
       lt = lt * a0 + l2 * a2;
       m = mn;
     }
   }
-  const float inv = (q_valid && lt > 0.f) ? 1.f / lt : 0.f;
-  if (q_tensor) {
+  const float inv = (Q.q_valid && lt > 0.f) ? 1.f / lt : 0.f;
+  if (Q.q_tensor) {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         typename M::v4 wv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wv[j] = (E)(o[cc][4 * i + j] * inv);
+        for (int j = 0; j < 4; ++j) wv[j] = (E)(st.o[cc][4 * i + j] * inv);
         *reinterpret_cast<typename M::v4 *>(out + qrow + 32 * cc + 8 * i + 4 * h) = wv;
       }
     if (lse != nullptr && h == 0)
-      lse[qrow / D] = q_valid ? (m + __log2f(lt)) * kLn2 : 0.f;
+      lse[qrow / D] = Q.q_valid ? (m + __log2f(lt)) * kLn2 : 0.f;
   }
 }
 
@@ -559,6 +642,53 @@ __device__ __forceinline__ bool combine_sum(char *smem, int W, int w, int n,
   return true;
 }
 
+// One 32-key chunk of the dQ role: S^T = K.Q^T, dP^T = V.dO^T,
+// dS^T = P^T (dP^T - delta), dQ^T += K^T.dS^T (K^T via LDS).
+template <typename T, int D>
+__device__ __forceinline__ void dq_chunk(f32x16 *acc,
+                                         const typename Mf<T>::v8 *qf,
+                                         const typename Mf<T>::v8 *df,
+                                         const T *kp, const T *vp,
+                                         const bool ok[16], float sl2,
+                                         float lse2, float dl,
+                                         typename Mf<T>::e *ta, int n, int h) {
+  typedef Mf<T> M;
+  typedef typename M::v8 v8;
+  constexpr int NK = D / 16, NC = D / 32;
+  v8 kf[NK], vf[NK];
+#pragma unroll
+  for (int t = 0; t < NK; ++t) {
+    kf[t] = ld8(kp + 16 * t + 8 * h);
+    vf[t] = ld8(vp + 16 * t + 8 * h);
+  }
+  f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+  for (int t = 0; t < NK; ++t) {
+    s = M::mma(kf[t], qf[t], s);
+    dp = M::mma(vf[t], df[t], dp);
+  }
+  float ds[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const float p = ok[e] ? __builtin_amdgcn_exp2f(fmaf(s[e], sl2, -lse2)) : 0.f;
+    ds[e] = p * (dp[e] - dl);
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int t = 0; t < NK; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ta[(16 * t + 8 * h + e) * kRow + n] = kf[t][e];
+  wave_lds_sync();
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc)
+      acc[cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h), bs,
+                       acc[cc]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Backward: blocks [0, n_q) are dQ tiles, [n_q, n_q + n_k) dK/dV tiles.
 template <typename T, int D>
@@ -590,127 +720,51 @@ __global__ void __launch_bounds__(256)
 
   if (tile < Tl.n_q) {
     // ------------------------------- dQ role -------------------------------
-    const TileCtx tc = decode_tile(P, Tl, tile, Tl.fH);
-    const int hk = tc.head / P.rep;
-    int u[3];
-    tile_slot(Tl, n, u);
-    const bool q_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
-    const bool q_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
-    const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
-    int pos[3];
-#pragma unroll
-    for (int a = 0; a < 3; ++a) pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
-    const int64_t qtok = tok_in(P, tc.b, pos[0], pos[1], pos[2]);
-    const int64_t qrow = (qtok * P.H + tc.head) * D;
-
-    Box bx;
-    int wlo[3], ww[3];
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
-      if (any) {
-        sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a], lo0, hi0);
-        sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + tc.nv[a] - 1, lo1, hi1);
-      }
-      bx.lo[a] = lo0;
-      bx.E[a] = any ? hi1 - lo0 : 1;
-      int lo = 0, hi = 0;
-      if (q_valid) sub_window(P, Tl, a, tc.L[a], tc.r[a], tc.i0[a] + u[a], lo, hi);
-      wlo[a] = lo - bx.lo[a];
-      ww[a] = q_valid ? hi - lo : 0;
-    }
-    box_init(bx);
-    const int nbox = any ? (bx.slots + 31) >> 5 : 0;
-    const int nchunk = nbox + (any ? (P.n_extra + 31) >> 5 : 0);
-
+    const QTile Q = query_tile(P, Tl, tile, n);
+    const int hk = Q.tc.head / P.rep;
+    const int64_t qrow = (Q.qtok * P.H + Q.tc.head) * D;
     v8 qf[NK], df[NK];
     float dl = 0.f;
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
-      qf[t] = q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
-      df[t] = q_valid ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
-      const v8 of = q_valid ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
+      qf[t] = Q.q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
+      df[t] = Q.q_valid ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
+      const v8 of = Q.q_valid ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
 #pragma unroll
       for (int e = 0; e < 8; ++e) dl = fmaf((float)df[t][e], (float)of[e], dl);
     }
     dl += __shfl_xor(dl, 32);
-    const int64_t lrow = qtok * P.H + tc.head;
-    if (q_valid && dlse != nullptr) dl -= dlse[lrow];
-    const float lse2 = q_valid ? lse[lrow] * kLog2e : 0.f;
+    const int64_t lrow = Q.qtok * P.H + Q.tc.head;
+    if (Q.q_valid && dlse != nullptr) dl -= dlse[lrow];
+    const float lse2 = Q.q_valid ? lse[lrow] * kLog2e : 0.f;
 
     f32x16 acc[1][NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[0][c] = zero16();
 
+    const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
     RowCursor rc{0, 0, 0};
-    for (int c = w; c < nchunk; c += W) {
-      const bool extra = c >= nbox;
-      if (!extra) cursor_seek(rc, bx, 32 * c);
-      bool kv;
-      const T *kp, *vp;
-      if (!extra) {
-        int e[3];
-        kv = box_point(bx, rc, 32 * c, n, e);
-        int kpos[3];
-#pragma unroll
-        for (int a = 0; a < 3; ++a)
-          kpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
-        const int64_t row =
-            (tok_in(P, tc.b, kpos[0], kpos[1], kpos[2]) * P.Hkv + hk) * D;
-        kp = k + row;
-        vp = v + row;
-      } else {
-        const int ne = 32 * (c - nbox) + n;
-        kv = ne < P.n_extra;
-        const int64_t row =
-            (((int64_t)tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
-        kp = ek + row;
-        vp = ev + row;
-      }
-      v8 kf[NK], vf[NK];
-#pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        kf[t] = kv ? ld8(kp + 16 * t + 8 * h) : zero8<T>();
-        vf[t] = kv ? ld8(vp + 16 * t + 8 * h) : zero8<T>();
-      }
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        s = M::mma(kf[t], qf[t], s);
-        dp = M::mma(vf[t], df[t], dp);
-      }
+    for (int c = w; c < Q.nbox; c += W) {
+      const ChunkRows cr = chunk_rows(rc, Q.bx, 32 * c);
+      int e[3];
+      box_point(Q.bx, cr, 32 * c, n, e);
+      const int off = box_off(ka, e);
       bool ok[16];
-      if (!extra) {
-        chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          ok[e] = q_valid &&
-                  32 * (c - nbox) + 8 * (e >> 2) + 4 * h + (e & 3) < P.n_extra;
-      }
-      float ds[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = ok[e] ? exp2f(fmaf(s[e], sl2, -lse2)) : 0.f;
-        ds[e] = p * (dp[e] - dl);
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int t = 0; t < NK; ++t)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ta[(16 * t + 8 * h + e) * kRow + n] = kf[t][e];
-      wave_lds_sync();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const v8 bs = pack8<T>(ds + 8 * kb);
-#pragma unroll
-        for (int cc = 0; cc < NC; ++cc)
-          acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
-                              bs, acc[0][cc]);
-      }
+      chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
+      dq_chunk<T, D>(acc[0], qf, df, k + ka.base + off, v + ka.base + off, ok,
+                     sl2, lse2, dl, ta, n, h);
+    }
+    for (int c = first_owned(Q.nbox, w, W); c < Q.nbox + Q.nextra; c += W) {
+      const int first = 32 * (c - Q.nbox);
+      const int ne = min(first + n, P.n_extra - 1);
+      const int64_t row = (((int64_t)Q.tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
+      bool ok[16];
+      extra_mask(Q.q_valid, first, P.n_extra, h, ok);
+      dq_chunk<T, D>(acc[0], qf, df, ek + row, ev + row, ok, sl2, lse2, dl, ta,
+                     n, h);
     }
     if (!combine_sum<NC, 1>(smem, W, w, n, h, acc)) return;
-    if (q_tensor) {
+    if (Q.q_tensor) {
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
@@ -718,7 +772,7 @@ __global__ void __launch_bounds__(256)
           typename M::v4 wv;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            wv[j] = (E)(q_valid ? acc[0][cc][4 * i + j] * P.scale : 0.f);
+            wv[j] = (E)(Q.q_valid ? acc[0][cc][4 * i + j] * P.scale : 0.f);
           *reinterpret_cast<typename M::v4 *>(dq + qrow + 32 * cc + 8 * i + 4 * h) = wv;
         }
     }
@@ -730,14 +784,17 @@ __global__ void __launch_bounds__(256)
   const int hk = tc.head;
   int u[3];
   tile_slot(Tl, n, u);
-  const bool k_tensor = u[0] < tc.nt[0] && u[1] < tc.nt[1] && u[2] < tc.nt[2];
-  const bool k_valid = u[0] < tc.nv[0] && u[1] < tc.nv[1] && u[2] < tc.nv[2];
-  const bool any = tc.nv[0] > 0 && tc.nv[1] > 0 && tc.nv[2] > 0;
+  const bool k_tensor = (u[0] < tc.nt[0]) & (u[1] < tc.nt[1]) & (u[2] < tc.nt[2]);
+  const bool k_valid = (u[0] < tc.nv[0]) & (u[1] < tc.nv[1]) & (u[2] < tc.nv[2]);
+  const bool any = (tc.nv[0] > 0) & (tc.nv[1] > 0) & (tc.nv[2] > 0);
   int pos[3], Lr[3];
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     pos[a] = tc.r[a] + P.ax[a].d * (tc.i0[a] + u[a]);
-    Lr[a] = tc.L[a] > tc.r[a] ? (tc.L[a] - 1 - tc.r[a]) / P.ax[a].d + 1 : 0;
+    Lr[a] = P.ax[a].d == 1 ? tc.L[a]
+            : tc.L[a] > tc.r[a]
+                ? (int)fdiv((uint32_t)(tc.L[a] - 1 - tc.r[a]), Tl.fd[a]) + 1
+                : 0;
   }
   const int64_t krow =
       (tok_in(P, tc.b, pos[0], pos[1], pos[2]) * P.Hkv + hk) * D;
@@ -750,11 +807,11 @@ __global__ void __launch_bounds__(256)
     int lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;
     if (any) {
       sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a], lo0, hi0);
-      sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + tc.nv[a] - 1, lo1,
-                  hi1);
+      sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + tc.nv[a] - 1,
+                  lo1, hi1);
     }
-    bx.lo[a] = lo0;
-    bx.E[a] = any ? max(hi1 - lo0 + 1, 1) : 1;
+    bx.lo[a] = uni(lo0);
+    bx.E[a] = uni(any ? max(hi1 - lo0 + 1, 1) : 1);
     int lo = 0, hi = -1;
     if (k_valid)
       sub_inverse(P, Tl, a, tc.L[a], tc.r[a], Lr[a], tc.i0[a] + u[a], lo, hi);
@@ -762,7 +819,8 @@ __global__ void __launch_bounds__(256)
     ww[a] = k_valid ? max(hi - lo + 1, 0) : 0;
   }
   box_init(bx);
-  const int nchunk = any ? (bx.slots + 31) >> 5 : 0;
+  bx.lgP = uni(bx.lgP);
+  const int nchunk = uni(any ? (bx.slots + 31) >> 5 : 0);
 
   v8 kf[NK], vf[NK];
 #pragma unroll
@@ -778,81 +836,80 @@ __global__ void __launch_bounds__(256)
   }
 
   for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
-  RowCursor rc{0, 0, 0};
-  for (int c = w; c < nchunk; c += W) {
-    cursor_seek(rc, bx, 32 * c);
-    int e[3];
-    const bool qv = box_point(bx, rc, 32 * c, n, e);
-    int qpos[3];
+    const BoxAddr qa_addr = box_addr(P, tc, bx, hq, P.H);
+    const int64_t lbase = qa_addr.base / D;  // lse/dlse offset of the box origin
+    RowCursor rc{0, 0, 0};
+    for (int c = w; c < nchunk; c += W) {
+      const ChunkRows cr = chunk_rows(rc, bx, 32 * c);
+      int e[3];
+      box_point(bx, cr, 32 * c, n, e);
+      const int off = box_off(qa_addr, e);
+      const int64_t qrow = qa_addr.base + off;
+      const int64_t lrow = lbase + off / D;
+      // padding slots load a real (clamped) query; the mask removes them
+      v8 qa[NK], da[NK];
+      float dl = 0.f;
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
-      qpos[a] = tc.r[a] + P.ax[a].d * (bx.lo[a] + e[a]);
-    const int64_t qtok = tok_in(P, tc.b, qpos[0], qpos[1], qpos[2]);
-    const int64_t qrow = (qtok * P.H + hq) * D;
-    v8 qa[NK], da[NK];
-    float dl = 0.f;
+      for (int t = 0; t < NK; ++t) {
+        qa[t] = ld8(q + qrow + 16 * t + 8 * h);
+        da[t] = ld8(dout + qrow + 16 * t + 8 * h);
+        const v8 of = ld8(out + qrow + 16 * t + 8 * h);
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      qa[t] = qv ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
-      da[t] = qv ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
-      const v8 of = qv ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
-    }
-    dl += __shfl_xor(dl, 32);
-    const int64_t lrow = qtok * P.H + hq;
-    if (qv && dlse != nullptr) dl -= dlse[lrow];
-    const float l2 = qv ? lse[lrow] * kLog2e : 0.f;
+        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
+      }
+      dl += __shfl_xor(dl, 32);
+      if (dlse != nullptr) dl -= dlse[lrow];
+      const float l2 = lse[lrow] * kLog2e;
 
-    wave_lds_sync();
+      wave_lds_sync();
 #pragma unroll
-    for (int t = 0; t < NK; ++t)
+      for (int t = 0; t < NK; ++t)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
-        tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+        for (int i = 0; i < 8; ++i) {
+          ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
+          tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+        }
+      if (h == 0) {
+        s_lse[n] = l2;
+        s_del[n] = dl;
       }
-    if (h == 0) {
-      s_lse[n] = l2;
-      s_del[n] = dl;
-    }
-    wave_lds_sync();
+      wave_lds_sync();
 
-    f32x16 s = zero16(), dp = zero16();
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      s = M::mma(qa[t], kf[t], s);
-      dp = M::mma(da[t], vf[t], dp);
-    }
-    bool ok[16];
-    chunk_mask(bx, rc, 32 * c, h, wlo, ww, ok);
-    float p[16], ds[16];
+      for (int t = 0; t < NK; ++t) {
+        s = M::mma(qa[t], kf[t], s);
+        dp = M::mma(da[t], vf[t], dp);
+      }
+      bool ok[16];
+      chunk_mask(bx, cr, 32 * c, h, wlo, ww, ok);
+      float p[16], ds[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
-      const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
-      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+      for (int i = 0; i < 4; ++i) {
+        const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
+        const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e2 = 4 * i + j;
-        p[e2] = ok[e2] ? exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
-        ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+        for (int j = 0; j < 4; ++j) {
+          const int e2 = 4 * i + j;
+          p[e2] = ok[e2] ? __builtin_amdgcn_exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
+          ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const v8 bp = pack8<T>(p + 8 * kb);
+        const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h),
+                              bp, acc[1][cc]);
+          acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
+                              bs, acc[0][cc]);
+        }
       }
     }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const v8 bp = pack8<T>(p + 8 * kb);
-      const v8 bs = pack8<T>(ds + 8 * kb);
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h), bp,
-                            acc[1][cc]);
-        acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h), bs,
-                            acc[0][cc]);
-      }
-    }
-  }
   }
   if (!combine_sum<NC, 2>(smem, W, w, n, h, acc)) return;
   if (k_tensor) {
