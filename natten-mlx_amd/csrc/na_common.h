@@ -165,6 +165,7 @@ struct Tiling {
   FastDiv fnt[3];     // per-axis tiles per phase
   FastDiv fd[3];      // per-axis dilation
   FastDiv fH, fHk;    // query heads, key/value heads
+  FastDiv fRep1;      // query heads per key/value head, plus one
 };
 
 // Extents of sample b (varlen aware).

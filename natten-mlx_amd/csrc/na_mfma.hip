@@ -384,23 +384,32 @@ struct Softmax {
   float m, l;
 };
 
-// One 32-key chunk of the forward: S^T = K.Q^T, masked online softmax,
-// O^T += V^T.P^T (V^T staged through this wave's LDS buffer).
+// Load the K and V rows of one chunk (A-operand layout: lane (key, h)
+// holds elements 16t + 8h .. 16t + 8h + 7).
 template <typename T, int D>
-__device__ __forceinline__ void fwd_chunk(Softmax<D / 32> &st,
-                                          const typename Mf<T>::v8 *qf,
-                                          const T *kp, const T *vp,
-                                          const bool ok[16], float sl2,
-                                          typename Mf<T>::e *vt, int n, int h) {
-  typedef Mf<T> M;
-  typedef typename M::v8 v8;
-  constexpr int NK = D / 16, NC = D / 32;
-  v8 kf[NK], vf[NK];
+__device__ __forceinline__ void load_kv(const T *kp, const T *vp,
+                                        typename Mf<T>::v8 *kf,
+                                        typename Mf<T>::v8 *vf, int h) {
 #pragma unroll
-  for (int t = 0; t < NK; ++t) {
+  for (int t = 0; t < D / 16; ++t) {
     kf[t] = ld8(kp + 16 * t + 8 * h);
     vf[t] = ld8(vp + 16 * t + 8 * h);
   }
+}
+
+// One 32-key chunk of the forward: S^T = K.Q^T, masked online softmax,
+// O^T += V^T.P^T (V^T staged through this wave's LDS buffer).
+template <typename T, int D>
+__device__ __forceinline__ void fwd_compute(Softmax<D / 32> &st,
+                                            const typename Mf<T>::v8 *qf,
+                                            const typename Mf<T>::v8 *kf,
+                                            const typename Mf<T>::v8 *vf,
+                                            const bool ok[16], float sl2,
+                                            typename Mf<T>::e *vt, int n,
+                                            int h) {
+  typedef Mf<T> M;
+  typedef typename M::v8 v8;
+  constexpr int NK = D / 16, NC = D / 32;
   f32x16 s = zero16();
 #pragma unroll
   for (int t = 0; t < NK; ++t) s = M::mma(kf[t], qf[t], s);
@@ -455,9 +464,9 @@ struct QTile {
 };
 
 __device__ __forceinline__ QTile query_tile(const Prob &P, const Tiling &Tl,
-                                            int tile, int n) {
+                                            const TileCtx &tc0, int n) {
   QTile Q;
-  Q.tc = decode_tile(P, Tl, tile, Tl.fH);
+  Q.tc = tc0;
   const TileCtx &tc = Q.tc;
   int u[3];
   tile_slot(Tl, n, u);
@@ -517,7 +526,7 @@ __global__ void __launch_bounds__(256)
   const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
   E *vt = reinterpret_cast<E *>(smem) + w * D * kRow;
-  const QTile Q = query_tile(P, Tl, tile, n);
+  const QTile Q = query_tile(P, Tl, decode_tile(P, Tl, tile, Tl.fH), n);
   const int hk = Q.tc.head / P.rep;
   const float sl2 = P.scale * kLog2e;
   const int64_t qrow = (Q.qtok * P.H + Q.tc.head) * D;
@@ -533,25 +542,50 @@ __global__ void __launch_bounds__(256)
   st.m = -INFINITY;
   st.l = 0.f;
 
+  // box chunks, software-pipelined: the next chunk's K/V loads are in
+  // flight while the current chunk computes
   const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
   RowCursor rc{0, 0, 0};
-  for (int c = w; c < Q.nbox; c += W) {
-    const ChunkRows cr = chunk_rows(rc, Q.bx, 32 * c);
+  int c = w;
+  ChunkRows cr{0, 0, 0};
+  v8 kf[NK], vf[NK];
+  if (c < Q.nbox) {
+    cr = chunk_rows(rc, Q.bx, 32 * c);
     int e[3];
     box_point(Q.bx, cr, 32 * c, n, e);
     const int off = box_off(ka, e);
+    load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
+  }
+  while (c < Q.nbox) {
+    const int cn = c + W;
+    ChunkRows crn = cr;
+    v8 kn[NK], vn[NK];
+    if (cn < Q.nbox) {
+      crn = chunk_rows(rc, Q.bx, 32 * cn);
+      int e[3];
+      box_point(Q.bx, crn, 32 * cn, n, e);
+      const int off = box_off(ka, e);
+      load_kv<T, D>(k + ka.base + off, v + ka.base + off, kn, vn, h);
+    }
     bool ok[16];
     chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
-    fwd_chunk<T, D>(st, qf, k + ka.base + off, v + ka.base + off, ok, sl2, vt,
-                    n, h);
+    fwd_compute<T, D>(st, qf, kf, vf, ok, sl2, vt, n, h);
+    c = cn;
+    cr = crn;
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      kf[t] = kn[t];
+      vf[t] = vn[t];
+    }
   }
-  for (int c = first_owned(Q.nbox, w, W); c < Q.nbox + Q.nextra; c += W) {
-    const int first = 32 * (c - Q.nbox);
+  for (int cx = first_owned(Q.nbox, w, W); cx < Q.nbox + Q.nextra; cx += W) {
+    const int first = 32 * (cx - Q.nbox);
     const int ne = min(first + n, P.n_extra - 1);
     const int64_t row = (((int64_t)Q.tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
     bool ok[16];
     extra_mask(Q.q_valid, first, P.n_extra, h, ok);
-    fwd_chunk<T, D>(st, qf, ek + row, ev + row, ok, sl2, vt, n, h);
+    load_kv<T, D>(ek + row, ev + row, kf, vf, h);
+    fwd_compute<T, D>(st, qf, kf, vf, ok, sl2, vt, n, h);
   }
 
   float lt = st.l + __shfl_xor(st.l, 32);
@@ -645,22 +679,18 @@ __device__ __forceinline__ bool combine_sum(char *smem, int W, int w, int n,
 // One 32-key chunk of the dQ role: S^T = K.Q^T, dP^T = V.dO^T,
 // dS^T = P^T (dP^T - delta), dQ^T += K^T.dS^T (K^T via LDS).
 template <typename T, int D>
-__device__ __forceinline__ void dq_chunk(f32x16 *acc,
-                                         const typename Mf<T>::v8 *qf,
-                                         const typename Mf<T>::v8 *df,
-                                         const T *kp, const T *vp,
-                                         const bool ok[16], float sl2,
-                                         float lse2, float dl,
-                                         typename Mf<T>::e *ta, int n, int h) {
+__device__ __forceinline__ void dq_compute(f32x16 *acc,
+                                           const typename Mf<T>::v8 *qf,
+                                           const typename Mf<T>::v8 *df,
+                                           const typename Mf<T>::v8 *kf,
+                                           const typename Mf<T>::v8 *vf,
+                                           const bool ok[16], float sl2,
+                                           float lse2, float dl,
+                                           typename Mf<T>::e *ta, int n,
+                                           int h) {
   typedef Mf<T> M;
   typedef typename M::v8 v8;
   constexpr int NK = D / 16, NC = D / 32;
-  v8 kf[NK], vf[NK];
-#pragma unroll
-  for (int t = 0; t < NK; ++t) {
-    kf[t] = ld8(kp + 16 * t + 8 * h);
-    vf[t] = ld8(vp + 16 * t + 8 * h);
-  }
   f32x16 s = zero16(), dp = zero16();
 #pragma unroll
   for (int t = 0; t < NK; ++t) {
@@ -710,6 +740,12 @@ __global__ void __launch_bounds__(256)
   if (tile >= Tl.n_q + Tl.n_k) return;
   const int W = blockDim.x >> 6, w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
+  // Tiles come in groups of rep + 1 over one spatial tile of one KV head:
+  // rep dQ tiles (one per query head of the group), then the dK/dV tile,
+  // so both roles spread evenly over the XCDs and share the group's data.
+  const uint32_t grp = fdiv((uint32_t)tile, Tl.fRep1);
+  const int role = tile - (int)grp * (P.rep + 1);
+  TileCtx tcg = decode_tile(P, Tl, (int)grp, Tl.fHk);
   // per-wave scratch: two transposed chunks + per-query lse / delta
   char *mys = smem + w * (2 * D * kRow * (int)sizeof(E) + 256);
   E *ta = reinterpret_cast<E *>(mys);                 // K^T (dQ) or Q^T (dK/dV)
@@ -718,10 +754,11 @@ __global__ void __launch_bounds__(256)
   float *s_del = s_lse + 32;
   const float sl2 = P.scale * kLog2e;
 
-  if (tile < Tl.n_q) {
+  if (role < P.rep) {
     // ------------------------------- dQ role -------------------------------
-    const QTile Q = query_tile(P, Tl, tile, n);
-    const int hk = Q.tc.head / P.rep;
+    const int hk = tcg.head;
+    tcg.head = hk * P.rep + role;
+    const QTile Q = query_tile(P, Tl, tcg, n);
     const int64_t qrow = (Q.qtok * P.H + Q.tc.head) * D;
     v8 qf[NK], df[NK];
     float dl = 0.f;
@@ -744,24 +781,46 @@ __global__ void __launch_bounds__(256)
 
     const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
     RowCursor rc{0, 0, 0};
-    for (int c = w; c < Q.nbox; c += W) {
-      const ChunkRows cr = chunk_rows(rc, Q.bx, 32 * c);
+    int c = w;
+    ChunkRows cr{0, 0, 0};
+    v8 kf[NK], vf[NK];
+    if (c < Q.nbox) {
+      cr = chunk_rows(rc, Q.bx, 32 * c);
       int e[3];
       box_point(Q.bx, cr, 32 * c, n, e);
       const int off = box_off(ka, e);
+      load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
+    }
+    while (c < Q.nbox) {
+      const int cn = c + W;
+      ChunkRows crn = cr;
+      v8 kn[NK], vn[NK];
+      if (cn < Q.nbox) {
+        crn = chunk_rows(rc, Q.bx, 32 * cn);
+        int e[3];
+        box_point(Q.bx, crn, 32 * cn, n, e);
+        const int off = box_off(ka, e);
+        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kn, vn, h);
+      }
       bool ok[16];
       chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
-      dq_chunk<T, D>(acc[0], qf, df, k + ka.base + off, v + ka.base + off, ok,
-                     sl2, lse2, dl, ta, n, h);
+      dq_compute<T, D>(acc[0], qf, df, kf, vf, ok, sl2, lse2, dl, ta, n, h);
+      c = cn;
+      cr = crn;
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        kf[t] = kn[t];
+        vf[t] = vn[t];
+      }
     }
-    for (int c = first_owned(Q.nbox, w, W); c < Q.nbox + Q.nextra; c += W) {
-      const int first = 32 * (c - Q.nbox);
+    for (int cx = first_owned(Q.nbox, w, W); cx < Q.nbox + Q.nextra; cx += W) {
+      const int first = 32 * (cx - Q.nbox);
       const int ne = min(first + n, P.n_extra - 1);
       const int64_t row = (((int64_t)Q.tc.b * P.n_extra + ne) * P.Hkv + hk) * D;
       bool ok[16];
       extra_mask(Q.q_valid, first, P.n_extra, h, ok);
-      dq_chunk<T, D>(acc[0], qf, df, ek + row, ev + row, ok, sl2, lse2, dl, ta,
-                     n, h);
+      load_kv<T, D>(ek + row, ev + row, kf, vf, h);
+      dq_compute<T, D>(acc[0], qf, df, kf, vf, ok, sl2, lse2, dl, ta, n, h);
     }
     if (!combine_sum<NC, 1>(smem, W, w, n, h, acc)) return;
     if (Q.q_tensor) {
@@ -780,7 +839,7 @@ __global__ void __launch_bounds__(256)
   }
 
   // ------------------------------ dK/dV role -------------------------------
-  const TileCtx tc = decode_tile(P, Tl, tile - Tl.n_q, Tl.fHk);
+  const TileCtx tc = tcg;
   const int hk = tc.head;
   int u[3];
   tile_slot(Tl, n, u);
@@ -838,28 +897,58 @@ __global__ void __launch_bounds__(256)
   for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
     const BoxAddr qa_addr = box_addr(P, tc, bx, hq, P.H);
     const int64_t lbase = qa_addr.base / D;  // lse/dlse offset of the box origin
+    // query chunks, software-pipelined like the forward; padding slots
+    // load a real (clamped) query and the mask removes them
     RowCursor rc{0, 0, 0};
-    for (int c = w; c < nchunk; c += W) {
-      const ChunkRows cr = chunk_rows(rc, bx, 32 * c);
+    int c = w;
+    ChunkRows cr{0, 0, 0};
+    v8 qa[NK], da[NK], oa[NK];
+    float lsev = 0.f, dlsev = 0.f;
+    if (c < nchunk) {
+      cr = chunk_rows(rc, bx, 32 * c);
       int e[3];
       box_point(bx, cr, 32 * c, n, e);
       const int off = box_off(qa_addr, e);
       const int64_t qrow = qa_addr.base + off;
       const int64_t lrow = lbase + off / D;
-      // padding slots load a real (clamped) query; the mask removes them
-      v8 qa[NK], da[NK];
-      float dl = 0.f;
 #pragma unroll
       for (int t = 0; t < NK; ++t) {
         qa[t] = ld8(q + qrow + 16 * t + 8 * h);
         da[t] = ld8(dout + qrow + 16 * t + 8 * h);
-        const v8 of = ld8(out + qrow + 16 * t + 8 * h);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)of[i], dl);
+        oa[t] = ld8(out + qrow + 16 * t + 8 * h);
       }
+      lsev = lse[lrow];
+      dlsev = dlse != nullptr ? dlse[lrow] : 0.f;
+    }
+    while (c < nchunk) {
+      const int cn = c + W;
+      ChunkRows crn = cr;
+      v8 qn[NK], dn[NK], on[NK];
+      float lsen = 0.f, dlsen = 0.f;
+      if (cn < nchunk) {
+        crn = chunk_rows(rc, bx, 32 * cn);
+        int e[3];
+        box_point(bx, crn, 32 * cn, n, e);
+        const int off = box_off(qa_addr, e);
+        const int64_t qrow = qa_addr.base + off;
+        const int64_t lrow = lbase + off / D;
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+          qn[t] = ld8(q + qrow + 16 * t + 8 * h);
+          dn[t] = ld8(dout + qrow + 16 * t + 8 * h);
+          on[t] = ld8(out + qrow + 16 * t + 8 * h);
+        }
+        lsen = lse[lrow];
+        dlsen = dlse != nullptr ? dlse[lrow] : 0.f;
+      }
+      float dl = 0.f;
+#pragma unroll
+      for (int t = 0; t < NK; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)oa[t][i], dl);
       dl += __shfl_xor(dl, 32);
-      if (dlse != nullptr) dl -= dlse[lrow];
-      const float l2 = lse[lrow] * kLog2e;
+      dl -= dlsev;
+      const float l2 = lsev * kLog2e;
 
       wave_lds_sync();
 #pragma unroll
@@ -908,6 +997,16 @@ __global__ void __launch_bounds__(256)
           acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
                               bs, acc[0][cc]);
         }
+      }
+      c = cn;
+      cr = crn;
+      lsev = lsen;
+      dlsev = dlsen;
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        qa[t] = qn[t];
+        da[t] = dn[t];
+        oa[t] = on[t];
       }
     }
   }
@@ -994,6 +1093,7 @@ Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv, double *chunks) {
   }
   best.fH = make_fastdiv((uint32_t)heads_q);
   best.fHk = make_fastdiv((uint32_t)heads_kv);
+  best.fRep1 = make_fastdiv((uint32_t)(heads_q / heads_kv + 1));
   return best;
 }
 
