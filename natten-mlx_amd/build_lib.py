@@ -53,9 +53,18 @@ def sources() -> list[str]:
     )
 
 
+# Per-file extra flags.  The matrix-core kernels keep MFMA accumulators in
+# ordinary VGPRs (gfx950 allows it), which removes the AGPR<->VGPR copies
+# their softmax arithmetic would otherwise need.
+EXTRA_FLAGS = {
+    "na_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src,
+           "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -23,6 +23,7 @@
 //                            dV^T += dO^T . P,  dK^T += Q^T . dS
 // delta = rowsum(dO * O) - dlse is recomputed per query from O and dO.
 #include <cmath>
+#include <cstdlib>
 
 #include "na_common.h"
 #include "na_launch.h"
@@ -1098,9 +1099,14 @@ Tiling choose_tiling(const Prob &P, int heads_q, int heads_kv, double *chunks) {
 }
 
 // Waves per tile: one per ~6 chunks, at most `cap` (2 for the backward at
-// head_dim 128, to stay within 64 KB of LDS).
-int waves_for(double chunks, int cap) {
-  const int w = (int)std::ceil(chunks / 6.0);
+// head_dim 128, to stay within 64 KB of LDS).  NATTEN_AMD_FWD_WAVES /
+// NATTEN_AMD_BWD_WAVES override the choice (tuning aid; still capped).
+int waves_for(double chunks, int cap, const char *env) {
+  int w = (int)std::ceil(chunks / 6.0);
+  if (const char *o = std::getenv(env)) {
+    const int v = std::atoi(o);
+    if (v > 0) w = v;
+  }
   return max(1, min(w, cap));
 }
 
@@ -1147,7 +1153,7 @@ void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
   Tiling Tl = choose_tiling(P, P.H, P.Hkv, &chunks);
   Tl.n_launch = (Tl.n_q + 7) & ~7;
   if (Tl.n_q == 0) return;
-  const int W = waves_for(chunks, 4);
+  const int W = waves_for(chunks, 4, "NATTEN_AMD_FWD_WAVES");
   const size_t lds = fwd_lds(P.D, W, 2);
 #define FWD_(DD)                                                             \
   if (dtype == NA_BF16)                                                      \
@@ -1172,7 +1178,7 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
   Tiling Tl = choose_tiling(P, P.H, P.Hkv, &chunks);
   Tl.n_launch = (Tl.n_q + Tl.n_k + 7) & ~7;
   if (Tl.n_q + Tl.n_k == 0) return;
-  const int W = waves_for(chunks * P.rep, P.D >= 128 ? 2 : 4);
+  const int W = waves_for(chunks * P.rep, P.D >= 128 ? 2 : 4, "NATTEN_AMD_BWD_WAVES");
   const size_t lds = bwd_lds(P.D, W, 2);
 #define BWD_(DD)                                                               \
   if (dtype == NA_BF16)                                                        \
