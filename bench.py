@@ -167,6 +167,19 @@ def time_calls(fn, steps: int, reps: int = 20) -> float:
     return total / (n * reps)
 
 
+def profile_calls(n: int) -> None:
+    from natten_amd._core import hip
+
+    q, k, v, do = make_inputs(torch.device("cuda:0"))
+    a = ((K, K), (1, 1), (1, 1), (False, False), None)
+    out, lse = hip.fused_forward(q, k, v, *a)
+    for _ in range(n):
+        hip.fused_forward(q, k, v, *a)
+        hip.fused_backward(q, k, v, out, lse, do, None, *a)
+    torch.cuda.synchronize()
+    print(f"profile-calls: {n} forward + {n} backward calls done", flush=True)
+
+
 def run_cpu_baseline():
     """Oracle fwd+bwd in bf16 on a bounded sample: one of the B=4 images."""
     from oracle import na as O
@@ -202,6 +215,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-calls", type=int, default=0, metavar="N",
+                    help="only run N fused forward and N fused backward calls at the "
+                         "dilation-1 workload (for rocprofv3 --pmc passes), then exit")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -212,6 +228,9 @@ def main(argv=None):
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
 
+    if args.profile_calls > 0:
+        profile_calls(args.profile_calls)
+        return 0
     res = run_gpu(args)
     fwd_f, bwd_f, fwd_b, bwd_b = algorithmic(K * K)
     r1 = res[1]

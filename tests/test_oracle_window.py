@@ -97,3 +97,51 @@ def test_neighbor_table_matches_axis_loops(spatial, ks, dil, caus, st):
             assert valid[o][n] == ok
             if ok:
                 assert lin[o][n] == np.ravel_multi_index(combo, spatial)
+
+
+def _phase_windows(L, K, d, r):
+    """Sub-grid windows [lo, hi) of every query of phase r (oracle rule)."""
+    out = []
+    for p in range(r, L, d):
+        s = W.window_start(p, L, K, K // 2, d)
+        e = W.window_end(s, L, K, d)
+        keys = [x for x in (s + k * d for k in range(K)) if 0 <= x < e]
+        out.append(((min(keys) - r) // d, (max(keys) - r) // d + 1))
+    return out
+
+
+def test_odd_k_windows_monotone_and_inverse_contiguous():
+    """The MFMA backward tiles keys by phase and gathers, per key, the
+    queries whose windows contain it as one contiguous run; that needs
+    window bounds non-decreasing in the query for odd K (any dilation,
+    including d*K > L as varlen allows)."""
+    for L in range(1, 44):
+        for K in range(1, L + 1, 2):
+            for d in range(1, L + 1):
+                if d > 8 and d * K > L + 8:
+                    break
+                for r in range(min(d, L)):
+                    wins = _phase_windows(L, K, d, r)
+                    los = [w[0] for w in wins]
+                    his = [w[1] for w in wins]
+                    assert los == sorted(los) and his == sorted(his)
+                    for j in range(len(wins)):
+                        inv = [i for i, (lo, hi) in enumerate(wins) if lo <= j < hi]
+                        assert inv and inv == list(range(inv[0], inv[-1] + 1))
+
+
+def test_inverse_range_closed_form():
+    """Closed form the MFMA backward uses when d*K <= L (odd K): the queries
+    of sub-grid key j are [0 if j <= K-1 else j - K//2,
+    Lr-1 if j >= Lr-K else j + K//2]."""
+    for L in range(1, 60):
+        for K in range(1, L + 1, 2):
+            for d in range(1, L // K + 1):
+                for r in range(d):
+                    wins = _phase_windows(L, K, d, r)
+                    Lr = len(wins)
+                    for j in range(Lr):
+                        inv = [i for i, (lo, hi) in enumerate(wins) if lo <= j < hi]
+                        qlo = 0 if j <= K - 1 else j - K // 2
+                        qhi = Lr - 1 if j >= Lr - K else j + K // 2
+                        assert inv == list(range(qlo, qhi + 1)), (L, K, d, r, j)
