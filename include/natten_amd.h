@@ -165,30 +165,70 @@ int na_qk_bwd(const na_params *p, const void *q, const void *k,
 int na_av_bwd(const na_params *p, const void *attn, const void *v,
               const void *dout, void *dattn, void *dv, void *stream);
 
-/* ---- DiNAT all-in-one 1D operators (extras/allin1) ----------------------- */
+/* ---- DiNAT all-in-one operators (extras/allin1) -------------------------- */
 /*
- * logits[b,i,h,k] = <q[b,i,h] * scale, key[b, n_i + k*dilation, h]>
- *                   + rpb[h, pb_i + k]        (-inf outside the window)
- * q, key: [B, L, H, D] in `dtype`; rpb: float32 [H, 2K-1] or NULL (zeros);
- * logits: float32 [B, L, H, K].  has_scale = 0 skips the scaling, matching
- * scale=None.  Replaces extras/allin1/__init__.py:40-79 and
- * functional_metal.py:1921-1976.
+ * Square window of side `kernel` with one dilation on every axis, rank 1
+ * ([B, L, H, X]) or rank 2 ([B, Hh, Hw, H, X]); heads_first = 1 selects the
+ * [B, H, L, X] / [B, H, Hh, Hw, X] layout of the lower-level
+ * natten{1,2}d* functions.  Windows use the dilation-partition start; slot
+ * (k0, k1) is n = k0*K + k1; the bias row of slot k on an axis is
+ * clip(pb_start + k, 0, 2K-2).  rpb: float32 [H, 2K-1] (rank 1) or
+ * [H, 2K-1, 2K-1] (rank 2).
  */
-int na1d_qk_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
-                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
-                    float scale, int32_t has_scale, int32_t dtype,
-                    const void *q, const void *key, const float *rpb,
-                    float *logits, void *stream);
+typedef struct na_rpb_params {
+  int32_t rank;        /* 1 or 2 */
+  int32_t batch;
+  int32_t heads;
+  int32_t head_dim;
+  int32_t extent[2];   /* L, or (Hh, Hw) */
+  int32_t kernel;      /* K */
+  int32_t dilation;
+  int32_t heads_first; /* 0: spatial-first rows, 1: heads-first rows */
+  int32_t dtype;       /* q / key / value and their gradients */
+  float scale;         /* query scale, applied in `dtype` before the dot */
+  int32_t has_scale;   /* 0: no scaling (scale=None) */
+} na_rpb_params;
+
 /*
- * out[b,i,h,:] = sum_k attn[b,i,h,k] * value[b, n_i + k*dilation, h, :]
- * attn: float32 [B, L, H, K]; value [B, L, H, D] in `dtype`;
- * out: float32 [B, L, H, D].  Replaces extras/allin1/__init__.py:82-109 and
- * functional_metal.py:1979-2033.
+ * logits[.., n] = <round(q * scale), key_nbr(n)> + rpb[h, bias rows of n],
+ * -inf for invalid slots; logits float32 with K^rank slots per row.
+ * rpb may be NULL (zero bias).  Replaces extras/allin1/__init__.py:40-79
+ * (na1d_qk_rpb), :112-150 (na2d_qk_rpb); functional_metal.py:1125-1161,
+ * 1921-1976.
  */
-int na1d_av_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
-                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
-                    int32_t dtype, const float *attn, const void *value,
-                    float *out, void *stream);
+int na_rpb_qk_fwd(const na_rpb_params *p, const void *q, const void *key,
+                  const float *rpb, float *logits, void *stream);
+/*
+ * out = sum over valid slots attn * value_nbr; attn float32; out in
+ * out_dtype (NA_F32 as the reference's Metal kernels, or p->dtype as its
+ * MLX fallback).  Replaces extras/allin1/__init__.py:82-109 (na1d_av_fused),
+ * :153-180 (na2d_av_fused); functional_metal.py:1164-1199, 1979-2033.
+ */
+int na_rpb_av_fwd(const na_rpb_params *p, const float *attn, const void *value,
+                  void *out, int32_t out_dtype, void *stream);
+/* Workspace na_rpb_qk_bwd needs when drpb is requested. */
+size_t na_rpb_bwd_workspace_bytes(const na_rpb_params *p);
+/*
+ * Gradients of na_rpb_qk_fwd: dq = scale * sum dlogits * key_nbr,
+ * dk[j] = sum over queries holding j of dlogits * round(q * scale),
+ * drpb[h, r] = sum of dlogits over the slots whose bias row is r (float32,
+ * deterministic).  Any of dq / dk / drpb may be NULL (not computed).
+ * Replaces functional_metal.py:1206-1338 (natten1dqkrpb_backward),
+ * 1418-1590 (natten2dqkrpb_backward), 2172-2192, 2216-2244.
+ */
+int na_rpb_qk_bwd(const na_rpb_params *p, const void *q, const void *key,
+                  const float *dlogits, void *dq, void *dk, float *drpb,
+                  void *workspace, size_t workspace_bytes, void *stream);
+/*
+ * Gradients of na_rpb_av_fwd: dattn = <dout, value_nbr> (0 for invalid
+ * slots, float32), dvalue[j] = sum over queries holding j of attn * dout.
+ * dout has out_dtype.  Either output may be NULL.  Replaces
+ * functional_metal.py:1340-1415 (natten1dav_backward), 1592-1918
+ * (natten2dav_backward), 2195-2213, 2247-2274.
+ */
+int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,
+                  const void *dout, int32_t out_dtype, float *dattn,
+                  void *dvalue, void *stream);
 
 #ifdef __cplusplus
 }

@@ -123,6 +123,56 @@ size_t delta_bytes(const na::Prob &P) {
                   P.ax[2].O * P.H);
 }
 
+// Validate the all-in-one parameters and build the device problem.
+int make_rpb(const na_rpb_params *p, na::RpbProb *A) {
+  if (p == nullptr) return fail(NA_ERR_INVALID, "params is NULL");
+  if (p->rank != 1 && p->rank != 2)
+    return fail(NA_ERR_INVALID, "allin1 rank must be 1 or 2, got %d", p->rank);
+  if (p->batch < 0 || p->heads < 1 || p->head_dim < 1)
+    return fail(NA_ERR_INVALID,
+                "batch/heads/head_dim must be positive (got %d/%d/%d)",
+                p->batch, p->heads, p->head_dim);
+  if (p->dtype != NA_F32 && p->dtype != NA_F16 && p->dtype != NA_BF16)
+    return fail(NA_ERR_INVALID, "unknown dtype %d", p->dtype);
+  if ((p->head_dim % 8 != 0 && p->head_dim > 128) ||
+      p->head_dim > kMaxHeadDim)
+    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported",
+                p->head_dim);
+  if (p->kernel < 1 || p->dilation < 1)
+    return fail(NA_ERR_INVALID, "kernel and dilation must be positive");
+  const int32_t L1 = p->rank == 2 ? p->extent[1] : 1;
+  if (p->extent[0] < 1 || L1 < 1)
+    return fail(NA_ERR_INVALID, "extents must be positive");
+  const int64_t kk = p->rank == 2 ? (int64_t)p->kernel * p->kernel : p->kernel;
+  const int64_t rows = (int64_t)p->batch * p->heads * p->extent[0] * L1;
+  if (rows >= ((int64_t)1 << 31) || kk >= ((int64_t)1 << 20))
+    return fail(NA_ERR_UNSUPPORTED, "allin1 problem too large");
+  A->rank = p->rank;
+  A->B = p->batch;
+  A->H = p->heads;
+  A->D = p->head_dim;
+  A->K = p->kernel;
+  A->dil = p->dilation;
+  A->L0 = p->extent[0];
+  A->L1 = L1;
+  A->K1 = p->rank == 2 ? p->kernel : 1;
+  A->KK = (int32_t)kk;
+  A->R = 2 * p->kernel - 1;
+  A->heads_first = p->heads_first ? 1 : 0;
+  A->has_scale = p->has_scale ? 1 : 0;
+  A->scale = p->scale;
+  A->n_rows = (int32_t)rows;
+  return NA_OK;
+}
+
+int check_out_dtype(const na_rpb_params *p, int32_t out_dtype) {
+  if (out_dtype != NA_F32 && out_dtype != p->dtype)
+    return fail(NA_ERR_INVALID,
+                "out_dtype must be NA_F32 or the input dtype (got %d)",
+                out_dtype);
+  return NA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -291,43 +341,78 @@ int na_av_bwd(const na_params *p, const void *attn, const void *v,
   return launch_status("na_av_bwd");
 }
 
-int na1d_qk_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
-                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
-                    float scale, int32_t has_scale, int32_t dtype,
-                    const void *q, const void *key, const float *rpb,
-                    float *logits, void *stream) {
-  if (batch < 0 || length < 1 || heads < 1 || head_dim < 1 ||
-      kernel_size < 1 || dilation < 1)
-    return fail(NA_ERR_INVALID, "invalid 1D QK+RPB shape");
-  if (head_dim > kMaxHeadDim || (head_dim % 8 != 0 && head_dim > 128))
-    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported", head_dim);
-  if (dtype != NA_F32 && dtype != NA_F16 && dtype != NA_BF16)
-    return fail(NA_ERR_INVALID, "unknown dtype %d", dtype);
-  if (batch == 0) return NA_OK;
+int na_rpb_qk_fwd(const na_rpb_params *p, const void *q, const void *key,
+                  const float *rpb, float *logits, void *stream) {
+  na::RpbProb A;
+  const int rc = make_rpb(p, &A);
+  if (rc != NA_OK) return rc;
+  if (A.n_rows == 0) return NA_OK;
   if (q == nullptr || key == nullptr || logits == nullptr)
     return fail(NA_ERR_INVALID, "q/key/logits must be non-NULL");
-  na::valu_qk_rpb(batch, length, heads, head_dim, kernel_size, dilation, scale,
-                  has_scale, dtype, q, key, rpb, logits, as_stream(stream));
-  return launch_status("na1d_qk_rpb_fwd");
+  na::rpb_qk_fwd(A, p->dtype, q, key, rpb, logits, as_stream(stream));
+  return launch_status("na_rpb_qk_fwd");
 }
 
-int na1d_av_rpb_fwd(int32_t batch, int32_t length, int32_t heads,
-                    int32_t head_dim, int32_t kernel_size, int32_t dilation,
-                    int32_t dtype, const float *attn, const void *value,
-                    float *out, void *stream) {
-  if (batch < 0 || length < 1 || heads < 1 || head_dim < 1 ||
-      kernel_size < 1 || dilation < 1)
-    return fail(NA_ERR_INVALID, "invalid 1D AV shape");
-  if (head_dim > kMaxHeadDim || (head_dim % 8 != 0 && head_dim > 128))
-    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported", head_dim);
-  if (dtype != NA_F32 && dtype != NA_F16 && dtype != NA_BF16)
-    return fail(NA_ERR_INVALID, "unknown dtype %d", dtype);
-  if (batch == 0) return NA_OK;
+int na_rpb_av_fwd(const na_rpb_params *p, const float *attn, const void *value,
+                  void *out, int32_t out_dtype, void *stream) {
+  na::RpbProb A;
+  int rc = make_rpb(p, &A);
+  if (rc != NA_OK) return rc;
+  rc = check_out_dtype(p, out_dtype);
+  if (rc != NA_OK) return rc;
+  if (A.n_rows == 0) return NA_OK;
   if (attn == nullptr || value == nullptr || out == nullptr)
     return fail(NA_ERR_INVALID, "attn/value/out must be non-NULL");
-  na::valu_av_rpb(batch, length, heads, head_dim, kernel_size, dilation,
-                  dtype, attn, value, out, as_stream(stream));
-  return launch_status("na1d_av_rpb_fwd");
+  na::rpb_av_fwd(A, p->dtype, out_dtype, attn, value, out, as_stream(stream));
+  return launch_status("na_rpb_av_fwd");
+}
+
+size_t na_rpb_bwd_workspace_bytes(const na_rpb_params *p) {
+  na::RpbProb A;
+  if (make_rpb(p, &A) != NA_OK) return 0;
+  return align256(na::rpb_bias_workspace_bytes(A));
+}
+
+int na_rpb_qk_bwd(const na_rpb_params *p, const void *q, const void *key,
+                  const float *dlogits, void *dq, void *dk, float *drpb,
+                  void *workspace, size_t workspace_bytes, void *stream) {
+  na::RpbProb A;
+  const int rc = make_rpb(p, &A);
+  if (rc != NA_OK) return rc;
+  if (drpb != nullptr) {
+    const size_t need = align256(na::rpb_bias_workspace_bytes(A));
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(NA_ERR_WORKSPACE,
+                  "na_rpb_qk_bwd needs a %zu-byte workspace for drpb (got %zu)",
+                  need, workspace_bytes);
+  }
+  if (A.n_rows == 0) {  // empty batch: drpb (if requested) is all zero
+    if (drpb != nullptr)
+      na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, nullptr, nullptr, drpb,
+                     (float *)workspace, as_stream(stream));
+    return launch_status("na_rpb_qk_bwd");
+  }
+  if (q == nullptr || key == nullptr || dlogits == nullptr)
+    return fail(NA_ERR_INVALID, "q/key/dlogits must be non-NULL");
+  na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, dq, dk, drpb, (float *)workspace,
+                 as_stream(stream));
+  return launch_status("na_rpb_qk_bwd");
+}
+
+int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,
+                  const void *dout, int32_t out_dtype, float *dattn,
+                  void *dvalue, void *stream) {
+  na::RpbProb A;
+  int rc = make_rpb(p, &A);
+  if (rc != NA_OK) return rc;
+  rc = check_out_dtype(p, out_dtype);
+  if (rc != NA_OK) return rc;
+  if (A.n_rows == 0) return NA_OK;
+  if (attn == nullptr || value == nullptr || dout == nullptr)
+    return fail(NA_ERR_INVALID, "attn/value/dout must be non-NULL");
+  na::rpb_av_bwd(A, p->dtype, out_dtype, attn, value, dout, dattn, dvalue,
+                 as_stream(stream));
+  return launch_status("na_rpb_av_bwd");
 }
 
 }  // extern "C"

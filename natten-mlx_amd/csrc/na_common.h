@@ -113,6 +113,39 @@ struct VecIO<bf16_t, 8> : VecIO16x8<bf16_t> {};
 template <>
 struct VecIO<f16_t, 8> : VecIO16x8<f16_t> {};
 
+template <typename T>
+struct VecIO16x4 {  // 4 x 16-bit elements = one 8-byte access
+  static __device__ __forceinline__ void load(const T *p, float *o) {
+    const uint2 t = *reinterpret_cast<const uint2 *>(p);
+    const uint32_t w[2] = {t.x, t.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      T lo, hi;
+      __builtin_memcpy(&lo, reinterpret_cast<const char *>(&w[i]), 2);
+      __builtin_memcpy(&hi, reinterpret_cast<const char *>(&w[i]) + 2, 2);
+      o[2 * i] = to_f32(lo);
+      o[2 * i + 1] = to_f32(hi);
+    }
+  }
+  static __device__ __forceinline__ void store(T *p, const float *x) {
+    uint32_t w[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const T lo = from_f32<T>(x[2 * i]);
+      const T hi = from_f32<T>(x[2 * i + 1]);
+      uint16_t a, b;
+      __builtin_memcpy(&a, &lo, 2);
+      __builtin_memcpy(&b, &hi, 2);
+      w[i] = (uint32_t)a | ((uint32_t)b << 16);
+    }
+    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+  }
+};
+template <>
+struct VecIO<bf16_t, 4> : VecIO16x4<bf16_t> {};
+template <>
+struct VecIO<f16_t, 4> : VecIO16x4<f16_t> {};
+
 // ---- problem descriptor (kernel argument, passed by value) ------------------
 struct Axis {
   int32_t L;       // tensor extent (maximum over samples for varlen)

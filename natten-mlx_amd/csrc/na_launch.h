@@ -24,14 +24,32 @@ void valu_qk_bwd(const Prob &P, int dtype, const void *q, const void *k,
                  const void *dl, void *dq, void *dk, hipStream_t st);
 void valu_av_bwd(const Prob &P, int dtype, const void *attn, const void *v,
                  const void *dout, void *dattn, void *dv, hipStream_t st);
-void valu_qk_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
-                 int32_t dil, float scale, int32_t has_scale, int dtype,
-                 const void *q, const void *key, const float *rpb,
-                 float *logits, hipStream_t st);
-void valu_av_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
-                 int32_t dil, int dtype, const float *attn, const void *v,
-                 float *out, hipStream_t st);
 void table(const Prob &P, int32_t *index, uint8_t *valid, hipStream_t st);
+
+// DiNAT all-in-one operators (na_rpb.hip): square window K (odd or even),
+// uniform dilation, rank 1 or 2, spatial-first or heads-first rows.
+struct RpbProb {
+  int32_t rank, B, H, D, K, dil;
+  int32_t L0, L1;       // L1 = 1 for rank 1
+  int32_t K1;           // window side on axis 1 (K, or 1 for rank 1)
+  int32_t KK;           // slots per query, K^rank
+  int32_t R;            // bias rows per axis, 2K-1
+  int32_t heads_first;  // 0: rows ordered [B, L0, L1, H]; 1: [B, H, L0, L1]
+  int32_t has_scale;    // q is scaled (and rounded to its dtype) first
+  float scale;
+  int32_t n_rows;       // B * H * L0 * L1 (< 2^31)
+};
+void rpb_qk_fwd(const RpbProb &A, int dtype, const void *q, const void *key,
+                const float *rpb, float *logits, hipStream_t st);
+void rpb_av_fwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
+                const void *value, void *out, hipStream_t st);
+size_t rpb_bias_workspace_bytes(const RpbProb &A);
+void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
+                const float *dlogits, void *dq, void *dk, float *drpb,
+                float *workspace, hipStream_t st);
+void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
+                const void *value, const void *dout, float *dattn, void *dvalue,
+                hipStream_t st);
 
 // Matrix-core kernels (na_mfma.hip): bf16/fp16, head_dim 32/64/128,
 // stride 1, odd kernel size on every non-causal axis.

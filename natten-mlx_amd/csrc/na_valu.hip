@@ -9,106 +9,10 @@
 // All arithmetic is fp32; outputs are rounded once to the storage type.
 #include "na_common.h"
 #include "na_launch.h"
+#include "na_row.h"
 
 namespace na {
 namespace {
-
-template <typename T, int VEC, int NT>
-struct Row {
-  float v[NT][VEC];
-
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[t][e] = 0.f;
-  }
-  __device__ __forceinline__ void load(const T *row, int lane, int G, int D) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d0 = (t * G + lane) * VEC;
-      if (d0 < D) {
-        VecIO<T, VEC>::load(row + d0, v[t]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) v[t][e] = 0.f;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(T *row, int lane, int G, int D) const {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d0 = (t * G + lane) * VEC;
-      if (d0 < D) VecIO<T, VEC>::store(row + d0, v[t]);
-    }
-  }
-  // Partial dot product with a row in memory (lane-local part).
-  __device__ __forceinline__ float dot_mem(const T *row, int lane, int G,
-                                           int D) const {
-    float acc = 0.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d0 = (t * G + lane) * VEC;
-      if (d0 < D) {
-        float x[VEC];
-        VecIO<T, VEC>::load(row + d0, x);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc = fmaf(v[t][e], x[e], acc);
-      }
-    }
-    return acc;
-  }
-  __device__ __forceinline__ float dot(const Row &o) const {
-    float acc = 0.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc = fmaf(v[t][e], o.v[t][e], acc);
-    return acc;
-  }
-  // this = this * a + w * row
-  __device__ __forceinline__ void scale_add_mem(float a, float w, const T *row,
-                                                int lane, int G, int D) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d0 = (t * G + lane) * VEC;
-      if (d0 < D) {
-        float x[VEC];
-        VecIO<T, VEC>::load(row + d0, x);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) v[t][e] = fmaf(v[t][e], a, w * x[e]);
-      }
-    }
-  }
-  __device__ __forceinline__ void add_scaled(float w, const Row &o) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[t][e] = fmaf(w, o.v[t][e], v[t][e]);
-  }
-  __device__ __forceinline__ void mul(float a) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[t][e] *= a;
-  }
-};
-
-struct Group {
-  int64_t id;  // group index (clamped to a live group for idle lanes)
-  int lane;
-  bool live;
-};
-
-__device__ __forceinline__ Group make_group(int lgG, int64_t n_groups) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  Group g;
-  g.id = gid >> lgG;
-  g.lane = (int)(gid & ((1 << lgG) - 1));
-  g.live = g.id < n_groups;
-  if (!g.live) g.id = 0;  // idle lanes shadow group 0 and never store
-  return g;
-}
 
 // Decode idx = (((b * E0 + x0) * E1 + x1) * E2 + x2) * Hn + h.
 struct Pos {
@@ -610,86 +514,6 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// DiNAT all-in-one 1D operators (dilation-partition window, RPB coupling).
-struct Rpb1d {
-  int32_t B, L, H, D, K, dil;
-  float scale;
-  int32_t has_scale;
-};
-
-template <typename T, int VEC, int NT>
-__global__ void __launch_bounds__(256)
-    k_qk_rpb(Rpb1d A, const T *__restrict__ q, const T *__restrict__ key,
-             const float *__restrict__ rpb, float *__restrict__ logits, int G,
-             int lgG, int64_t n_groups) {
-  const Group g = make_group(lgG, n_groups);
-  const int h = (int)(g.id % A.H);
-  const int i = (int)((g.id / A.H) % A.L);
-  const int b = (int)(g.id / ((int64_t)A.H * A.L));
-  const int nh = A.K / 2;
-  Row<T, VEC, NT> qr;
-  qr.load(q + g.id * A.D, g.lane, G, A.D);
-  if (A.has_scale) {
-    // the reference scales the query in its storage dtype before the dot
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) qr.v[t][e] = round_to<T>(qr.v[t][e] * A.scale);
-  }
-  const int32_t ni = window_start_partition(i, A.L, A.K, nh, A.dil);
-  const int32_t ei = window_end(ni, A.L, A.K, A.dil);
-  const int32_t pi = pb_start(i, A.L, A.K, nh, A.dil);
-  float *dst = logits + g.id * A.K;
-  for (int kk = 0; kk < A.K; ++kk) {
-    const int32_t j = ni + kk * A.dil;
-    float s = -INFINITY;
-    if (j >= 0 && j < ei) {
-      const int64_t row = (((int64_t)b * A.L + j) * A.H + h) * A.D;
-      s = group_sum(qr.dot_mem(key + row, g.lane, G, A.D), G);
-      if (rpb != nullptr) {
-        int32_t bi = pi + kk;
-        bi = bi < 0 ? 0 : (bi > 2 * A.K - 2 ? 2 * A.K - 2 : bi);
-        s += rpb[h * (2 * A.K - 1) + bi];
-      }
-    }
-    if (g.live && g.lane == 0) dst[kk] = s;
-  }
-}
-
-template <typename T, int VEC, int NT>
-__global__ void __launch_bounds__(256)
-    k_av_rpb(Rpb1d A, const float *__restrict__ attn, const T *__restrict__ v,
-             float *__restrict__ out, int G, int lgG, int64_t n_groups) {
-  const Group g = make_group(lgG, n_groups);
-  const int h = (int)(g.id % A.H);
-  const int i = (int)((g.id / A.H) % A.L);
-  const int b = (int)(g.id / ((int64_t)A.H * A.L));
-  const int nh = A.K / 2;
-  const int32_t ni = window_start_partition(i, A.L, A.K, nh, A.dil);
-  const int32_t ei = window_end(ni, A.L, A.K, A.dil);
-  const float *arow = attn + g.id * A.K;
-  Row<T, VEC, NT> acc;
-  acc.zero();
-  for (int kk = 0; kk < A.K; ++kk) {
-    const int32_t j = ni + kk * A.dil;
-    if (j >= 0 && j < ei) {
-      const int64_t row = (((int64_t)b * A.L + j) * A.H + h) * A.D;
-      acc.scale_add_mem(1.f, arow[kk], v + row, g.lane, G, A.D);
-    }
-  }
-  if (g.live) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int d0 = (t * G + g.lane) * VEC;
-      if (d0 < A.D) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) out[g.id * A.D + d0 + e] = acc.v[t][e];
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Device neighbor table (pure.py:24-152 layout) for bit-exact checks.
 __global__ void k_table(Prob P, int32_t *__restrict__ index,
                         uint8_t *__restrict__ valid, int64_t n) {
@@ -909,31 +733,6 @@ void av_bwd_t(const Prob &P, const void *attn, const void *v, const void *dout,
 #undef L_
 }
 
-template <typename T>
-void qk_rpb_t(const Rpb1d &A, const void *q, const void *key, const float *rpb,
-              float *logits, hipStream_t st) {
-  const Shape s = pick_shape<T>(A.D);
-  const int64_t n = (int64_t)A.B * A.L * A.H;
-#define L_(TT, V, N)                                                         \
-  hipLaunchKernelGGL((k_qk_rpb<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
-                     st, A, (const TT *)q, (const TT *)key, rpb, logits, s.G, \
-                     s.lgG, n)
-  NA_VALU_DISPATCH(T, s, L_);
-#undef L_
-}
-
-template <typename T>
-void av_rpb_t(const Rpb1d &A, const float *attn, const void *v, float *out,
-              hipStream_t st) {
-  const Shape s = pick_shape<T>(A.D);
-  const int64_t n = (int64_t)A.B * A.L * A.H;
-#define L_(TT, V, N)                                                         \
-  hipLaunchKernelGGL((k_av_rpb<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
-                     st, A, attn, (const TT *)v, out, s.G, s.lgG, n)
-  NA_VALU_DISPATCH(T, s, L_);
-#undef L_
-}
-
 }  // namespace
 
 #define NA_BY_DTYPE(dt, FN, ...)             \
@@ -993,20 +792,6 @@ void valu_av_bwd(const Prob &P, int dtype, const void *attn, const void *v,
   NA_BY_DTYPE(dtype, av_bwd_t, P, attn, v, dout, dattn, dv, st);
 }
 
-void valu_qk_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
-                 int32_t dil, float scale, int32_t has_scale, int dtype,
-                 const void *q, const void *key, const float *rpb,
-                 float *logits, hipStream_t st) {
-  const Rpb1d A{B, L, H, D, K, dil, scale, has_scale};
-  NA_BY_DTYPE(dtype, qk_rpb_t, A, q, key, rpb, logits, st);
-}
-
-void valu_av_rpb(int32_t B, int32_t L, int32_t H, int32_t D, int32_t K,
-                 int32_t dil, int dtype, const float *attn, const void *v,
-                 float *out, hipStream_t st) {
-  const Rpb1d A{B, L, H, D, K, dil, 1.f, 0};
-  NA_BY_DTYPE(dtype, av_rpb_t, A, attn, v, out, st);
-}
 
 void table(const Prob &P, int32_t *index, uint8_t *valid, hipStream_t st) {
   const int64_t n =

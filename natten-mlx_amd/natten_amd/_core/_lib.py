@@ -51,7 +51,26 @@ class NaParams(ctypes.Structure):
     ]
 
 
+class NaRpbParams(ctypes.Structure):
+    """Mirror of ``na_rpb_params`` (include/natten_amd.h)."""
+
+    _fields_ = [
+        ("rank", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("extent", ctypes.c_int32 * 2),
+        ("kernel", ctypes.c_int32),
+        ("dilation", ctypes.c_int32),
+        ("heads_first", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("has_scale", ctypes.c_int32),
+    ]
+
+
 _P = ctypes.POINTER(NaParams)
+_R = ctypes.POINTER(NaRpbParams)
 _V = ctypes.c_void_p
 _I = ctypes.c_int32
 
@@ -72,8 +91,11 @@ SIGNATURES = {
     "na_av_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V]),
     "na_qk_bwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V]),
     "na_av_bwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V]),
-    "na1d_qk_rpb_fwd": (ctypes.c_int, [_I] * 6 + [ctypes.c_float, _I, _I, _V, _V, _V, _V, _V]),
-    "na1d_av_rpb_fwd": (ctypes.c_int, [_I] * 7 + [_V, _V, _V, _V]),
+    "na_rpb_qk_fwd": (ctypes.c_int, [_R, _V, _V, _V, _V, _V]),
+    "na_rpb_av_fwd": (ctypes.c_int, [_R, _V, _V, _V, _I, _V]),
+    "na_rpb_bwd_workspace_bytes": (ctypes.c_size_t, [_R]),
+    "na_rpb_qk_bwd": (ctypes.c_int, [_R, _V, _V, _V, _V, _V, _V, _V, ctypes.c_size_t, _V]),
+    "na_rpb_av_bwd": (ctypes.c_int, [_R, _V, _V, _V, _I, _V, _V, _V]),
 }
 
 _lib = None
@@ -150,4 +172,19 @@ def make_params(rank: int, batch: int, heads: int, kv_heads: int, head_dim: int,
     p.n_extra = int(n_extra)
     p.flags = int(flags)
     p.sample_extent = None if sample_extent is None else sample_extent.data_ptr()
+    return p
+
+
+def make_rpb_params(rank: int, batch: int, heads: int, head_dim: int, extent, kernel: int,
+                    dilation: int, heads_first: bool, dtype: int,
+                    scale: float | None) -> NaRpbParams:
+    p = NaRpbParams()
+    p.rank, p.batch, p.heads, p.head_dim = rank, batch, heads, head_dim
+    p.extent[0] = int(extent[0])
+    p.extent[1] = int(extent[1]) if rank == 2 else 1
+    p.kernel, p.dilation = int(kernel), int(dilation)
+    p.heads_first = 1 if heads_first else 0
+    p.dtype = dtype
+    p.scale = 1.0 if scale is None else float(scale)
+    p.has_scale = 0 if scale is None else 1
     return p

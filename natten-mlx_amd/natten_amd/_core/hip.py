@@ -294,37 +294,125 @@ def varlen_forward(q, k, v, sample_extent, kernel_size, dilation, scale):
 
 
 # ---------------------------------------------------------------------------
-# DiNAT allin1 1D
+# DiNAT all-in-one operators (rank 1 and 2, square window, one dilation)
 
-def qk_rpb_1d(q, k, rpb, kernel_size, dilation, scale):
+def _rpb_geometry(x: torch.Tensor, heads_first: bool):
+    """(rank, batch, heads, extent, last) of a [B, *L, H, X] (or heads-first
+    [B, H, *L, X]) tensor."""
+    rank = x.dim() - 3
+    if rank not in (1, 2):
+        raise ValueError(f"allin1 ops take rank-1 or rank-2 tensors, got {x.dim()}D")
+    if heads_first:
+        return rank, x.shape[0], x.shape[1], tuple(x.shape[2:-1]), x.shape[-1]
+    return rank, x.shape[0], x.shape[-2], tuple(x.shape[1:-2]), x.shape[-1]
+
+
+def _rpb_params(x, kernel_size, dilation, heads_first, scale=None):
+    rank, B, H, ext, D = _rpb_geometry(x, heads_first)
+    return _lib.make_rpb_params(rank, B, H, D, ext, int(kernel_size), int(dilation),
+                                heads_first, _lib.dtype_code(x.dtype), scale)
+
+
+def _slots_shape(x, kernel_size, heads_first):
+    rank = x.dim() - 3
+    return tuple(x.shape[:-1]) + (int(kernel_size) ** rank,)
+
+
+def _check_same_layout(a, b, what):
+    if tuple(a.shape) != tuple(b.shape):
+        raise ValueError(f"{what} must have identical shapes, got {tuple(a.shape)} and "
+                         f"{tuple(b.shape)}")
+
+
+def _bias_shape(rank, heads, kernel_size):
+    r = 2 * int(kernel_size) - 1
+    return (heads, r) if rank == 1 else (heads, r, r)
+
+
+def rpb_qk_forward(q, k, rpb, kernel_size, dilation, scale=None, heads_first=False):
+    """float32 logits ``[.., K^rank]``: <round(q*scale), key_nbr> + bias, -inf
+    outside the window (C ABI ``na_rpb_qk_fwd``)."""
     _require_device(q, k, rpb)
     q, k = _c(q), _c(k)
     if k.dtype != q.dtype:
         k = k.to(q.dtype)
-    B, L, H, D = q.shape
-    rp = None if rpb is None else _c(rpb.to(torch.float32))
-    if rp is not None and tuple(rp.shape) != (H, 2 * kernel_size - 1):
-        raise ValueError(f"rpb must have shape [{H}, {2 * kernel_size - 1}], got {tuple(rp.shape)}")
-    out = torch.empty((B, L, H, kernel_size), dtype=torch.float32, device=q.device)
+    _check_same_layout(q, k, "query and key")
+    p = _rpb_params(q, kernel_size, dilation, heads_first, scale)
+    rp = None
+    if rpb is not None:
+        rp = _c(rpb.to(torch.float32))
+        want = _bias_shape(p.rank, p.heads, kernel_size)
+        if tuple(rp.shape) != want:
+            raise ValueError(f"rpb must have shape {list(want)}, got {tuple(rp.shape)}")
+    out = torch.empty(_slots_shape(q, kernel_size, heads_first), dtype=torch.float32,
+                      device=q.device)
     lib = _lib.load()
-    _lib.check(lib.na1d_qk_rpb_fwd(B, L, H, D, kernel_size, dilation,
-                                   1.0 if scale is None else float(scale),
-                                   0 if scale is None else 1, _lib.dtype_code(q.dtype),
-                                   _lib.ptr(q), _lib.ptr(k), _lib.ptr(rp), _lib.ptr(out),
-                                   _lib.stream_of(q)), "na1d_qk_rpb_fwd")
+    _lib.check(lib.na_rpb_qk_fwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(rp), _lib.ptr(out),
+                                 _lib.stream_of(q)), "na_rpb_qk_fwd")
     return out
 
 
-def av_rpb_1d(attn, v, kernel_size, dilation):
+def rpb_av_forward(attn, v, kernel_size, dilation, heads_first=False, out_dtype=torch.float32):
+    """out = sum attn * value_nbr in ``out_dtype`` (float32 or v.dtype)
+    (C ABI ``na_rpb_av_fwd``)."""
     _require_device(attn, v)
-    a = _c(attn.to(torch.float32))
     v = _c(v)
-    B, L, H, D = v.shape
-    if tuple(a.shape) != (B, L, H, kernel_size):
-        raise ValueError(f"attn must have shape {(B, L, H, kernel_size)}, got {tuple(a.shape)}")
-    out = torch.empty((B, L, H, D), dtype=torch.float32, device=v.device)
+    a = _c(attn.to(torch.float32))
+    want = _slots_shape(v, kernel_size, heads_first)
+    if tuple(a.shape) != want:
+        raise ValueError(f"attn must have shape {want}, got {tuple(a.shape)}")
+    if out_dtype not in (torch.float32, v.dtype):
+        raise ValueError("out_dtype must be float32 or the value dtype")
+    p = _rpb_params(v, kernel_size, dilation, heads_first)
+    out = torch.empty(v.shape, dtype=out_dtype, device=v.device)
     lib = _lib.load()
-    _lib.check(lib.na1d_av_rpb_fwd(B, L, H, D, kernel_size, dilation, _lib.dtype_code(v.dtype),
-                                   _lib.ptr(a), _lib.ptr(v), _lib.ptr(out), _lib.stream_of(v)),
-               "na1d_av_rpb_fwd")
+    _lib.check(lib.na_rpb_av_fwd(p, _lib.ptr(a), _lib.ptr(v), _lib.ptr(out),
+                                 _lib.dtype_code(out_dtype), _lib.stream_of(v)), "na_rpb_av_fwd")
     return out
+
+
+def rpb_qk_backward(q, k, d_logits, kernel_size, dilation, scale=None, heads_first=False,
+                    need_q=True, need_k=True, need_rpb=True):
+    """(dq, dk, drpb) of ``rpb_qk_forward``; drpb is float32 (C ABI
+    ``na_rpb_qk_bwd``).  Unrequested gradients come back as None."""
+    _require_device(q, k, d_logits)
+    q, k = _c(q), _c(k)
+    if k.dtype != q.dtype:
+        k = k.to(q.dtype)
+    dl = _c(d_logits.to(torch.float32))
+    if tuple(dl.shape) != _slots_shape(q, kernel_size, heads_first):
+        raise ValueError(f"d_logits must have shape {_slots_shape(q, kernel_size, heads_first)}")
+    p = _rpb_params(q, kernel_size, dilation, heads_first, scale)
+    dq = torch.empty_like(q) if need_q else None
+    dk = torch.empty_like(k) if need_k else None
+    drpb = ws = None
+    lib = _lib.load()
+    nbytes = 0
+    if need_rpb:
+        drpb = torch.empty(_bias_shape(p.rank, p.heads, kernel_size), dtype=torch.float32,
+                           device=q.device)
+        nbytes = lib.na_rpb_bwd_workspace_bytes(p)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.na_rpb_qk_bwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(dl), _lib.ptr(dq),
+                                 _lib.ptr(dk), _lib.ptr(drpb), _lib.ptr(ws), nbytes,
+                                 _lib.stream_of(q)), "na_rpb_qk_bwd")
+    return dq, dk, drpb
+
+
+def rpb_av_backward(attn, v, d_out, kernel_size, dilation, heads_first=False, need_attn=True,
+                    need_v=True):
+    """(dattn float32, dv) of ``rpb_av_forward``; ``d_out`` has the forward's
+    output dtype (C ABI ``na_rpb_av_bwd``)."""
+    _require_device(attn, v, d_out)
+    v = _c(v)
+    a = _c(attn.to(torch.float32))
+    do = _c(d_out if d_out.dtype in (torch.float32, v.dtype) else d_out.to(torch.float32))
+    _check_same_layout(v, do, "value and d_out")
+    p = _rpb_params(v, kernel_size, dilation, heads_first)
+    da = torch.empty(a.shape, dtype=torch.float32, device=v.device) if need_attn else None
+    dv = torch.empty_like(v) if need_v else None
+    lib = _lib.load()
+    _lib.check(lib.na_rpb_av_bwd(p, _lib.ptr(a), _lib.ptr(v), _lib.ptr(do),
+                                 _lib.dtype_code(do.dtype), _lib.ptr(da), _lib.ptr(dv),
+                                 _lib.stream_of(v)), "na_rpb_av_bwd")
+    return da, dv

@@ -15,9 +15,11 @@ Reference code followed:
 * ``full_attn_with_lse``: ``functional.py:71-104``.
 * ``merge_attentions``: ``merge.py:20-68`` (sigmoid form, float32 inside).
 * ``na_varlen``: ``pure.py:497-688`` (per-sample calls, zero padding).
-* ``qk_rpb_1d`` / ``av_1d``: ``extras/allin1/__init__.py:40-109`` with the
-  MLX fallback ``extras/allin1/functional.py:260-368`` (query scaled in its
-  own dtype first; partition window; rpb index clip(pb + k, 0, 2K-2)).
+* ``qk_rpb`` / ``av_rpb`` (rank 1 and 2): ``extras/allin1/__init__.py:40-180``
+  with the MLX fallbacks ``extras/allin1/functional.py:57-368`` (query scaled
+  in its own dtype first; partition window, equal to the legacy window when
+  d*K <= L; rpb index clip(pb + k, 0, 2K-2) per axis, 2D pair index
+  i*(2K-1)+j).
 
 Pinned by (tests/test_oracle_na.py): scalar brute-force loops
 (``oracle.brute``), the global-attention special case against a plain
@@ -196,43 +198,81 @@ def na_varlen(q, k, v, sizes, kernel_size, dilation=1, scale=None,
     return out
 
 
-def qk_rpb_1d(q, k, rpb, kernel_size, dilation=1, scale=None, compute_dtype=torch.float64):
-    """allin1 ``na1d_qk_rpb``: q ``[B, L, H, D]`` -> logits ``[B, L, H, K]``."""
-    if scale is not None:
-        q = q * scale  # in the storage dtype, before the dot (``__init__.py:61-62``)
-    B, L, H, D = q.shape
-    K, d = int(kernel_size), int(dilation)
+def _allin1_axis(L, K, d):
+    """Per-axis partition windows: slot positions [L, K], validity [L, K] and
+    clipped bias rows [L, K] (``extras/allin1/reference_impl.py:13-45``,
+    ``compat/v014.py:18-23``)."""
     nh = K // 2
     ni = np.array([W.window_start_partition(i, L, K, nh, d) for i in range(L)])
     ei = np.minimum(L, ni + K * d)
     pi = np.array([W.pb_start(i, L, K, nh, d) for i in range(L)])
     pos = ni[:, None] + np.arange(K)[None, :] * d
-    valid = torch.from_numpy((pos >= 0) & (pos < ei[:, None]))
-    kn = k.to(compute_dtype)[:, torch.from_numpy(np.clip(pos, 0, L - 1).reshape(-1))]
-    kn = kn.reshape(B, L, K, H, D)
-    logits = torch.einsum("blhd,blkhd->blhk", q.to(compute_dtype), kn)
+    valid = (pos >= 0) & (pos < ei[:, None])
+    bias = np.clip(pi[:, None] + np.arange(K)[None, :], 0, 2 * K - 2)
+    return np.clip(pos, 0, L - 1), valid, bias
+
+
+def _allin1_tables(spatial, K, d):
+    """Flattened neighbor index, validity and bias index over all query
+    positions of a rank-1/2 grid: arrays [prod(spatial), K^rank]."""
+    axes = [_allin1_axis(L, K, d) for L in spatial]
+    if len(spatial) == 1:
+        pos, valid, bias = axes[0]
+        return pos, valid, bias
+    (p0, v0, b0), (p1, v1, b1) = axes
+    L0, L1 = spatial
+    R = 2 * K - 1
+    lin = (p0[:, None, :, None] * L1 + p1[None, :, None, :]).reshape(L0 * L1, K * K)
+    val = (v0[:, None, :, None] & v1[None, :, None, :]).reshape(L0 * L1, K * K)
+    bia = (b0[:, None, :, None] * R + b1[None, :, None, :]).reshape(L0 * L1, K * K)
+    return lin, val, bia
+
+
+def qk_rpb(q, k, rpb, kernel_size, dilation=1, scale=None, compute_dtype=torch.float64):
+    """allin1 ``na{1,2}d_qk_rpb``: q ``[B, *L, H, D]`` -> logits
+    ``[B, *L, H, K^rank]``; rpb ``[H, 2K-1]`` or ``[H, 2K-1, 2K-1]``."""
+    if scale is not None:
+        q = q * scale  # in the storage dtype, before the dot (``__init__.py:61-62``)
+    B, H, D = q.shape[0], q.shape[-2], q.shape[-1]
+    sp = tuple(q.shape[1:-2])
+    K, d = int(kernel_size), int(dilation)
+    lin, valid, bidx = _allin1_tables(sp, K, d)
+    n, kk = lin.shape
+    qf = q.to(compute_dtype).reshape(B, n, H, D)
+    kn = k.to(compute_dtype).reshape(B, n, H, D)[:, torch.from_numpy(lin.reshape(-1))]
+    kn = kn.reshape(B, n, kk, H, D)
+    logits = torch.einsum("bnhd,bnkhd->bnhk", qf, kn)
     if rpb is not None:
-        bidx = torch.from_numpy(np.clip(pi[:, None] + np.arange(K)[None, :], 0, 2 * K - 2))
-        bias = rpb.to(compute_dtype)[:, bidx]  # [H, L, K]
+        flat = rpb.to(compute_dtype).reshape(H, -1)
+        bias = flat[:, torch.from_numpy(bidx)]  # [H, n, kk]
         logits = logits + bias.permute(1, 0, 2).unsqueeze(0)
-    return torch.where(valid.reshape(1, L, 1, K), logits,
-                       torch.full_like(logits, -math.inf))
+    logits = torch.where(torch.from_numpy(valid).reshape(1, n, 1, kk), logits,
+                         torch.full_like(logits, -math.inf))
+    return logits.reshape(B, *sp, H, kk)
+
+
+def av_rpb(attn, v, kernel_size, dilation=1, compute_dtype=torch.float64):
+    """allin1 ``na{1,2}d_av_fused``: attn ``[B, *L, H, K^rank]``, v ``[B, *L, H, D]``."""
+    B, H, D = v.shape[0], v.shape[-2], v.shape[-1]
+    sp = tuple(v.shape[1:-2])
+    K, d = int(kernel_size), int(dilation)
+    lin, valid, _ = _allin1_tables(sp, K, d)
+    n, kk = lin.shape
+    vn = v.to(compute_dtype).reshape(B, n, H, D)[:, torch.from_numpy(lin.reshape(-1))]
+    vn = vn.reshape(B, n, kk, H, D)
+    a = torch.where(torch.from_numpy(valid).reshape(1, n, 1, kk),
+                    attn.to(compute_dtype).reshape(B, n, H, kk), torch.zeros((), dtype=compute_dtype))
+    return torch.einsum("bnhk,bnkhd->bnhd", a, vn).reshape(B, *sp, H, D)
+
+
+def qk_rpb_1d(q, k, rpb, kernel_size, dilation=1, scale=None, compute_dtype=torch.float64):
+    """allin1 ``na1d_qk_rpb``: q ``[B, L, H, D]`` -> logits ``[B, L, H, K]``."""
+    return qk_rpb(q, k, rpb, kernel_size, dilation, scale, compute_dtype)
 
 
 def av_1d(attn, v, kernel_size, dilation=1, compute_dtype=torch.float64):
     """allin1 ``na1d_av_fused``: attn ``[B, L, H, K]``, v ``[B, L, H, D]``."""
-    B, L, H, D = v.shape
-    K, d = int(kernel_size), int(dilation)
-    nh = K // 2
-    ni = np.array([W.window_start_partition(i, L, K, nh, d) for i in range(L)])
-    ei = np.minimum(L, ni + K * d)
-    pos = ni[:, None] + np.arange(K)[None, :] * d
-    valid = torch.from_numpy((pos >= 0) & (pos < ei[:, None]))
-    vn = v.to(compute_dtype)[:, torch.from_numpy(np.clip(pos, 0, L - 1).reshape(-1))]
-    vn = vn.reshape(B, L, K, H, D)
-    a = torch.where(valid.reshape(1, L, 1, K), attn.to(compute_dtype),
-                    torch.zeros((), dtype=compute_dtype))
-    return torch.einsum("blhk,blkhd->blhd", a, vn)
+    return av_rpb(attn, v, kernel_size, dilation, compute_dtype)
 
 
 def grads(fn, inputs: Sequence[torch.Tensor], cotangents: Sequence[Optional[torch.Tensor]]):

@@ -25,7 +25,8 @@ def _declared_functions():
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
     for n in ("na_fwd", "na_bwd", "na_bwd_workspace_bytes", "na_qk_fwd", "na_av_fwd",
-              "na_qk_bwd", "na_av_bwd", "na1d_qk_rpb_fwd", "na1d_av_rpb_fwd",
+              "na_qk_bwd", "na_av_bwd", "na_rpb_qk_fwd", "na_rpb_av_fwd", "na_rpb_qk_bwd",
+              "na_rpb_av_bwd", "na_rpb_bwd_workspace_bytes",
               "na_neighbor_table", "na_last_error", "na_abi_version"):
         assert n in names
 

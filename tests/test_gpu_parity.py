@@ -237,25 +237,6 @@ def test_varlen_gqa_extra_cfg4_shape(dtype):
         assert (out[b, Lb:] == 0).all()
 
 
-@pytest.mark.parametrize("K,d", [(3, 1), (5, 2), (7, 4), (5, 8), (7, 8)])
-def test_allin1(K, d):
-    from natten_amd.extras.allin1 import na1d_av_fused, na1d_qk_rpb
-
-    _say(f"[case] allin1 K={K} d={d}")
-    B, L, H, D = 2, 256, 12, 12
-    q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (1, 2, 3))
-    rpb = randn((H, 2 * K - 1), torch.float32, 4, std=0.02)
-    logits = na1d_qk_rpb(q.to(DEV), k.to(DEV), rpb.to(DEV), K, d, scale=0.288)
-    assert logits.dtype == torch.float32
-    ref = O.qk_rpb_1d(q, k, rpb, K, d, scale=0.288)
-    assert_close(logits, ref, torch.float32, "qk_rpb")
-    attn = torch.softmax(logits, -1)
-    out = na1d_av_fused(attn, v.to(DEV), K, d)
-    assert_close(out, O.av_1d(attn.cpu(), v, K, d), torch.float32, "av")
-    none = na1d_qk_rpb(q.to(DEV), k.to(DEV), None, K, d)
-    assert_close(none, O.qk_rpb_1d(q, k, None, K, d), torch.float32, "qk no rpb")
-
-
 def test_backward_is_deterministic():
     import natten_amd
 

@@ -126,6 +126,70 @@ def test_allin1_av_equals_split_av(K, d):
     torch.testing.assert_close(O.av_1d(a, v, K, d), O.na_av(a, v, K, 1, d, False))
 
 
+@pytest.mark.parametrize("K,d,shape", [(3, 1, (9, 11)), (5, 2, (12, 10)), (7, 1, (7, 15)),
+                                       (3, 3, (10, 9))])
+def test_allin1_2d_qk_rpb_relations(K, d, shape):
+    """2D QK+RPB == split 2D QK (legacy windows) + the bias at each axis's
+    relative offset, pair index r0*(2K-1)+r1 (reference
+    tests/test_extras_allin1.py:35-68); rpb = arange known answer."""
+    B, H, D = 2, 2, 12
+    Hh, Hw = shape
+    q, k = _r((B, Hh, Hw, H, D), 1), _r((B, Hh, Hw, H, D), 2)
+    R = 2 * K - 1
+    rpb = _r((H, R, R), 3)
+    got = O.qk_rpb(q, k, rpb, K, d, scale=0.3)
+    base = O.na_qk(q, k, K, 1, d, False, 0.3)
+
+    def rel(L):
+        st = np.array([O.W.window_start(i, L, K, K // 2, d) for i in range(L)])
+        return (st[:, None] + np.arange(K)[None, :] * d - np.arange(L)[:, None]) // d + K - 1
+
+    r0, r1 = rel(Hh), rel(Hw)
+    pair = (r0[:, None, :, None] * R + r1[None, :, None, :]).reshape(Hh, Hw, K * K)
+    bias = rpb.reshape(H, R * R)[:, torch.from_numpy(pair)].permute(1, 2, 0, 3)
+    torch.testing.assert_close(got, base + bias.unsqueeze(0))
+    zero = torch.zeros((1, Hh, Hw, 1, 4), dtype=torch.float64)
+    ar = torch.arange(R * R, dtype=torch.float64).reshape(1, R, R)
+    got0 = O.qk_rpb(zero, zero, ar, K, d)
+    torch.testing.assert_close(got0[0, :, :, 0], torch.from_numpy(pair).to(torch.float64))
+
+
+@pytest.mark.parametrize("K,d", [(3, 1), (5, 2)])
+def test_allin1_2d_av_equals_split_av(K, d):
+    B, H, D = 2, 2, 12
+    a = torch.softmax(_r((B, 11, 10, H, K * K), 1), -1)
+    v = _r((B, 11, 10, H, D), 2)
+    torch.testing.assert_close(O.av_rpb(a, v, K, d), O.na_av(a, v, K, 1, d, False))
+
+
+def test_allin1_partition_edges_beyond_d_times_k():
+    """Where d*K > L the partition window can start below zero: those slots
+    are invalid (-inf), matching a scalar walk of the partition rule."""
+    L, K, d, H, D = 9, 5, 3, 1, 2
+    q, k = _r((1, L, H, D), 1), _r((1, L, H, D), 2)
+    got = O.qk_rpb(q, k, None, K, d)
+    for i in range(L):
+        s = O.W.window_start_partition(i, L, K, K // 2, d)
+        e = min(L, s + K * d)
+        for n in range(K):
+            j = s + n * d
+            if 0 <= j < e:
+                assert got[0, i, 0, n] == (q[0, i, 0] * k[0, j, 0]).sum()
+            else:
+                assert got[0, i, 0, n] == -math.inf
+
+
+def test_allin1_backward_matches_finite_differences():
+    q, k = _r((1, 6, 5, 2, 3), 1), _r((1, 6, 5, 2, 3), 2)
+    rpb = _r((2, 5, 5), 3)
+    a, v = torch.softmax(_r((1, 6, 5, 2, 9), 4), -1), _r((1, 6, 5, 2, 3), 5)
+    for t in (q, k, rpb, a, v):
+        t.requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda x, y, z: O.qk_rpb(x, y, z, 3, 2, 0.7).clamp_min(-1e9),
+                                    (q, k, rpb))
+    assert torch.autograd.gradcheck(lambda x, y: O.av_rpb(x, y, 3, 2), (a, v))
+
+
 def test_backward_matches_finite_differences():
     q, k, v = _r((1, 5, 4, 2, 3), 1), _r((1, 5, 4, 1, 3), 2), _r((1, 5, 4, 1, 3), 3)
     ek, ev = _r((1, 2, 1, 3), 4), _r((1, 2, 1, 3), 5)
