@@ -15,6 +15,7 @@ Printed JSON line (rank 0): metric/value/unit per the driver contract, with
    autograd) on a bounded sample, timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+       python bench.py --workload {split,cfg3,cfg4,cfg5}   (other configurations)
 """
 
 from __future__ import annotations
@@ -34,6 +35,7 @@ import torch  # noqa: E402
 
 B, HH, WW, HEADS, D, K = 4, 56, 56, 4, 32, 7
 HBM_PEAK_GBS = 8000.0
+COPY_BYTES = 1 << 30   # calibration copy for --profile-calls (1 GiB each way)
 BF16_PEAK_TFLOPS = 2516.6
 
 
@@ -130,6 +132,25 @@ def run_gpu(args):
     return results
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_hbm_traffic.md")
+CALL_KERNEL = {"na_fwd": "k_mfwd", "na_bwd": "k_mbwd"}
+
+
+def measured_traffic(call: str):
+    """HBM bytes per launch of the call's kernel from the committed counter
+    summary (FETCH_SIZE / WRITE_SIZE runs, copy-calibrated), or None."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and \
+                parts[1] == CALL_KERNEL.get(call):
+            return int(parts[2])
+    return None
+
+
 def time_calls(fn, steps: int, reps: int = 20) -> float:
     """Average device time (ms) of one call of ``fn``: events bracket a
     graph replay of ``reps`` back-to-back calls (eager loop if capture
@@ -173,11 +194,211 @@ def profile_calls(n: int) -> None:
     q, k, v, do = make_inputs(torch.device("cuda:0"))
     a = ((K, K), (1, 1), (1, 1), (False, False), None)
     out, lse = hip.fused_forward(q, k, v, *a)
+    # calibration for the HBM byte counters: a plain device copy of a known
+    # size (COPY_BYTES read + COPY_BYTES written), far larger than the caches
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=q.device).uniform_()
+    dst = torch.empty_like(src)
     for _ in range(n):
+        dst.copy_(src)
         hip.fused_forward(q, k, v, *a)
         hip.fused_backward(q, k, v, out, lse, do, None, *a)
     torch.cuda.synchronize()
-    print(f"profile-calls: {n} forward + {n} backward calls done", flush=True)
+    print(f"profile-calls: {n} copies of {COPY_BYTES} B, {n} forward + {n} backward calls done",
+          flush=True)
+
+
+# ---------------------------------------------------------------------------
+# the other BASELINE.json configurations (parity-test cases; measured with
+# --workload, one JSON line each, not the driver's bench line)
+
+def _gen(shape, dtype, seed, std=1.0, device="cuda:0"):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype).to(device)
+
+
+def _valid_pairs(spatial, ks, dil, caus):
+    """Valid (query, neighbor) pairs per (batch, head): validity is a product
+    over axes, so the count factorises; non-causal slots are all valid when
+    d*K <= L, causal ones keep min(K, i//d + 1) keys."""
+    total = 1
+    for L, kx, d, c in zip(spatial, ks, dil, caus):
+        total *= sum(min(kx, i // d + 1) for i in range(L)) if c else L * kx
+    return total
+
+
+def _roof(call, nbytes, flops, ms, flop_peak):
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "call": call,
+            "call_ms": round(ms, 5), "bytes": nbytes, "flops": flops,
+            "flop_frac": round(flops / (ms * 1e-3) / 1e12 / flop_peak, 6)}
+
+
+def _line(metric, value, unit, ms, dtype, config, roofline, extra=None):
+    line = {"metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic, seed 0", "config": config,
+            "roofline": roofline, "cpu_baseline": None}
+    line.update(extra or {})
+    return line
+
+
+def wl_split(args):
+    """Config 2s: na2d_qk -> softmax -> na2d_av, bf16, B=4 56x56 heads 4 D 32 k 7."""
+    from natten_amd._core import hip
+
+    q, k, v, do = make_inputs(torch.device("cuda:0"))
+    a = ((K, K), (1, 1), (1, 1), (False, False))
+    logits = hip.qk_forward(q, k, *a, None)
+    attn = torch.softmax(logits, -1)
+    qk_ms = time_calls(lambda: hip.qk_forward(q, k, *a, None), args.steps)
+    av_ms = time_calls(lambda: hip.av_forward(attn, v, *a), args.steps)
+    dl = _gen(logits.shape, torch.bfloat16, 5)
+    qkb_ms = time_calls(lambda: hip.qk_backward(q, k, dl, *a, None), args.steps)
+    avb_ms = time_calls(lambda: hip.av_backward(attn, v, do, *a), args.steps)
+    t = B * HH * WW * HEADS * D * 2
+    lg = B * HH * WW * HEADS * K * K * 2
+    pairs = B * HEADS * _valid_pairs((HH, WW), (K, K), (1, 1), (False, False))
+    qk_b, av_b = 2 * t + lg, lg + 2 * t
+    fl = 2 * D * pairs
+    rq = _roof("na_qk_fwd", qk_b, fl, qk_ms, BF16_PEAK_TFLOPS)
+    ra = _roof("na_av_fwd", av_b, fl, av_ms, BF16_PEAK_TFLOPS)
+    value = (qk_b + av_b) / ((qk_ms + av_ms) * 1e-3) / 1e9
+    cfg = {"workload": "na2d_qk + na2d_av split forward, bf16 B=4 56x56 heads=4 head_dim=32 "
+                       "k=7 dilation=1", "global_batch": B}
+    return _line("na2d split qk/av bf16 HBM GB/s, 1 MI355X", value, "GB/s", qk_ms + av_ms,
+                 "bf16", cfg, rq if qk_ms >= av_ms else ra,
+                 {"calls": {"qk": rq, "av": ra,
+                            "qk_bwd_ms": round(qkb_ms, 5), "av_bwd_ms": round(avb_ms, 5)}})
+
+
+def wl_cfg3(args):
+    """Config 3: na3d fwd+bwd bf16 with LSE, [1,16,32,32,8,64], k (3,7,7),
+    causal (T,F,F)."""
+    import natten_amd
+    from natten_amd._core import hip
+
+    dev = torch.device("cuda:0")
+    shape = (1, 16, 32, 32, 8, 64)
+    q, k, v, do = (_gen(shape, torch.bfloat16, s) for s in range(4))
+    ks, st, dl, ca = (3, 7, 7), (1, 1, 1), (1, 1, 1), (True, False, False)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        out, lse = natten_amd.na3d(q, k, v, ks, is_causal=ca, return_lse=True)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    step_ms = _eager_ms(step, args)
+    qd, kd, vd = q.detach(), k.detach(), v.detach()
+    out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
+    f_ms = time_calls(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None), args.steps)
+    b_ms = time_calls(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca,
+                                                 None), args.steps)
+    pairs = 8 * _valid_pairs(shape[1:4], ks, dl, ca)
+    tb = 16 * 32 * 32 * 8 * 64 * 2
+    lse_b = 16 * 32 * 32 * 8 * 4
+    fwd_f, bwd_f = 4 * 64 * pairs, 8 * 64 * pairs
+    fwd_b, bwd_b = 4 * tb + lse_b, 8 * tb + lse_b
+    rf = _roof("na_fwd", fwd_b, fwd_f, f_ms, BF16_PEAK_TFLOPS)
+    rb = _roof("na_bwd", bwd_b, bwd_f, b_ms, BF16_PEAK_TFLOPS)
+    cfg = {"workload": "na3d fused fwd+bwd with return_lse, bf16 [1,16,32,32,8,64] "
+                       "k=(3,7,7) causal=(T,F,F)", "global_batch": 1}
+    return _line("na3d 16x32x32 k(3,7,7) causal bf16 fwd+bwd TFLOP/s, 1 MI355X",
+                 (fwd_f + bwd_f) / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "bf16", cfg,
+                 rb if b_ms >= f_ms else rf,
+                 {"timing": {"fwd_call_ms": round(f_ms, 5), "bwd_call_ms": round(b_ms, 5),
+                             "calls_tflops": round((fwd_f + bwd_f) / ((f_ms + b_ms) * 1e-3)
+                                                   / 1e12, 3)},
+                  "calls": {"fwd": rf, "bwd": rb}})
+
+
+def wl_cfg4(args):
+    """Config 4: na1d varlen GQA + 16 additional tokens, fp16 forward,
+    q [8,4096,16,64], k/v [8,4096,4,64], seq_lens ~ U{1024..4096}, k 63, d 2."""
+    import natten_amd
+    from natten_amd._core import hip
+
+    Bc, L, H, Hkv, Dc, nx = 8, 4096, 16, 4, 64, 16
+    q = _gen((Bc, L, H, Dc), torch.float16, 0)
+    k, v = (_gen((Bc, L, Hkv, Dc), torch.float16, s) for s in (1, 2))
+    ak, av = (_gen((Bc, nx, Hkv, Dc), torch.float16, s) for s in (3, 4))
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(1024, 4097, (Bc,), generator=g, dtype=torch.int32)
+    lens_d = lens.to("cuda:0")
+
+    def step():
+        return natten_amd.na1d_varlen_gqa(q, k, v, lens_d, 63, 2, additional_keys=ak,
+                                          additional_values=av)
+
+    step_ms = _eager_ms(step, args)
+    se = lens_d.reshape(Bc, 1).contiguous()
+    f_ms = time_calls(lambda: hip.fused_forward(q, k, v, (63,), (1,), (2,), (False,), None,
+                                                extra_k=ak, extra_v=av, sample_extent=se),
+                      args.steps)
+    tokens = int(lens.sum())
+    flops = tokens * H * 4 * Dc * (63 + nx)
+    nbytes = tokens * (H * Dc * 2 + 2 * Hkv * Dc * 2 + H * Dc * 2) + 2 * Bc * nx * Hkv * Dc * 2
+    nbytes_pad = nbytes + (Bc * L - tokens) * H * Dc * 2  # padded rows written as zeros
+    rf = _roof("na_fwd", nbytes_pad, flops, f_ms, BF16_PEAK_TFLOPS)
+    cfg = {"workload": "na1d varlen GQA (16 q heads / 4 kv heads) + 16 additional tokens, fp16 "
+                       "forward, [8,4096,*,64], k=63 d=2", "global_batch": Bc,
+           "seq_lens": lens.tolist(), "tokens": tokens}
+    return _line("na1d varlen gqa+extra fp16 fwd TFLOP/s, 1 MI355X",
+                 flops / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "fp16", cfg, rf,
+                 {"timing": {"fwd_call_ms": round(f_ms, 5),
+                             "call_tflops": round(flops / (f_ms * 1e-3) / 1e12, 3)}})
+
+
+def wl_cfg5(args):
+    """Config 5: allin1 na1d_qk_rpb + na1d_av_fused fp32 [8,2048,12,12],
+    K in {3,5,7} x d in {1,2,4,8}, scale 0.288 (forward, plus the backward
+    calls timed alongside)."""
+    from natten_amd._core import hip
+
+    Bc, L, H, Dc = 8, 2048, 12, 12
+    q, k, v = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
+    t = Bc * L * H * Dc * 4
+    rows = Bc * L * H
+    table = {}
+    best = None
+    for Kx in (3, 5, 7):
+        rpb = _gen((H, 2 * Kx - 1), torch.float32, 10 + Kx, std=0.02)
+        for d in (1, 2, 4, 8):
+            logits = hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288)
+            attn = torch.softmax(logits, -1)
+            qk_ms = time_calls(lambda: hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288), args.steps)
+            av_ms = time_calls(lambda: hip.rpb_av_forward(attn, v, Kx, d), args.steps)
+            qkb_ms = time_calls(lambda: hip.rpb_qk_backward(q, k, attn, Kx, d, 0.288),
+                                args.steps)
+            avb_ms = time_calls(lambda: hip.rpb_av_backward(attn, v, v, Kx, d), args.steps)
+            lg = rows * Kx * 4
+            qk_b, av_b = 2 * t + lg, lg + 2 * t
+            rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, qk_ms, 157.3)
+            ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, av_ms, 157.3)
+            table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd_ms": round(qkb_ms, 5),
+                                    "av_bwd_ms": round(avb_ms, 5)}
+            if Kx == 7 and d == 1:
+                best = (rq, ra, qk_ms + av_ms, (qk_b + av_b) / ((qk_ms + av_ms) * 1e-3) / 1e9)
+    rq, ra, ms, gbs = best
+    cfg = {"workload": "allin1 na1d_qk_rpb + na1d_av_fused fp32 [8,2048,12,12] K=7 d=1 "
+                       "(all K x d in 'sweep')", "global_batch": Bc}
+    return _line("allin1 qk_rpb+av fp32 HBM GB/s (K=7 d=1), 1 MI355X", gbs, "GB/s", ms, "f32",
+                 cfg, rq if rq["call_ms"] >= ra["call_ms"] else ra, {"sweep": table})
+
+
+def _eager_ms(step, args):
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / args.steps
+
+
+WORKLOADS = {"split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4, "cfg5": wl_cfg5}
 
 
 def run_cpu_baseline():
@@ -218,6 +439,9 @@ def main(argv=None):
     ap.add_argument("--profile-calls", type=int, default=0, metavar="N",
                     help="only run N fused forward and N fused backward calls at the "
                          "dilation-1 workload (for rocprofv3 --pmc passes), then exit")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
+                    help="cfg2 (default) is the driver's bench line; the others measure the "
+                         "remaining BASELINE.json configurations")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -230,6 +454,9 @@ def main(argv=None):
 
     if args.profile_calls > 0:
         profile_calls(args.profile_calls)
+        return 0
+    if args.workload != "cfg2":
+        print(json.dumps(WORKLOADS[args.workload](args)), flush=True)
         return 0
     res = run_gpu(args)
     fwd_f, bwd_f, fwd_b, bwd_b = algorithmic(K * K)
@@ -245,7 +472,8 @@ def main(argv=None):
         dom, dom_ms, dom_bytes, dom_flops = "na_fwd", r1["fwd_ms"], fwd_b, fwd_f
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                "traffic": measured_traffic(dom), "algorithmic_bytes": dom_bytes,
                 "call": dom, "call_ms": round(dom_ms, 5),
                 "mfma_frac": round(dom_flops / (dom_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 6)}
 
