@@ -188,10 +188,38 @@ def time_calls(fn, steps: int, reps: int = 20) -> float:
     return total / (n * reps)
 
 
-def profile_calls(n: int) -> None:
+def profile_calls(n: int, workload: str = "cfg2") -> None:
+    """Run n calls of each library entry point of a workload (for rocprofv3
+    counter passes); cfg2 also runs a calibration copy of COPY_BYTES."""
     from natten_amd._core import hip
 
     q, k, v, do = make_inputs(torch.device("cuda:0"))
+    if workload == "split":
+        a = ((K, K), (1, 1), (1, 1), (False, False))
+        logits = hip.qk_forward(q, k, *a, None)
+        attn = torch.softmax(logits, -1)
+        for _ in range(n):
+            hip.qk_forward(q, k, *a, None)
+            hip.av_forward(attn, v, *a)
+            hip.qk_backward(q, k, attn, *a, None)
+            hip.av_backward(attn, v, do, *a)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x split qk/av forward and backward done", flush=True)
+        return
+    if workload == "cfg5":
+        Bc, L, H, Dc = 8, 2048, 12, 12
+        qa, ka, va = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
+        rpb = _gen((H, 13), torch.float32, 17, std=0.02)
+        logits = hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
+        attn = torch.softmax(logits, -1)
+        for _ in range(n):
+            hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
+            hip.rpb_av_forward(attn, va, 7, 1)
+            hip.rpb_qk_backward(qa, ka, attn, 7, 1, 0.288)
+            hip.rpb_av_backward(attn, va, va, 7, 1)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x allin1 K=7 d=1 forward and backward done", flush=True)
+        return
     a = ((K, K), (1, 1), (1, 1), (False, False), None)
     out, lse = hip.fused_forward(q, k, v, *a)
     # calibration for the HBM byte counters: a plain device copy of a known
@@ -437,8 +465,9 @@ def main(argv=None):
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-calls", type=int, default=0, metavar="N",
-                    help="only run N fused forward and N fused backward calls at the "
-                         "dilation-1 workload (for rocprofv3 --pmc passes), then exit")
+                    help="only run N calls of each library entry point of --workload "
+                         "(cfg2: fused forward/backward at dilation 1; split; cfg5) for "
+                         "rocprofv3 passes, then exit")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
                     help="cfg2 (default) is the driver's bench line; the others measure the "
                          "remaining BASELINE.json configurations")
@@ -453,7 +482,7 @@ def main(argv=None):
         return 2
 
     if args.profile_calls > 0:
-        profile_calls(args.profile_calls)
+        profile_calls(args.profile_calls, args.workload)
         return 0
     if args.workload != "cfg2":
         print(json.dumps(WORKLOADS[args.workload](args)), flush=True)

@@ -116,6 +116,10 @@ bool use_mfma(const na_params *p, const na::Prob &P) {
   return (p->flags & NA_FLAG_GENERIC) == 0 && na::mfma_eligible(P, p->dtype);
 }
 
+bool use_msplit(const na_params *p, const na::Prob &P) {
+  return (p->flags & NA_FLAG_GENERIC) == 0 && na::msplit_eligible(P, p->dtype);
+}
+
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 size_t delta_bytes(const na::Prob &P) {
@@ -296,7 +300,11 @@ int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,
   if (P.B == 0) return NA_OK;
   if (q == nullptr || k == nullptr || logits == nullptr)
     return fail(NA_ERR_INVALID, "q/k/logits must be non-NULL");
-  na::valu_qk(P, p->dtype, q, k, logits, as_stream(stream));
+  if (use_msplit(p, P))
+    na::msplit_qk(P, p->dtype, q, k, logits, P.scale, -INFINITY,
+                  as_stream(stream));
+  else
+    na::valu_qk(P, p->dtype, q, k, logits, as_stream(stream));
   return launch_status("na_qk_fwd");
 }
 
@@ -309,7 +317,10 @@ int na_av_fwd(const na_params *p, const void *attn, const void *v, void *out,
   if (P.B == 0) return NA_OK;
   if (attn == nullptr || v == nullptr || out == nullptr)
     return fail(NA_ERR_INVALID, "attn/v/out must be non-NULL");
-  na::valu_av(P, p->dtype, attn, v, out, as_stream(stream));
+  if (use_msplit(p, P))
+    na::msplit_av(P, p->dtype, attn, v, out, 1.f, as_stream(stream));
+  else
+    na::valu_av(P, p->dtype, attn, v, out, as_stream(stream));
   return launch_status("na_av_fwd");
 }
 
@@ -323,7 +334,12 @@ int na_qk_bwd(const na_params *p, const void *q, const void *k,
   if (q == nullptr || k == nullptr || dlogits == nullptr || dq == nullptr ||
       dk == nullptr)
     return fail(NA_ERR_INVALID, "q/k/dlogits/dq/dk must be non-NULL");
-  na::valu_qk_bwd(P, p->dtype, q, k, dlogits, dq, dk, as_stream(stream));
+  if (use_msplit(p, P)) {
+    na::msplit_av(P, p->dtype, dlogits, k, dq, P.scale, as_stream(stream));
+    na::msplit_inv(P, p->dtype, dlogits, q, dk, P.scale, as_stream(stream));
+  } else {
+    na::valu_qk_bwd(P, p->dtype, q, k, dlogits, dq, dk, as_stream(stream));
+  }
   return launch_status("na_qk_bwd");
 }
 
@@ -337,7 +353,12 @@ int na_av_bwd(const na_params *p, const void *attn, const void *v,
   if (attn == nullptr || v == nullptr || dout == nullptr || dattn == nullptr ||
       dv == nullptr)
     return fail(NA_ERR_INVALID, "attn/v/dout/dattn/dv must be non-NULL");
-  na::valu_av_bwd(P, p->dtype, attn, v, dout, dattn, dv, as_stream(stream));
+  if (use_msplit(p, P)) {
+    na::msplit_qk(P, p->dtype, dout, v, dattn, 1.f, 0.f, as_stream(stream));
+    na::msplit_inv(P, p->dtype, attn, dout, dv, 1.f, as_stream(stream));
+  } else {
+    na::valu_av_bwd(P, p->dtype, attn, v, dout, dattn, dv, as_stream(stream));
+  }
   return launch_status("na_av_bwd");
 }
 

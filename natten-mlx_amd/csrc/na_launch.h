@@ -63,6 +63,19 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
               void *dk, void *dv, hipStream_t st);
 void mfma_selftest(int dtype, float *out, hipStream_t st);
 
+// Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with
+// d*K <= L on every non-causal axis and at most 512 kernel slots.
+bool msplit_eligible(const Prob &P, int dtype);
+// out[q, slot] = scale * <x_q, y_key(slot)>, `fill` outside the window.
+void msplit_qk(const Prob &P, int dtype, const void *x, const void *y,
+               void *out, float scale, float fill, hipStream_t st);
+// out_q = scale * sum_slot a[q, slot] * y_key(slot).
+void msplit_av(const Prob &P, int dtype, const void *a, const void *y,
+               void *out, float scale, hipStream_t st);
+// out_key = scale * sum over (q, slot) holding the key of a[q, slot] * x_q.
+void msplit_inv(const Prob &P, int dtype, const void *a, const void *x,
+                void *out, float scale, hipStream_t st);
+
 // Generic pieces reused around the MFMA backward.
 void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
                 const float *dlse, float *delta, hipStream_t st);

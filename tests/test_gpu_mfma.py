@@ -119,3 +119,61 @@ def test_mfma_backward_deterministic():
         res.append([t.grad.clone() for t in ts])
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+SPLIT_CASES = [
+    # (name, B, spatial, H, Hkv, D, ks, dil, caus)
+    ("cfg2s_d1", 4, (56, 56), 4, 4, 32, (7, 7), (1, 1), (False, False)),
+    ("cfg2s_d4", 2, (56, 56), 4, 4, 32, (7, 7), (4, 4), (False, False)),
+    ("2d_gqa_d64", 2, (17, 20), 4, 2, 64, (5, 7), (2, 1), (False, False)),
+    ("3d_causal", 1, (6, 12, 12), 4, 4, 64, (3, 7, 7), (1, 1, 1), (True, False, False)),
+    ("1d_k63_d128", 2, (300,), 2, 1, 128, (63,), (2,), (False,)),
+    ("1d_causal", 2, (70,), 2, 2, 32, (9,), (3,), (True,)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_mfma_split_ops(case, dtype):
+    """Matrix-core split QK / AV forward and backward against the oracle,
+    and the generic kernels on the same inputs against the oracle too."""
+    import natten_amd
+    from natten_amd._core import hip
+
+    name, B, sp, H, Hkv, D, ks, dil, caus = case
+    _say(f"[case] mfma split {name} {dtype}")
+    rank = len(sp)
+    qk = {1: natten_amd.na1d_qk, 2: natten_amd.na2d_qk, 3: natten_amd.na3d_qk}[rank]
+    av = {1: natten_amd.na1d_av, 2: natten_amd.na2d_av, 3: natten_amd.na3d_av}[rank]
+    q = randn((B, *sp, H, D), dtype, 11)
+    k = randn((B, *sp, Hkv, D), dtype, 12)
+    v = randn((B, *sp, Hkv, D), dtype, 13)
+    ref_logits = O.na_qk(q, k, ks, 1, dil, caus, 0.25)
+    finite = torch.isfinite(ref_logits)
+    attn = torch.softmax(ref_logits, -1).to(dtype)
+    gl = randn(ref_logits.shape, dtype, 14)
+    go = randn((B, *sp, H, D), dtype, 15)
+
+    def qk_masked(a, b):
+        x = O.na_qk(a, b, ks, 1, dil, caus, 0.25)
+        return torch.where(finite, x, torch.zeros_like(x))
+
+    rq, rk = O.grads(qk_masked, (q, k), (gl,))
+    ra, rv = O.grads(lambda a, b: O.na_av(a, b, ks, 1, dil, caus), (attn, v), (go,))
+    ref_out = O.na_av(attn, v, ks, 1, dil, caus)
+    for generic in (False, True):
+        tag = f"{name}{' generic' if generic else ''}"
+        with hip.generic_kernels(generic):
+            qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+            logits = qk(qd, kd, ks, dil, is_causal=caus, scale=0.25)
+            assert torch.equal(torch.isinf(logits).cpu(), ~finite), f"{tag} mask"
+            assert_close(logits, ref_logits, dtype, f"{tag} logits")
+            ad = attn.to(DEV).requires_grad_(True)
+            out = av(ad, vd, ks, dil, is_causal=caus)
+            assert_close(out, ref_out, dtype, f"{tag} av")
+            logits.backward(gl.to(DEV))
+            out.backward(go.to(DEV))
+            assert_close(qd.grad, rq, dtype, f"{tag} dq")
+            assert_close(kd.grad, rk, dtype, f"{tag} dk")
+            assert_close(ad.grad, ra, dtype, f"{tag} dattn")
+            assert_close(vd.grad, rv, dtype, f"{tag} dv")
