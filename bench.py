@@ -409,6 +409,13 @@ def wl_cfg5(args):
             if Kx == 7 and d == 1:
                 best = (rq, ra, qk_ms + av_ms, (qk_b + av_b) / ((qk_ms + av_ms) * 1e-3) / 1e9)
     rq, ra, ms, gbs = best
+    # practical ceiling at this size: a device copy moving the same bytes as
+    # one K=7 call (read + write of 12.2 MB)
+    src = torch.empty((rq["bytes"] // 2) // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    copy_ms = time_calls(lambda: dst.copy_(src), args.steps)
+    table["copy_same_bytes"] = {"call_ms": round(copy_ms, 5),
+                                "achieved": round(rq["bytes"] / (copy_ms * 1e-3) / 1e9, 2)}
     cfg = {"workload": "allin1 na1d_qk_rpb + na1d_av_fused fp32 [8,2048,12,12] K=7 d=1 "
                        "(all K x d in 'sweep')", "global_batch": Bc}
     return _line("allin1 qk_rpb+av fp32 HBM GB/s (K=7 d=1), 1 MI355X", gbs, "GB/s", ms, "f32",

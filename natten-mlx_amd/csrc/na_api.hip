@@ -166,6 +166,10 @@ int make_rpb(const na_rpb_params *p, na::RpbProb *A) {
   A->has_scale = p->has_scale ? 1 : 0;
   A->scale = p->scale;
   A->n_rows = (int32_t)rows;
+  A->fH = na::make_fastdiv((uint32_t)A->H);
+  A->fL0 = na::make_fastdiv((uint32_t)A->L0);
+  A->fL1 = na::make_fastdiv((uint32_t)A->L1);
+  A->fdil = na::make_fastdiv((uint32_t)A->dil);
   return NA_OK;
 }
 

@@ -38,6 +38,7 @@ struct RpbProb {
   int32_t has_scale;    // q is scaled (and rounded to its dtype) first
   float scale;
   int32_t n_rows;       // B * H * L0 * L1 (< 2^31)
+  FastDiv fH, fL0, fL1, fdil;  // row decode and window arithmetic
 };
 void rpb_qk_fwd(const RpbProb &A, int dtype, const void *q, const void *key,
                 const float *rpb, float *logits, hipStream_t st);

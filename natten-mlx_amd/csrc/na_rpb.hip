@@ -23,7 +23,8 @@
 namespace na {
 namespace {
 
-constexpr int kNT = 4;  // element chunks per lane
+constexpr int kNT = 4;         // element chunks per lane
+constexpr int kBiasChunk = 16;  // queries per bias-gradient partial
 
 struct RPos {
   int32_t b, h, i0, i1;
@@ -31,20 +32,27 @@ struct RPos {
 
 __device__ __forceinline__ RPos rpos(const RpbProb &A, uint32_t r) {
   RPos p;
+  uint32_t q;
   if (A.heads_first) {
-    p.i1 = (int32_t)(r % (uint32_t)A.L1);
-    r /= (uint32_t)A.L1;
-    p.i0 = (int32_t)(r % (uint32_t)A.L0);
-    r /= (uint32_t)A.L0;
-    p.h = (int32_t)(r % (uint32_t)A.H);
-    p.b = (int32_t)(r / (uint32_t)A.H);
+    q = fdiv(r, A.fL1);
+    p.i1 = (int32_t)(r - q * (uint32_t)A.L1);
+    r = q;
+    q = fdiv(r, A.fL0);
+    p.i0 = (int32_t)(r - q * (uint32_t)A.L0);
+    r = q;
+    q = fdiv(r, A.fH);
+    p.h = (int32_t)(r - q * (uint32_t)A.H);
+    p.b = (int32_t)q;
   } else {
-    p.h = (int32_t)(r % (uint32_t)A.H);
-    r /= (uint32_t)A.H;
-    p.i1 = (int32_t)(r % (uint32_t)A.L1);
-    r /= (uint32_t)A.L1;
-    p.i0 = (int32_t)(r % (uint32_t)A.L0);
-    p.b = (int32_t)(r / (uint32_t)A.L0);
+    q = fdiv(r, A.fH);
+    p.h = (int32_t)(r - q * (uint32_t)A.H);
+    r = q;
+    q = fdiv(r, A.fL1);
+    p.i1 = (int32_t)(r - q * (uint32_t)A.L1);
+    r = q;
+    q = fdiv(r, A.fL0);
+    p.i0 = (int32_t)(r - q * (uint32_t)A.L0);
+    p.b = (int32_t)q;
   }
   return p;
 }
@@ -62,18 +70,42 @@ struct RWin {
   int32_t pb;  // bias row of slot 0 (before clipping)
 };
 
-__device__ __forceinline__ RWin rwin(int32_t i, int32_t L, int32_t K,
-                                     int32_t dil) {
+// Window of position i on an axis of length L: window_start_partition,
+// window_end and pb_start (na_window.h) with the divisions by the dilation
+// done by multiply-shift.
+__device__ __forceinline__ RWin rwin(const RpbProb &A, int32_t i, int32_t L) {
+  const int32_t K = A.K, nh = K / 2, d = A.dil;
   RWin w;
-  w.s = window_start_partition(i, L, K, K / 2, dil);
-  w.e = window_end(w.s, L, K, dil);
-  w.pb = pb_start(i, L, K, K / 2, dil);
+  if (d == 1) {
+    int32_t s = i > nh ? i - nh : 0;
+    if (i + nh >= L) s += L - i - nh - 1;
+    w.s = s;
+    w.e = min(s + K, L);
+    int32_t pb = nh;
+    if (i < nh) pb += nh - i;
+    if (i + nh >= L) pb += L - i - 1 - nh;
+    w.pb = pb;
+    return w;
+  }
+  const int32_t slot = (int32_t)fdiv((uint32_t)i, A.fdil);
+  const int32_t phase = i - slot * d;
+  const int32_t plen = (int32_t)fdiv((uint32_t)(L - 1 - phase), A.fdil) + 1;
+  int32_t s = slot > nh ? slot - nh : 0;
+  if (slot + nh >= plen) s += plen - slot - nh - 1;
+  w.s = s * d + phase;
+  w.e = min(w.s + K * d, L);
+  if (i < nh * d)
+    w.pb = K - 1 - slot;
+  else if (i + nh * d >= L)
+    w.pb = (int32_t)fdiv((uint32_t)(L - i - 1), A.fdil);
+  else
+    w.pb = nh;
   return w;
 }
 
 // Axis-1 window (a single always-valid slot for rank 1).
 __device__ __forceinline__ RWin rwin1(const RpbProb &A, int32_t i1) {
-  if (A.rank == 2) return rwin(i1, A.L1, A.K, A.dil);
+  if (A.rank == 2) return rwin(A, i1, A.L1);
   return RWin{0, 1, 0};
 }
 
@@ -159,69 +191,161 @@ __device__ __forceinline__ void scale_round(float (&v)[kNT][VEC], float s) {
     for (int e = 0; e < VEC; ++e) v[t][e] = round_to<TX>(v[t][e] * s);
 }
 
+
+// Rank 1: the keys (or values) of every row of a block lie within K*dil
+// positions of the block's rows, i.e. in the row range [lo, hi) below;
+// the block copies that range into LDS with contiguous 16-byte loads
+// (`ystage`) so the per-slot row reads hit LDS.  Returns lo.
+template <typename T>
+__device__ __forceinline__ int64_t stage_window(const RpbProb &A, const T *y,
+                                                T *ystage, int lgG) {
+  const int64_t step = A.heads_first ? 1 : A.H;
+  const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
+  const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
+  const int64_t reach = (int64_t)A.K * A.dil * step;
+  const int64_t lo = max((int64_t)0, row0 - reach);
+  const int64_t hi = min((int64_t)A.n_rows, row0 + rows + reach);
+  const int64_t n16 = (hi - lo) * A.D * (int64_t)sizeof(T) / 16;
+  const uint4 *src = reinterpret_cast<const uint4 *>(y + lo * A.D);
+  uint4 *dst = reinterpret_cast<uint4 *>(ystage);
+  for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+  __syncthreads();
+  return lo;
+}
+
+// Rows of the staged window per block (bounds the LDS it needs).
+inline int64_t window_rows(const RpbProb &A, int lgG) {
+  const int64_t step = A.heads_first ? 1 : A.H;
+  return (256 >> lgG) + 2 * (int64_t)A.K * A.dil * step;
+}
+
 // ---- kernels ---------------------------------------------------------------
 
 // out[r, n] = <x'[r], y[nbr(r, n)]> (+ bias) for valid slots, `fill` for
 // invalid ones; x' = round(x * scale) when scale_x.  QK+RPB forward
 // (x = q, y = key, fill = -inf) and the AV backward's dattn (x = dout,
 // y = value, no bias, fill = 0).
-template <typename TX, typename TY, int VEC>
+template <typename TX, typename TY, int VEC, bool YS>
 __global__ void __launch_bounds__(256)
     k_rpb_dot(RpbProb A, const TX *__restrict__ x, const TY *__restrict__ y,
               const float *__restrict__ rpb, float *__restrict__ out,
-              int scale_x, float fill, int G, int lgG) {
+              int scale_x, float fill, int staged, int G, int lgG) {
   const Group g = make_group(lgG, A.n_rows);
   const RPos p = rpos(A, (uint32_t)g.id);
   float xv[kNT][VEC];
   ld_row<TX, VEC>(xv, x + g.id * A.D, g.lane, G, A.D);
   if (scale_x) scale_round<TX, VEC>(xv, A.scale);
-  const RWin w0 = rwin(p.i0, A.L0, A.K, A.dil);
+  const RWin w0 = rwin(A, p.i0, A.L0);
   const RWin w1 = rwin1(A, p.i1);
-  float *dst = out + g.id * A.KK;
-  int n = 0;
-  for (int k0 = 0; k0 < A.K; ++k0) {
-    const int32_t j0 = w0.s + k0 * A.dil;
-    const bool v0 = j0 >= 0 && j0 < w0.e;
-    for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
-      const int32_t j1 = w1.s + k1 * A.dil;
-      float s = fill;
-      if (v0 && j1 >= 0 && j1 < w1.e) {
-        const TY *yr = y + rrow(A, p.b, p.h, j0, j1) * A.D;
-        s = group_sum(dot_row<TY, VEC>(xv, yr, g.lane, G, A.D), G);
-        if (rpb != nullptr) s += rpb[bias_index(A, p.h, w0.pb + k0, w1.pb + k1)];
-      }
-      if (g.live && g.lane == 0) dst[n] = s;
+  // rows of this block are consecutive in memory: stage them in LDS and
+  // write the block's slot values as one contiguous range
+  extern __shared__ __align__(16) float stage[];
+  const int lrow = (int)(threadIdx.x >> lgG);
+  float *dst = staged ? stage + lrow * A.KK : out + g.id * A.KK;
+  if (A.rank == 1) {
+    // one axis: the row of key position j is this row + (j - i) * step
+    const int64_t step = A.heads_first ? 1 : A.H;
+    const float *rb = rpb != nullptr ? rpb + p.h * A.R : nullptr;
+    const TY *ybase = y;
+    int64_t ylo = 0;
+    if constexpr (YS) {
+      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (256 >> lgG) * A.KK : 0));
+      ylo = stage_window<TY>(A, y, ys, lgG);
+      ybase = ys;
     }
+    for (int k0 = 0; k0 < A.K; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.dil;
+      float s = fill;
+      if (j0 >= 0 && j0 < w0.e) {
+        const TY *yr = ybase + (g.id - ylo + (int64_t)(j0 - p.i0) * step) * A.D;
+        s = group_sum(dot_row<TY, VEC>(xv, yr, g.lane, G, A.D), G);
+        if (rb != nullptr) s += rb[clampi(w0.pb + k0, 0, A.R - 1)];
+      }
+      if (g.live && g.lane == 0) dst[k0] = s;
+    }
+  } else {
+    int n = 0;
+    for (int k0 = 0; k0 < A.K; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.dil;
+      const bool v0 = j0 >= 0 && j0 < w0.e;
+      for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
+        const int32_t j1 = w1.s + k1 * A.dil;
+        float s = fill;
+        if (v0 && j1 >= 0 && j1 < w1.e) {
+          const TY *yr = y + rrow(A, p.b, p.h, j0, j1) * A.D;
+          s = group_sum(dot_row<TY, VEC>(xv, yr, g.lane, G, A.D), G);
+          if (rpb != nullptr) s += rpb[bias_index(A, p.h, w0.pb + k0, w1.pb + k1)];
+        }
+        if (g.live && g.lane == 0) dst[n] = s;
+      }
+    }
+  }
+  if (staged) {
+    __syncthreads();
+    const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
+    const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
+    const int64_t nv = rows * A.KK;
+    float *o = out + row0 * A.KK;
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) o[i] = stage[i];
   }
 }
 
 // out[r] = post * sum_n w[r, n] * y[nbr(r, n)] over valid slots.  AV
 // forward (w = attn, y = value) and the QK backward's dq (w = dlogits,
 // y = key, post = the query scale).
-template <typename TY, typename TO, int VEC>
+template <typename TY, typename TO, int VEC, bool YS>
 __global__ void __launch_bounds__(256)
     k_rpb_gather(RpbProb A, const float *__restrict__ w,
                  const TY *__restrict__ y, TO *__restrict__ out, float post,
-                 int G, int lgG) {
+                 int staged, int G, int lgG) {
   const Group g = make_group(lgG, A.n_rows);
   const RPos p = rpos(A, (uint32_t)g.id);
-  const RWin w0 = rwin(p.i0, A.L0, A.K, A.dil);
+  const RWin w0 = rwin(A, p.i0, A.L0);
   const RWin w1 = rwin1(A, p.i1);
+  // the block's weight rows are one contiguous range: read it coalesced
+  extern __shared__ __align__(16) float stage[];
   const float *wr = w + g.id * A.KK;
+  if (staged) {
+    const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
+    const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
+    const int64_t nv = rows * A.KK;
+    const float *src = w + row0 * A.KK;
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) stage[i] = src[i];
+    __syncthreads();
+    wr = stage + (int)(threadIdx.x >> lgG) * A.KK;
+  }
   float acc[kNT][VEC];
 #pragma unroll
   for (int t = 0; t < kNT; ++t)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[t][e] = 0.f;
-  int n = 0;
-  for (int k0 = 0; k0 < A.K; ++k0) {
-    const int32_t j0 = w0.s + k0 * A.dil;
-    const bool v0 = j0 >= 0 && j0 < w0.e;
-    for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
-      const int32_t j1 = w1.s + k1 * A.dil;
-      if (v0 && j1 >= 0 && j1 < w1.e)
-        axpy_row<TY, VEC>(acc, wr[n], y + rrow(A, p.b, p.h, j0, j1) * A.D,
+  if (A.rank == 1) {
+    const int64_t step = A.heads_first ? 1 : A.H;
+    const TY *ybase = y;
+    int64_t ylo = 0;
+    if constexpr (YS) {
+      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (256 >> lgG) * A.KK : 0));
+      ylo = stage_window<TY>(A, y, ys, lgG);
+      ybase = ys;
+    }
+    for (int k0 = 0; k0 < A.K; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.dil;
+      if (j0 >= 0 && j0 < w0.e)
+        axpy_row<TY, VEC>(acc, wr[k0],
+                          ybase + (g.id - ylo + (int64_t)(j0 - p.i0) * step) * A.D,
                           g.lane, G, A.D);
+    }
+  } else {
+    int n = 0;
+    for (int k0 = 0; k0 < A.K; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.dil;
+      const bool v0 = j0 >= 0 && j0 < w0.e;
+      for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
+        const int32_t j1 = w1.s + k1 * A.dil;
+        if (v0 && j1 >= 0 && j1 < w1.e)
+          axpy_row<TY, VEC>(acc, wr[n], y + rrow(A, p.b, p.h, j0, j1) * A.D,
+                            g.lane, G, A.D);
+      }
     }
   }
   if (g.live) st_row<TO, VEC>(out + g.id * A.D, acc, post, g.lane, G, A.D);
@@ -249,7 +373,7 @@ __global__ void __launch_bounds__(256)
   for (int32_t t0 = -A.K; t0 <= A.K; ++t0) {
     const int32_t i0 = p.i0 + t0 * A.dil;
     if (i0 < 0 || i0 >= A.L0) continue;
-    const RWin w0 = rwin(i0, A.L0, A.K, A.dil);
+    const RWin w0 = rwin(A, i0, A.L0);
     if (p.i0 < w0.s || p.i0 >= w0.e) continue;
     const int32_t k0 = (p.i0 - w0.s) / A.dil;
     for (int32_t t1 = -t1max; t1 <= t1max; ++t1) {
@@ -284,61 +408,77 @@ __device__ __forceinline__ void slots_of_bias_row(int32_t r, int32_t pb,
   *hi = b > K - 1 ? K - 1 : b;
 }
 
-// Bias gradient, pass 1: partial[c, h, bin] = sum of dlogits over the
-// queries of chunk c (rows in (b, i0, i1) order) and the slots whose
-// clipped bias row is `bin`.  One thread per (c, h, bin), fixed order.
+// Bias gradient, pass 1: one block per chunk of `chunk` queries (rows in
+// (b, i0, i1) order).  The chunk's windows are computed once into LDS; then
+// thread t owns bins t, t + 256, ... (bin = (h, r0[, r1])) and sums, in
+// query order, dlogits over the slots whose clipped bias row is the bin.
+// partial is output-major, partial[bin * n_chunks + c], so pass 2 reads
+// each bin's partials contiguously.
 __global__ void __launch_bounds__(256)
     k_rpb_bias_partial(RpbProb A, const float *__restrict__ dl,
                        float *__restrict__ partial, int32_t chunk,
                        int32_t n_chunks) {
-  const int32_t nb = A.rank == 2 ? A.R * A.R : A.R;
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= (int64_t)n_chunks * A.H * nb) return;
-  const int32_t bin = (int32_t)(id % nb);
-  const int32_t h = (int32_t)((id / nb) % A.H);
-  const int32_t c = (int32_t)(id / ((int64_t)nb * A.H));
-  const int32_t r0 = A.rank == 2 ? bin / A.R : bin;
-  const int32_t r1 = A.rank == 2 ? bin % A.R : 0;
+  __shared__ RWin sw0[kBiasChunk], sw1[kBiasChunk];
+  __shared__ int32_t sb[kBiasChunk], si0[kBiasChunk], si1[kBiasChunk];
+  const int32_t c = blockIdx.x;
   const int32_t nq = A.B * A.L0 * A.L1;
   const int32_t q0 = c * chunk;
-  const int32_t q1 = q0 + chunk < nq ? q0 + chunk : nq;
-  float acc = 0.f;
-  for (int32_t qi = q0; qi < q1; ++qi) {
-    const int32_t i1 = qi % A.L1;
-    const int32_t rest = qi / A.L1;
-    const int32_t i0 = rest % A.L0;
-    const int32_t b = rest / A.L0;
-    const RWin w0 = rwin(i0, A.L0, A.K, A.dil);
-    int32_t a0, b0;
-    slots_of_bias_row(r0, w0.pb, A.K, A.R, &a0, &b0);
-    if (a0 > b0) continue;
-    const RWin w1 = rwin1(A, i1);
-    int32_t a1 = 0, b1 = 0;
-    if (A.rank == 2) slots_of_bias_row(r1, w1.pb, A.K, A.R, &a1, &b1);
-    const float *row = dl + rrow(A, b, h, i0, i1) * A.KK;
-    for (int32_t k0 = a0; k0 <= b0; ++k0) {
-      const int32_t j0 = w0.s + k0 * A.dil;
-      if (j0 < 0 || j0 >= w0.e) continue;
-      for (int32_t k1 = a1; k1 <= b1; ++k1) {
-        const int32_t j1 = w1.s + k1 * A.dil;
-        if (j1 < 0 || j1 >= w1.e) continue;
-        acc += row[k0 * A.K1 + k1];
+  const int32_t nqc = min(chunk, nq - q0);
+  const int tid = threadIdx.x;
+  if (tid < nqc) {
+    const int32_t qi = q0 + tid;
+    const int32_t rest = (int32_t)fdiv((uint32_t)qi, A.fL1);
+    const int32_t i1 = qi - rest * A.L1;
+    const int32_t b = (int32_t)fdiv((uint32_t)rest, A.fL0);
+    const int32_t i0 = rest - b * A.L0;
+    sw0[tid] = rwin(A, i0, A.L0);
+    sw1[tid] = rwin1(A, i1);
+    sb[tid] = b;
+    si0[tid] = i0;
+    si1[tid] = i1;
+  }
+  __syncthreads();
+  const int32_t nb = A.H * (A.rank == 2 ? A.R * A.R : A.R);
+  for (int32_t bin = tid; bin < nb; bin += blockDim.x) {
+    const int32_t per_h = A.rank == 2 ? A.R * A.R : A.R;
+    const int32_t h = bin / per_h;
+    const int32_t rb = bin - h * per_h;
+    const int32_t r0 = A.rank == 2 ? rb / A.R : rb;
+    const int32_t r1 = A.rank == 2 ? rb - r0 * A.R : 0;
+    float acc = 0.f;
+    for (int32_t t = 0; t < nqc; ++t) {
+      const RWin w0 = sw0[t];
+      int32_t a0, b0;
+      slots_of_bias_row(r0, w0.pb, A.K, A.R, &a0, &b0);
+      if (a0 > b0) continue;
+      const RWin w1 = sw1[t];
+      int32_t a1 = 0, b1 = 0;
+      if (A.rank == 2) slots_of_bias_row(r1, w1.pb, A.K, A.R, &a1, &b1);
+      const float *row = dl + rrow(A, sb[t], h, si0[t], si1[t]) * A.KK;
+      for (int32_t k0 = a0; k0 <= b0; ++k0) {
+        const int32_t j0 = w0.s + k0 * A.dil;
+        if (j0 < 0 || j0 >= w0.e) continue;
+        for (int32_t k1 = a1; k1 <= b1; ++k1) {
+          const int32_t j1 = w1.s + k1 * A.dil;
+          if (j1 < 0 || j1 >= w1.e) continue;
+          acc += row[k0 * A.K1 + k1];
+        }
       }
     }
+    partial[(int64_t)bin * n_chunks + c] = acc;
   }
-  partial[id] = acc;
 }
 
-// Bias gradient, pass 2: one wavefront per (h, bin) sums the chunk
-// partials, lane l taking chunks l, l+64, ... and a fixed xor tree after.
+// Bias gradient, pass 2: one wavefront per bin sums its chunk partials,
+// lane l taking chunks l, l+64, ... and a fixed xor tree after.
 __global__ void __launch_bounds__(64)
     k_rpb_bias_reduce(const float *__restrict__ partial, int32_t n_chunks,
-                      int32_t n_out, float *__restrict__ drpb) {
+                      float *__restrict__ drpb) {
   const int32_t o = blockIdx.x;
   const int lane = threadIdx.x;
+  const float *src = partial + (int64_t)o * n_chunks;
   float acc = 0.f;
-  for (int32_t c = lane; c < n_chunks; c += 64)
-    acc += partial[(int64_t)c * n_out + o];
+  for (int32_t c = lane; c < n_chunks; c += 64) acc += src[c];
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (lane == 0) drpb[o] = acc;
 }
@@ -375,20 +515,45 @@ constexpr int vmax_of() {
   return 16 / (int)(sizeof(A_) > sizeof(B_) ? sizeof(A_) : sizeof(B_));
 }
 
+// LDS for a block's slot rows (256 / G rows of KK floats), or 0 when that
+// exceeds 32 KB and the rows go straight to memory.
+size_t stage_bytes(const RpbProb &A, int lgG) {
+  const size_t b = (size_t)(256 >> lgG) * A.KK * sizeof(float);
+  return b <= 32768 ? b : 0;
+}
+
+// LDS of the staged neighbor window (rank 1), or 0 when it is not used:
+// rows must be whole 16-byte units, the halo at most the block's rows and
+// the window must fit with the slot staging in 64 KB.
+template <typename TY>
+size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes) {
+  if (A.rank != 1 || (A.D * sizeof(TY)) % 16 != 0) return 0;
+  // only worth it while the halo is no larger than the block's own rows
+  // (large dilations would mostly copy other phases' rows)
+  if (window_rows(A, lgG) > 2 * (int64_t)(256 >> lgG)) return 0;
+  const size_t b = (size_t)window_rows(A, lgG) * A.D * sizeof(TY);
+  return slot_bytes + b <= 65536 ? b : 0;
+}
+
 template <typename TX, typename TY>
 void launch_dot(const RpbProb &A, const void *x, const void *y,
                 const float *rpb, float *out, int scale_x, float fill,
                 hipStream_t st) {
   constexpr int V = vmax_of<TX, TY>();
   const RShape s = rshape(A.D, V);
-  if (s.vec == V)
-    hipLaunchKernelGGL((k_rpb_dot<TX, TY, V>), rgrid(A, s.lgG), dim3(256), 0,
-                       st, A, (const TX *)x, (const TY *)y, rpb, out, scale_x,
-                       fill, s.G, s.lgG);
-  else
-    hipLaunchKernelGGL((k_rpb_dot<TX, TY, 1>), rgrid(A, s.lgG), dim3(256), 0,
-                       st, A, (const TX *)x, (const TY *)y, rpb, out, scale_x,
-                       fill, s.G, s.lgG);
+  const size_t lds = stage_bytes(A, s.lgG);
+  const int staged = lds > 0;
+  const size_t wb = window_bytes<TY>(A, s.lgG, lds);
+#define DOT_(VV, YS)                                                          \
+  hipLaunchKernelGGL((k_rpb_dot<TX, TY, VV, YS>), rgrid(A, s.lgG), dim3(256), \
+                     lds + wb, st, A, (const TX *)x, (const TY *)y, rpb, out,  \
+                     scale_x, fill, staged, s.G, s.lgG)
+  if (s.vec == V) {
+    if (wb > 0) DOT_(V, true); else DOT_(V, false);
+  } else {
+    if (wb > 0) DOT_(1, true); else DOT_(1, false);
+  }
+#undef DOT_
 }
 
 template <typename TY, typename TO>
@@ -396,12 +561,19 @@ void launch_gather(const RpbProb &A, const float *w, const void *y, void *out,
                    float post, hipStream_t st) {
   constexpr int V = vmax_of<TY, TO>();
   const RShape s = rshape(A.D, V);
-  if (s.vec == V)
-    hipLaunchKernelGGL((k_rpb_gather<TY, TO, V>), rgrid(A, s.lgG), dim3(256),
-                       0, st, A, w, (const TY *)y, (TO *)out, post, s.G, s.lgG);
-  else
-    hipLaunchKernelGGL((k_rpb_gather<TY, TO, 1>), rgrid(A, s.lgG), dim3(256),
-                       0, st, A, w, (const TY *)y, (TO *)out, post, s.G, s.lgG);
+  const size_t lds = stage_bytes(A, s.lgG);
+  const int staged = lds > 0;
+  const size_t wb = window_bytes<TY>(A, s.lgG, lds);
+#define GAT_(VV, YS)                                                          \
+  hipLaunchKernelGGL((k_rpb_gather<TY, TO, VV, YS>), rgrid(A, s.lgG),         \
+                     dim3(256), lds + wb, st, A, w, (const TY *)y, (TO *)out,  \
+                     post, staged, s.G, s.lgG)
+  if (s.vec == V) {
+    if (wb > 0) GAT_(V, true); else GAT_(V, false);
+  } else {
+    if (wb > 0) GAT_(1, true); else GAT_(1, false);
+  }
+#undef GAT_
 }
 
 template <typename TX, typename TO>
@@ -430,16 +602,11 @@ void with_dtype(int dt, F &&f) {
     f(bf16_t{});
 }
 
-// Chunk of queries per bias-gradient partial: about 2^18 threads in pass 1.
+// Queries per bias-gradient partial (one pass-1 block each).
 void bias_chunking(const RpbProb &A, int32_t *chunk, int32_t *n_chunks) {
-  const int64_t nb = (int64_t)A.H * (A.rank == 2 ? A.R * A.R : A.R);
   const int64_t nq = (int64_t)A.B * A.L0 * A.L1;
-  int64_t want = ((int64_t)1 << 18) / (nb > 0 ? nb : 1);
-  if (want < 1) want = 1;
-  int64_t c = (nq + want - 1) / want;
-  if (c < 16) c = 16;
-  *chunk = (int32_t)c;
-  *n_chunks = (int32_t)((nq + c - 1) / c);
+  *chunk = kBiasChunk;
+  *n_chunks = (int32_t)((nq + kBiasChunk - 1) / kBiasChunk);
 }
 
 }  // namespace
@@ -485,13 +652,11 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     int32_t chunk, n_chunks;
     bias_chunking(A, &chunk, &n_chunks);
     const int32_t nb = A.H * (A.rank == 2 ? A.R * A.R : A.R);
-    const int64_t n1 = (int64_t)n_chunks * nb;
-    if (n1 > 0)
-      hipLaunchKernelGGL(k_rpb_bias_partial,
-                         dim3((unsigned)((n1 + 255) / 256)), dim3(256), 0, st,
-                         A, dlogits, workspace, chunk, n_chunks);
+    if (n_chunks > 0)
+      hipLaunchKernelGGL(k_rpb_bias_partial, dim3((unsigned)n_chunks), dim3(256),
+                         0, st, A, dlogits, workspace, chunk, n_chunks);
     hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)nb), dim3(64), 0, st,
-                       (const float *)workspace, n_chunks, nb, drpb);
+                       (const float *)workspace, n_chunks, drpb);
   }
 }
 
