@@ -206,8 +206,9 @@ __device__ __forceinline__ void fwd_group(Softmax<D / 32> &st,
   }
 }
 
-// Forward.
-template <typename T, int D>
+// Forward.  GROUPED: the tile's box fits one group of chunks (see
+// fwd_group); otherwise chunks are software-pipelined one ahead.
+template <typename T, int D, bool GROUPED>
 __global__ void __launch_bounds__(256)
     k_mfwd(Prob P, Tiling Tl, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
@@ -241,27 +242,64 @@ __global__ void __launch_bounds__(256)
   st.m = -INFINITY;
   st.l = 0.f;
 
-  // box chunks c = w, w + W, ... in groups of NB: a group's K/V loads are
-  // all issued before its first chunk computes, so each group waits on
-  // memory once (a 7x7 window's tile has 5 chunks: one group)
-  constexpr int NB = group_chunks(D);
   const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
   RowCursor rc{0, 0, 0};
-  const int n_own = uni(Q.nbox > w ? (Q.nbox - w + W - 1) / W : 0);
-  for (int i0 = 0; i0 < n_own; i0 += NB) {
-    ChunkRows cr[NB];
-    v8 kg[NB][NK], vg[NB][NK];
+  if constexpr (GROUPED) {
+    // the whole box in one group of NB chunks (c = w, w + W, ...): every
+    // K/V load is issued before the first chunk computes, then the
+    // two-phase group softmax
+    constexpr int NB = group_chunks(D);
+    const int n_own = uni(Q.nbox > w ? (Q.nbox - w + W - 1) / W : 0);
+    for (int i0 = 0; i0 < n_own; i0 += NB) {
+      ChunkRows cr[NB];
+      v8 kg[NB][NK], vg[NB][NK];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      if (i0 + j >= n_own) break;
-      const int c = w + W * (i0 + j);
-      cr[j] = chunk_rows(rc, Q.bx, 32 * c);
-      int e[3];
-      box_point(Q.bx, cr[j], 32 * c, n, e);
-      const int off = box_off(ka, e);
-      load_kv<T, D>(k + ka.base + off, v + ka.base + off, kg[j], vg[j], h);
+      for (int j = 0; j < NB; ++j) {
+        if (i0 + j >= n_own) break;
+        const int c = w + W * (i0 + j);
+        cr[j] = chunk_rows(rc, Q.bx, 32 * c);
+        int e[3];
+        box_point(Q.bx, cr[j], 32 * c, n, e);
+        const int off = box_off(ka, e);
+        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kg[j], vg[j], h);
+      }
+      fwd_group<T, D, NB>(st, qf, kg, vg, cr, Q, w, W, i0, n_own, sl2, vt, n, h);
     }
-    fwd_group<T, D, NB>(st, qf, kg, vg, cr, Q, w, W, i0, n_own, sl2, vt, n, h);
+  } else {
+    // software-pipelined chunks: the next chunk's K/V loads are in flight
+    // while the current chunk computes
+    int c = w;
+    ChunkRows cr{0, 0, 0};
+    v8 kf[NK], vf[NK];
+    if (c < Q.nbox) {
+      cr = chunk_rows(rc, Q.bx, 32 * c);
+      int e[3];
+      box_point(Q.bx, cr, 32 * c, n, e);
+      const int off = box_off(ka, e);
+      load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
+    }
+    while (c < Q.nbox) {
+      const int cn = c + W;
+      ChunkRows crn = cr;
+      v8 kn[NK], vn[NK];
+      if (cn < Q.nbox) {
+        crn = chunk_rows(rc, Q.bx, 32 * cn);
+        int e[3];
+        box_point(Q.bx, crn, 32 * cn, n, e);
+        const int off = box_off(ka, e);
+        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kn, vn, h);
+      }
+      bool ok[16];
+      chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
+      fwd_compute<T, D>(st, qf, kf, vf, ok, sl2, vt, n, h);
+      c = cn;
+      cr = crn;
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        kf[t] = kn[t];
+        vf[t] = vn[t];
+      }
+    }
   }
   v8 kf[NK], vf[NK];
   for (int cx = first_owned(Q.nbox, w, W); cx < Q.nbox + Q.nextra; cx += W) {
@@ -717,6 +755,10 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 // Host side: LDS sizes, eligibility, launch.
 
+// Waves up to which the whole forward launch is resident at once (two per
+// SIMD on 256 CUs x 4 SIMDs at the grouped kernel's register use).
+constexpr int64_t kGroupedMaxWaves = 2048;
+
 size_t fwd_lds(int D, int W, int esize) {
   const size_t tr = (size_t)W * D * group_row(group_chunks(D)) * esize;
   const size_t cb = (size_t)(W - 1) * (D * 32 + 64) * sizeof(float);
@@ -765,18 +807,27 @@ void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
   if (Tl.n_q == 0) return;
   const int W = waves_for(chunks, 4, "NATTEN_AMD_FWD_WAVES");
   const size_t lds = fwd_lds(P.D, W, 2);
-#define FWD_(DD)                                                             \
-  if (dtype == NA_BF16)                                                      \
-    hipLaunchKernelGGL((k_mfwd<bf16_t, DD>), dim3(Tl.n_launch), dim3(64 * W), \
-                       lds, st, P, Tl, (const bf16_t *)q, (const bf16_t *)k, \
-                       (const bf16_t *)v, (const bf16_t *)ek,                \
-                       (const bf16_t *)ev, (bf16_t *)out, lse);              \
-  else                                                                       \
-    hipLaunchKernelGGL((k_mfwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64 * W),  \
-                       lds, st, P, Tl, (const f16_t *)q, (const f16_t *)k,   \
-                       (const f16_t *)v, (const f16_t *)ek,                  \
-                       (const f16_t *)ev, (f16_t *)out, lse)
+  // The grouped kernel trades occupancy (more VGPRs) for one memory wait
+  // per tile: a gain only while the launch is a single round of waves.
+  // Box chunks per tile (the cost model's count includes additional tokens):
+  const double box_chunks = chunks - std::ceil(P.n_extra / 32.0);
+#define FWD_(DD)                                                               \
+  do {                                                                         \
+    const bool grouped = std::ceil(box_chunks / W) <= group_chunks(DD) &&      \
+                         (int64_t)Tl.n_q * W <= kGroupedMaxWaves;              \
+    if (dtype == NA_BF16) {                                                    \
+      if (grouped) FWD_LAUNCH(bf16_t, DD, true); else FWD_LAUNCH(bf16_t, DD, false); \
+    } else {                                                                   \
+      if (grouped) FWD_LAUNCH(f16_t, DD, true); else FWD_LAUNCH(f16_t, DD, false); \
+    }                                                                          \
+  } while (0)
+#define FWD_LAUNCH(TT, DD, GG)                                                 \
+  hipLaunchKernelGGL((k_mfwd<TT, DD, GG>), dim3(Tl.n_launch), dim3(64 * W),   \
+                     lds, st, P, Tl, (const TT *)q, (const TT *)k,             \
+                     (const TT *)v, (const TT *)ek, (const TT *)ev, (TT *)out, \
+                     lse)
   NA_MFMA_D(P.D, FWD_);
+#undef FWD_LAUNCH
 #undef FWD_
 }
 
