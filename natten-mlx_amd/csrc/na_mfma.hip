@@ -54,6 +54,19 @@ __global__ void __launch_bounds__(64) k_selftest(float *out) {
 // with its own LDS transpose buffer, and the partial results are combined
 // in LDS in wave order at the end (deterministic).  Inside the chunk loops a
 // wave only synchronises with itself.
+// Backward chunk loops without next-chunk prefetch at head_dim 32: there the
+// registers the prefetch needs would cost the kernel a wave per SIMD
+// (123 VGPRs: four waves, all of config 2's 3136 waves resident at once).
+constexpr bool kLeanBwd(int D) { return D == 32; }
+
+// LDS row stride (elements) of a dK/dV tile's K / V rows: 16 bytes of skew.
+constexpr int kKvRow(int D) { return D + 8; }
+// Per-wave LDS of the backward: two transposed chunks, lse / delta of a
+// chunk, and (lean variant) the dK/dV tile's K and V rows.
+constexpr int bwd_wave_lds(int D, int esize) {
+  return 2 * D * kRow * esize + 256 + (kLeanBwd(D) ? 2 * 32 * kKvRow(D) * esize : 0);
+}
+
 // Chunks of K/V rows a wave loads together (registers: 16*D/8 per chunk).
 constexpr int group_chunks(int D) { return D == 32 ? 6 : D == 64 ? 3 : 2; }
 // LDS row stride (elements) of a group's V^T: 32 per chunk plus 4 of skew.
@@ -471,11 +484,12 @@ __global__ void __launch_bounds__(256)
   const int role = tile - (int)grp * (P.rep + 1);
   TileCtx tcg = decode_tile(P, Tl, (int)grp, Tl.fHk);
   // per-wave scratch: two transposed chunks + per-query lse / delta
-  char *mys = smem + w * (2 * D * kRow * (int)sizeof(E) + 256);
+  char *mys = smem + w * bwd_wave_lds(D, (int)sizeof(E));
   E *ta = reinterpret_cast<E *>(mys);                 // K^T (dQ) or Q^T (dK/dV)
   E *tb = ta + D * kRow;                              // dO^T (dK/dV)
   float *s_lse = reinterpret_cast<float *>(tb + D * kRow);
   float *s_del = s_lse + 32;
+  E *kvs = reinterpret_cast<E *>(s_del + 32);         // K, V rows of a dK/dV tile
   const float sl2 = P.scale * kLog2e;
 
   if (role < P.rep) {
@@ -503,38 +517,56 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[0][c] = zero16();
 
-    const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
-    RowCursor rc{0, 0, 0};
-    int c = w;
-    ChunkRows cr{0, 0, 0};
     v8 kf[NK], vf[NK];
-    if (c < Q.nbox) {
-      cr = chunk_rows(rc, Q.bx, 32 * c);
-      int e[3];
-      box_point(Q.bx, cr, 32 * c, n, e);
-      const int off = box_off(ka, e);
-      load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
-    }
-    while (c < Q.nbox) {
-      const int cn = c + W;
-      ChunkRows crn = cr;
-      v8 kn[NK], vn[NK];
-      if (cn < Q.nbox) {
-        crn = chunk_rows(rc, Q.bx, 32 * cn);
+    if constexpr (kLeanBwd(D)) {
+      // box chunks, loaded when used (see the dK/dV role on occupancy)
+      const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
+      RowCursor rc{0, 0, 0};
+      for (int c = w; c < Q.nbox; c += W) {
+        const ChunkRows cr = chunk_rows(rc, Q.bx, 32 * c);
         int e[3];
-        box_point(Q.bx, crn, 32 * cn, n, e);
+        box_point(Q.bx, cr, 32 * c, n, e);
         const int off = box_off(ka, e);
-        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kn, vn, h);
+        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
+        bool ok[16];
+        chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
+        dq_compute<T, D>(acc[0], qf, df, kf, vf, ok, sl2, lse2, dl, ta, n, h);
       }
-      bool ok[16];
-      chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
-      dq_compute<T, D>(acc[0], qf, df, kf, vf, ok, sl2, lse2, dl, ta, n, h);
-      c = cn;
-      cr = crn;
+    } else {
+      // software-pipelined chunks: the next chunk's K/V loads are in flight
+      // while the current chunk computes
+      const BoxAddr ka = box_addr(P, Q.tc, Q.bx, hk, P.Hkv);
+      RowCursor rc{0, 0, 0};
+      int c = w;
+      ChunkRows cr{0, 0, 0};
+      if (c < Q.nbox) {
+        cr = chunk_rows(rc, Q.bx, 32 * c);
+        int e[3];
+        box_point(Q.bx, cr, 32 * c, n, e);
+        const int off = box_off(ka, e);
+        load_kv<T, D>(k + ka.base + off, v + ka.base + off, kf, vf, h);
+      }
+      while (c < Q.nbox) {
+        const int cn = c + W;
+        ChunkRows crn = cr;
+        v8 kn[NK], vn[NK];
+        if (cn < Q.nbox) {
+          crn = chunk_rows(rc, Q.bx, 32 * cn);
+          int e[3];
+          box_point(Q.bx, crn, 32 * cn, n, e);
+          const int off = box_off(ka, e);
+          load_kv<T, D>(k + ka.base + off, v + ka.base + off, kn, vn, h);
+        }
+        bool ok[16];
+        chunk_mask(Q.bx, cr, 32 * c, h, Q.wlo, Q.ww, ok);
+        dq_compute<T, D>(acc[0], qf, df, kf, vf, ok, sl2, lse2, dl, ta, n, h);
+        c = cn;
+        cr = crn;
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        kf[t] = kn[t];
-        vf[t] = vn[t];
+        for (int t = 0; t < NK; ++t) {
+          kf[t] = kn[t];
+          vf[t] = vn[t];
+        }
       }
     }
     for (int cx = first_owned(Q.nbox, w, W); cx < Q.nbox + Q.nextra; cx += W) {
@@ -605,12 +637,29 @@ __global__ void __launch_bounds__(256)
   bx.lgP = uni(bx.lgP);
   const int nchunk = uni(any ? (bx.slots + 31) >> 5 : 0);
 
+  // the tile's K and V rows (B operands of every chunk): in LDS for the
+  // lean variant, whose register peak sets the kernel's occupancy, else in
+  // registers
   v8 kf[NK], vf[NK];
+  if constexpr (kLeanBwd(D)) {
+    E *kr = kvs + n * kKvRow(D);
+    E *vr = kvs + (32 + n) * kKvRow(D);
 #pragma unroll
-  for (int t = 0; t < NK; ++t) {
-    kf[t] = k_valid ? ld8(k + krow + 16 * t + 8 * h) : zero8<T>();
-    vf[t] = k_valid ? ld8(v + krow + 16 * t + 8 * h) : zero8<T>();
+    for (int t = 0; t < NK; ++t) {
+      *reinterpret_cast<v8 *>(kr + 16 * t + 8 * h) =
+          k_valid ? ld8(k + krow + 16 * t + 8 * h) : zero8<T>();
+      *reinterpret_cast<v8 *>(vr + 16 * t + 8 * h) =
+          k_valid ? ld8(v + krow + 16 * t + 8 * h) : zero8<T>();
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      kf[t] = k_valid ? ld8(k + krow + 16 * t + 8 * h) : zero8<T>();
+      vf[t] = k_valid ? ld8(v + krow + 16 * t + 8 * h) : zero8<T>();
+    }
   }
+  const E *kfl = kvs + n * kKvRow(D) + 8 * h;
+  const E *vfl = kvs + (32 + n) * kKvRow(D) + 8 * h;
   f32x16 acc[2][NC];  // [0] = dK^T, [1] = dV^T
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -621,116 +670,201 @@ __global__ void __launch_bounds__(256)
   for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
     const BoxAddr qa_addr = box_addr(P, tc, bx, hq, P.H);
     const int64_t lbase = qa_addr.base / D;  // lse/dlse offset of the box origin
-    // query chunks, software-pipelined like the forward; padding slots
-    // load a real (clamped) query and the mask removes them
-    RowCursor rc{0, 0, 0};
-    int c = w;
-    ChunkRows cr{0, 0, 0};
-    v8 qa[NK], da[NK], oa[NK];
-    float lsev = 0.f, dlsev = 0.f;
-    if (c < nchunk) {
-      cr = chunk_rows(rc, bx, 32 * c);
-      int e[3];
-      box_point(bx, cr, 32 * c, n, e);
-      const int off = box_off(qa_addr, e);
-      const int64_t qrow = qa_addr.base + off;
-      const int64_t lrow = lbase + off / D;
+    if constexpr (kLeanBwd(D)) {
+      // query chunks; padding slots load a real (clamped) query and the mask
+      // removes them.  No next-chunk prefetch here: this role's register peak
+      // sets the whole kernel's occupancy, and at four waves per SIMD the
+      // other resident waves hide the chunk loads instead.
+      RowCursor rc{0, 0, 0};
+      for (int c = w; c < nchunk; c += W) {
+        const ChunkRows cr = chunk_rows(rc, bx, 32 * c);
+        v8 qa[NK], da[NK];
+        float dl = 0.f, lsev, dlsev;
+        {
+          int e[3];
+          box_point(bx, cr, 32 * c, n, e);
+          const int off = box_off(qa_addr, e);
+          const int64_t qrow = qa_addr.base + off;
+          const int64_t lrow = lbase + off / D;
+          v8 oa[NK];
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        qa[t] = ld8(q + qrow + 16 * t + 8 * h);
-        da[t] = ld8(dout + qrow + 16 * t + 8 * h);
-        oa[t] = ld8(out + qrow + 16 * t + 8 * h);
+          for (int t = 0; t < NK; ++t) {
+            qa[t] = ld8(q + qrow + 16 * t + 8 * h);
+            da[t] = ld8(dout + qrow + 16 * t + 8 * h);
+            oa[t] = ld8(out + qrow + 16 * t + 8 * h);
+          }
+          lsev = lse[lrow];
+          dlsev = dlse != nullptr ? dlse[lrow] : 0.f;
+#pragma unroll
+          for (int t = 0; t < NK; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)oa[t][i], dl);
+        }
+        dl += __shfl_xor(dl, 32);
+        dl -= dlsev;
+        const float l2 = lsev * kLog2e;
+
+        wave_lds_sync();
+#pragma unroll
+        for (int t = 0; t < NK; ++t)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
+            tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+          }
+        if (h == 0) {
+          s_lse[n] = l2;
+          s_del[n] = dl;
+        }
+        wave_lds_sync();
+
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+          s = M::mma(qa[t], *reinterpret_cast<const v8 *>(kfl + 16 * t), s);
+          dp = M::mma(da[t], *reinterpret_cast<const v8 *>(vfl + 16 * t), dp);
+        }
+        bool ok[16];
+        chunk_mask(bx, cr, 32 * c, h, wlo, ww, ok);
+        float p[16], ds[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
+          const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+          const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int e2 = 4 * i + j;
+            p[e2] = ok[e2] ? __builtin_amdgcn_exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
+            ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+          }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const v8 bp = pack8<T>(p + 8 * kb);
+          const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h),
+                                bp, acc[1][cc]);
+            acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
+                                bs, acc[0][cc]);
+          }
+        }
       }
-      lsev = lse[lrow];
-      dlsev = dlse != nullptr ? dlse[lrow] : 0.f;
-    }
-    while (c < nchunk) {
-      const int cn = c + W;
-      ChunkRows crn = cr;
-      v8 qn[NK], dn[NK], on[NK];
-      float lsen = 0.f, dlsen = 0.f;
-      if (cn < nchunk) {
-        crn = chunk_rows(rc, bx, 32 * cn);
+    } else {
+      // query chunks, software-pipelined like the forward; padding slots
+      // load a real (clamped) query and the mask removes them
+      RowCursor rc{0, 0, 0};
+      int c = w;
+      ChunkRows cr{0, 0, 0};
+      v8 qa[NK], da[NK], oa[NK];
+      float lsev = 0.f, dlsev = 0.f;
+      if (c < nchunk) {
+        cr = chunk_rows(rc, bx, 32 * c);
         int e[3];
-        box_point(bx, crn, 32 * cn, n, e);
+        box_point(bx, cr, 32 * c, n, e);
         const int off = box_off(qa_addr, e);
         const int64_t qrow = qa_addr.base + off;
         const int64_t lrow = lbase + off / D;
 #pragma unroll
         for (int t = 0; t < NK; ++t) {
-          qn[t] = ld8(q + qrow + 16 * t + 8 * h);
-          dn[t] = ld8(dout + qrow + 16 * t + 8 * h);
-          on[t] = ld8(out + qrow + 16 * t + 8 * h);
+          qa[t] = ld8(q + qrow + 16 * t + 8 * h);
+          da[t] = ld8(dout + qrow + 16 * t + 8 * h);
+          oa[t] = ld8(out + qrow + 16 * t + 8 * h);
         }
-        lsen = lse[lrow];
-        dlsen = dlse != nullptr ? dlse[lrow] : 0.f;
+        lsev = lse[lrow];
+        dlsev = dlse != nullptr ? dlse[lrow] : 0.f;
       }
-      float dl = 0.f;
+      while (c < nchunk) {
+        const int cn = c + W;
+        ChunkRows crn = cr;
+        v8 qn[NK], dn[NK], on[NK];
+        float lsen = 0.f, dlsen = 0.f;
+        if (cn < nchunk) {
+          crn = chunk_rows(rc, bx, 32 * cn);
+          int e[3];
+          box_point(bx, crn, 32 * cn, n, e);
+          const int off = box_off(qa_addr, e);
+          const int64_t qrow = qa_addr.base + off;
+          const int64_t lrow = lbase + off / D;
 #pragma unroll
-      for (int t = 0; t < NK; ++t)
+          for (int t = 0; t < NK; ++t) {
+            qn[t] = ld8(q + qrow + 16 * t + 8 * h);
+            dn[t] = ld8(dout + qrow + 16 * t + 8 * h);
+            on[t] = ld8(out + qrow + 16 * t + 8 * h);
+          }
+          lsen = lse[lrow];
+          dlsen = dlse != nullptr ? dlse[lrow] : 0.f;
+        }
+        float dl = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)oa[t][i], dl);
-      dl += __shfl_xor(dl, 32);
-      dl -= dlsev;
-      const float l2 = lsev * kLog2e;
+        for (int t = 0; t < NK; ++t)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)oa[t][i], dl);
+        dl += __shfl_xor(dl, 32);
+        dl -= dlsev;
+        const float l2 = lsev * kLog2e;
 
-      wave_lds_sync();
+        wave_lds_sync();
 #pragma unroll
-      for (int t = 0; t < NK; ++t)
+        for (int t = 0; t < NK; ++t)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
-          tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+          for (int i = 0; i < 8; ++i) {
+            ta[(16 * t + 8 * h + i) * kRow + n] = qa[t][i];
+            tb[(16 * t + 8 * h + i) * kRow + n] = da[t][i];
+          }
+        if (h == 0) {
+          s_lse[n] = l2;
+          s_del[n] = dl;
         }
-      if (h == 0) {
-        s_lse[n] = l2;
-        s_del[n] = dl;
-      }
-      wave_lds_sync();
+        wave_lds_sync();
 
-      f32x16 s = zero16(), dp = zero16();
+        f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        s = M::mma(qa[t], kf[t], s);
-        dp = M::mma(da[t], vf[t], dp);
-      }
-      bool ok[16];
-      chunk_mask(bx, cr, 32 * c, h, wlo, ww, ok);
-      float p[16], ds[16];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
-        const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e2 = 4 * i + j;
-          p[e2] = ok[e2] ? __builtin_amdgcn_exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
-          ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+        for (int t = 0; t < NK; ++t) {
+          s = M::mma(qa[t], kf[t], s);
+          dp = M::mma(da[t], vf[t], dp);
         }
-      }
+        bool ok[16];
+        chunk_mask(bx, cr, 32 * c, h, wlo, ww, ok);
+        float p[16], ds[16];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const v8 bp = pack8<T>(p + 8 * kb);
-        const v8 bs = pack8<T>(ds + 8 * kb);
+        for (int i = 0; i < 4; ++i) {
+          const float4 l4 = *reinterpret_cast<const float4 *>(s_lse + 8 * i + 4 * h);
+          const float4 d4 = *reinterpret_cast<const float4 *>(s_del + 8 * i + 4 * h);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+          const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-        for (int cc = 0; cc < NC; ++cc) {
-          acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h),
-                              bp, acc[1][cc]);
-          acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
-                              bs, acc[0][cc]);
+          for (int j = 0; j < 4; ++j) {
+            const int e2 = 4 * i + j;
+            p[e2] = ok[e2] ? __builtin_amdgcn_exp2f(fmaf(s[e2], sl2, -lv[j])) : 0.f;
+            ds[e2] = p[e2] * (dp[e2] - dv4[j]);
+          }
         }
-      }
-      c = cn;
-      cr = crn;
-      lsev = lsen;
-      dlsev = dlsen;
 #pragma unroll
-      for (int t = 0; t < NK; ++t) {
-        qa[t] = qn[t];
-        da[t] = dn[t];
-        oa[t] = on[t];
+        for (int kb = 0; kb < 2; ++kb) {
+          const v8 bp = pack8<T>(p + 8 * kb);
+          const v8 bs = pack8<T>(ds + 8 * kb);
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            acc[1][cc] = M::mma(lds_a<T>(tb + (32 * cc + n) * kRow + 16 * kb, h),
+                                bp, acc[1][cc]);
+            acc[0][cc] = M::mma(lds_a<T>(ta + (32 * cc + n) * kRow + 16 * kb, h),
+                                bs, acc[0][cc]);
+          }
+        }
+        c = cn;
+        cr = crn;
+        lsev = lsen;
+        dlsev = dlsen;
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+          qa[t] = qn[t];
+          da[t] = dn[t];
+          oa[t] = on[t];
+        }
       }
     }
   }
@@ -766,7 +900,7 @@ size_t fwd_lds(int D, int W, int esize) {
 }
 
 size_t bwd_lds(int D, int W, int esize) {
-  const size_t tr = (size_t)W * (2 * D * kRow * esize + 256);
+  const size_t tr = (size_t)W * bwd_wave_lds(D, esize);
   const size_t cb = (size_t)(W - 1) * 2 * (D / 32) * 16 * 64 * sizeof(float);
   return tr > cb ? tr : cb;
 }
