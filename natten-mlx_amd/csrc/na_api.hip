@@ -281,13 +281,15 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
   float *delta = static_cast<float *>(workspace);
   const hipStream_t st = as_stream(stream);
   if (use_mfma(p, P)) {
-    na::mfma_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
-                 dq, dk, dv, st);
-    if (P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr) {
+    const bool dextra =
+        P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
+    if (dextra || na::mfma_bwd_reads_delta(P))
       na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+    na::mfma_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
+                 delta, dq, dk, dv, st);
+    if (dextra)
       na::valu_dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout,
                       d_extra_k, d_extra_v, st);
-    }
   } else {
     na::valu_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
                  dq, dk, dv, d_extra_k, d_extra_v, delta, st);

@@ -58,10 +58,14 @@ bool mfma_eligible(const Prob &P, int dtype);
 void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,
               float *lse, hipStream_t st);
+// delta: rowsum(dO * O) - dlse per (query, head), from valu_delta; read only
+// where mfma_bwd_reads_delta(P), else recomputed from out and dlse.
+bool mfma_bwd_reads_delta(const Prob &P);
 void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, const void *out,
-              const float *lse, const void *dout, const float *dlse, void *dq,
-              void *dk, void *dv, hipStream_t st);
+              const float *lse, const void *dout, const float *dlse,
+              const float *delta, void *dq, void *dk, void *dv,
+              hipStream_t st);
 void mfma_selftest(int dtype, float *out, hipStream_t st);
 
 // Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with

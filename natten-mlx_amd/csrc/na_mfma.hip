@@ -21,7 +21,10 @@
 //   dK/dV tiles (32 keys)    over the queries whose windows contain them
 //                            (inverse neighborhood, a box per axis):
 //                            dV^T += dO^T . P,  dK^T += Q^T . dS
-// delta = rowsum(dO * O) - dlse is recomputed per query from O and dO.
+// delta = rowsum(dO * O) - dlse: at head_dim 32 each role recomputes it from
+// O and dO (cheaper than one more launch on these short problems); from
+// head_dim 64 a pre-pass writes one fp32 per (query, head) and neither role
+// reads O, which keeps the prefetching loops within two waves per SIMD.
 #include "na_mfma.h"
 
 namespace na {
@@ -58,6 +61,9 @@ __global__ void __launch_bounds__(64) k_selftest(float *out) {
 // registers the prefetch needs would cost the kernel a wave per SIMD
 // (123 VGPRs: four waves, all of config 2's 3136 waves resident at once).
 constexpr bool kLeanBwd(int D) { return D == 32; }
+// From head_dim 64 the backward reads delta from a pre-pass instead of
+// recomputing it from O.
+constexpr bool kPreDelta(int D) { return !kLeanBwd(D); }
 
 // LDS row stride (elements) of a dK/dV tile's K / V rows: 16 bytes of skew.
 constexpr int kKvRow(int D) { return D + 8; }
@@ -464,7 +470,8 @@ __global__ void __launch_bounds__(256)
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, const T *__restrict__ out,
            const float *__restrict__ lse, const T *__restrict__ dout,
-           const float *__restrict__ dlse, T *__restrict__ dq,
+           const float *__restrict__ dlse, const float *__restrict__ delta,
+           T *__restrict__ dq,
            T *__restrict__ dk, T *__restrict__ dv) {
   typedef Mf<T> M;
   typedef typename M::v8 v8;
@@ -504,13 +511,19 @@ __global__ void __launch_bounds__(256)
     for (int t = 0; t < NK; ++t) {
       qf[t] = Q.q_valid ? ld8(q + qrow + 16 * t + 8 * h) : zero8<T>();
       df[t] = Q.q_valid ? ld8(dout + qrow + 16 * t + 8 * h) : zero8<T>();
-      const v8 of = Q.q_valid ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
+      if constexpr (!kPreDelta(D)) {
+        const v8 of = Q.q_valid ? ld8(out + qrow + 16 * t + 8 * h) : zero8<T>();
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dl = fmaf((float)df[t][e], (float)of[e], dl);
+        for (int e = 0; e < 8; ++e) dl = fmaf((float)df[t][e], (float)of[e], dl);
+      }
     }
-    dl += __shfl_xor(dl, 32);
     const int64_t lrow = Q.qtok * P.H + Q.tc.head;
-    if (Q.q_valid && dlse != nullptr) dl -= dlse[lrow];
+    if constexpr (kPreDelta(D)) {
+      dl = Q.q_valid ? delta[lrow] : 0.f;
+    } else {
+      dl += __shfl_xor(dl, 32);
+      if (Q.q_valid && dlse != nullptr) dl -= dlse[lrow];
+    }
     const float lse2 = Q.q_valid ? lse[lrow] * kLog2e : 0.f;
 
     f32x16 acc[1][NC];
@@ -669,7 +682,7 @@ __global__ void __launch_bounds__(256)
 
   for (int hq = hk * P.rep; hq < (hk + 1) * P.rep; ++hq) {
     const BoxAddr qa_addr = box_addr(P, tc, bx, hq, P.H);
-    const int64_t lbase = qa_addr.base / D;  // lse/dlse offset of the box origin
+    const int64_t lbase = qa_addr.base / D;  // lse/dlse/delta offset of the box origin
     if constexpr (kLeanBwd(D)) {
       // query chunks; padding slots load a real (clamped) query and the mask
       // removes them.  No next-chunk prefetch here: this role's register peak
@@ -759,8 +772,8 @@ __global__ void __launch_bounds__(256)
       RowCursor rc{0, 0, 0};
       int c = w;
       ChunkRows cr{0, 0, 0};
-      v8 qa[NK], da[NK], oa[NK];
-      float lsev = 0.f, dlsev = 0.f;
+      v8 qa[NK], da[NK];
+      float lsev = 0.f, delv = 0.f;
       if (c < nchunk) {
         cr = chunk_rows(rc, bx, 32 * c);
         int e[3];
@@ -772,16 +785,15 @@ __global__ void __launch_bounds__(256)
         for (int t = 0; t < NK; ++t) {
           qa[t] = ld8(q + qrow + 16 * t + 8 * h);
           da[t] = ld8(dout + qrow + 16 * t + 8 * h);
-          oa[t] = ld8(out + qrow + 16 * t + 8 * h);
         }
         lsev = lse[lrow];
-        dlsev = dlse != nullptr ? dlse[lrow] : 0.f;
+        delv = delta[lrow];
       }
       while (c < nchunk) {
         const int cn = c + W;
         ChunkRows crn = cr;
-        v8 qn[NK], dn[NK], on[NK];
-        float lsen = 0.f, dlsen = 0.f;
+        v8 qn[NK], dn[NK];
+        float lsen = 0.f, deln = 0.f;
         if (cn < nchunk) {
           crn = chunk_rows(rc, bx, 32 * cn);
           int e[3];
@@ -793,18 +805,11 @@ __global__ void __launch_bounds__(256)
           for (int t = 0; t < NK; ++t) {
             qn[t] = ld8(q + qrow + 16 * t + 8 * h);
             dn[t] = ld8(dout + qrow + 16 * t + 8 * h);
-            on[t] = ld8(out + qrow + 16 * t + 8 * h);
           }
           lsen = lse[lrow];
-          dlsen = dlse != nullptr ? dlse[lrow] : 0.f;
+          deln = delta[lrow];
         }
-        float dl = 0.f;
-#pragma unroll
-        for (int t = 0; t < NK; ++t)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) dl = fmaf((float)da[t][i], (float)oa[t][i], dl);
-        dl += __shfl_xor(dl, 32);
-        dl -= dlsev;
+        const float dl = delv;
         const float l2 = lsev * kLog2e;
 
         wave_lds_sync();
@@ -858,12 +863,11 @@ __global__ void __launch_bounds__(256)
         c = cn;
         cr = crn;
         lsev = lsen;
-        dlsev = dlsen;
+        delv = deln;
 #pragma unroll
         for (int t = 0; t < NK; ++t) {
           qa[t] = qn[t];
           da[t] = dn[t];
-          oa[t] = on[t];
         }
       }
     }
@@ -965,10 +969,13 @@ void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef FWD_
 }
 
+bool mfma_bwd_reads_delta(const Prob &P) { return kPreDelta(P.D); }
+
 void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, const void *out,
-              const float *lse, const void *dout, const float *dlse, void *dq,
-              void *dk, void *dv, hipStream_t st) {
+              const float *lse, const void *dout, const float *dlse,
+              const float *delta, void *dq, void *dk, void *dv,
+              hipStream_t st) {
   double chunks = 1.0;
   Tiling Tl = choose_tiling(P, P.H, P.Hkv, &chunks);
   Tl.n_launch = (Tl.n_q + Tl.n_k + 7) & ~7;
@@ -981,14 +988,16 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
                        lds, st, P, Tl, (const bf16_t *)q, (const bf16_t *)k,   \
                        (const bf16_t *)v, (const bf16_t *)ek,                  \
                        (const bf16_t *)ev, (const bf16_t *)out, lse,           \
-                       (const bf16_t *)dout, dlse, (bf16_t *)dq, (bf16_t *)dk, \
+                       (const bf16_t *)dout, dlse, delta, (bf16_t *)dq,        \
+                       (bf16_t *)dk,                                           \
                        (bf16_t *)dv);                                          \
   else                                                                         \
     hipLaunchKernelGGL((k_mbwd<f16_t, DD>), dim3(Tl.n_launch), dim3(64 * W),    \
                        lds, st, P, Tl, (const f16_t *)q, (const f16_t *)k,     \
                        (const f16_t *)v, (const f16_t *)ek,                    \
                        (const f16_t *)ev, (const f16_t *)out, lse,             \
-                       (const f16_t *)dout, dlse, (f16_t *)dq, (f16_t *)dk,    \
+                       (const f16_t *)dout, dlse, delta, (f16_t *)dq,          \
+                       (f16_t *)dk,                                            \
                        (f16_t *)dv)
   NA_MFMA_D(P.D, BWD_);
 #undef BWD_
