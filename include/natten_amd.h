@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NA_ABI_VERSION 1
+#define NA_ABI_VERSION 2
 
 enum na_dtype { NA_F32 = 0, NA_F16 = 1, NA_BF16 = 2 };
 
@@ -181,8 +181,8 @@ typedef struct na_rpb_params {
   int32_t heads;
   int32_t head_dim;
   int32_t extent[2];   /* L, or (Hh, Hw) */
-  int32_t kernel;      /* K */
-  int32_t dilation;
+  int32_t kernel[2];   /* window side per axis (axis 1 unused for rank 1) */
+  int32_t dilation[2]; /* dilation per axis (axis 1 unused for rank 1) */
   int32_t heads_first; /* 0: spatial-first rows, 1: heads-first rows */
   int32_t dtype;       /* q / key / value and their gradients */
   float scale;         /* query scale, applied in `dtype` before the dot */

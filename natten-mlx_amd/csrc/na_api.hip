@@ -142,12 +142,17 @@ int make_rpb(const na_rpb_params *p, na::RpbProb *A) {
       p->head_dim > kMaxHeadDim)
     return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported",
                 p->head_dim);
-  if (p->kernel < 1 || p->dilation < 1)
+  const int32_t K1 = p->rank == 2 ? p->kernel[1] : 1;
+  const int32_t d1 = p->rank == 2 ? p->dilation[1] : 1;
+  if (p->kernel[0] < 1 || p->dilation[0] < 1 || K1 < 1 || d1 < 1)
     return fail(NA_ERR_INVALID, "kernel and dilation must be positive");
   const int32_t L1 = p->rank == 2 ? p->extent[1] : 1;
   if (p->extent[0] < 1 || L1 < 1)
     return fail(NA_ERR_INVALID, "extents must be positive");
-  const int64_t kk = p->rank == 2 ? (int64_t)p->kernel * p->kernel : p->kernel;
+  if ((int64_t)p->kernel[0] * p->dilation[0] > (1 << 20) ||
+      (int64_t)K1 * d1 > (1 << 20))
+    return fail(NA_ERR_UNSUPPORTED, "kernel * dilation too large");
+  const int64_t kk = (int64_t)p->kernel[0] * K1;
   const int64_t rows = (int64_t)p->batch * p->heads * p->extent[0] * L1;
   if (rows >= ((int64_t)1 << 31) || kk >= ((int64_t)1 << 20))
     return fail(NA_ERR_UNSUPPORTED, "allin1 problem too large");
@@ -155,13 +160,15 @@ int make_rpb(const na_rpb_params *p, na::RpbProb *A) {
   A->B = p->batch;
   A->H = p->heads;
   A->D = p->head_dim;
-  A->K = p->kernel;
-  A->dil = p->dilation;
+  A->K0 = p->kernel[0];
+  A->K1 = K1;
+  A->d0 = p->dilation[0];
+  A->d1 = d1;
   A->L0 = p->extent[0];
   A->L1 = L1;
-  A->K1 = p->rank == 2 ? p->kernel : 1;
   A->KK = (int32_t)kk;
-  A->R = 2 * p->kernel - 1;
+  A->R0 = 2 * A->K0 - 1;
+  A->R1 = p->rank == 2 ? 2 * K1 - 1 : 1;
   A->heads_first = p->heads_first ? 1 : 0;
   A->has_scale = p->has_scale ? 1 : 0;
   A->scale = p->scale;
@@ -169,7 +176,8 @@ int make_rpb(const na_rpb_params *p, na::RpbProb *A) {
   A->fH = na::make_fastdiv((uint32_t)A->H);
   A->fL0 = na::make_fastdiv((uint32_t)A->L0);
   A->fL1 = na::make_fastdiv((uint32_t)A->L1);
-  A->fdil = na::make_fastdiv((uint32_t)A->dil);
+  A->fd0 = na::make_fastdiv((uint32_t)A->d0);
+  A->fd1 = na::make_fastdiv((uint32_t)A->d1);
   return NA_OK;
 }
 

@@ -29,16 +29,17 @@ void table(const Prob &P, int32_t *index, uint8_t *valid, hipStream_t st);
 // DiNAT all-in-one operators (na_rpb.hip): square window K (odd or even),
 // uniform dilation, rank 1 or 2, spatial-first or heads-first rows.
 struct RpbProb {
-  int32_t rank, B, H, D, K, dil;
+  int32_t rank, B, H, D;
   int32_t L0, L1;       // L1 = 1 for rank 1
-  int32_t K1;           // window side on axis 1 (K, or 1 for rank 1)
-  int32_t KK;           // slots per query, K^rank
-  int32_t R;            // bias rows per axis, 2K-1
+  int32_t K0, K1;       // window side per axis (K1 = 1 for rank 1)
+  int32_t d0, d1;       // dilation per axis (d1 = 1 for rank 1)
+  int32_t KK;           // slots per query, K0 * K1
+  int32_t R0, R1;       // bias rows per axis, 2K-1 (R1 = 1 for rank 1)
   int32_t heads_first;  // 0: rows ordered [B, L0, L1, H]; 1: [B, H, L0, L1]
   int32_t has_scale;    // q is scaled (and rounded to its dtype) first
   float scale;
   int32_t n_rows;       // B * H * L0 * L1 (< 2^31)
-  FastDiv fH, fL0, fL1, fdil;  // row decode and window arithmetic
+  FastDiv fH, fL0, fL1, fd0, fd1;  // row decode and window arithmetic
 };
 void rpb_qk_fwd(const RpbProb &A, int dtype, const void *q, const void *key,
                 const float *rpb, float *logits, hipStream_t st);

@@ -1,8 +1,9 @@
 // na_rpb.hip — DiNAT all-in-one operators: QK with relative position bias
-// and AV over a square window (side K, uniform dilation) on one or two
-// spatial axes, forward and backward (reference extras/allin1).
+// and AV over a window of side K_a and dilation d_a per axis on one or two
+// spatial axes, forward and backward (reference extras/allin1 and the
+// NATTEN 0.14 compat functions).
 //
-// Window of a query on an axis: slot k holds key s + k*dil with s the
+// Window of a query on an axis: slot k holds key s + k*d with s the
 // dilation-partition start, valid iff 0 <= key < end; its bias row is
 // clip(pb + k, 0, 2K-2) (reference extras/allin1/reference_impl.py:13-45,
 // compat/v014.py:18-23).  Invalid slots produce -inf logits (zero dattn)
@@ -70,11 +71,12 @@ struct RWin {
   int32_t pb;  // bias row of slot 0 (before clipping)
 };
 
-// Window of position i on an axis of length L: window_start_partition,
-// window_end and pb_start (na_window.h) with the divisions by the dilation
-// done by multiply-shift.
-__device__ __forceinline__ RWin rwin(const RpbProb &A, int32_t i, int32_t L) {
-  const int32_t K = A.K, nh = K / 2, d = A.dil;
+// Window of position i on an axis of length L, side K and dilation d:
+// window_start_partition, window_end and pb_start (na_window.h) with the
+// divisions by the dilation done by multiply-shift (fd divides by d).
+__device__ __forceinline__ RWin rwin_axis(int32_t K, int32_t d, FastDiv fd,
+                                          int32_t i, int32_t L) {
+  const int32_t nh = K / 2;
   RWin w;
   if (d == 1) {
     int32_t s = i > nh ? i - nh : 0;
@@ -87,9 +89,9 @@ __device__ __forceinline__ RWin rwin(const RpbProb &A, int32_t i, int32_t L) {
     w.pb = pb;
     return w;
   }
-  const int32_t slot = (int32_t)fdiv((uint32_t)i, A.fdil);
+  const int32_t slot = (int32_t)fdiv((uint32_t)i, fd);
   const int32_t phase = i - slot * d;
-  const int32_t plen = (int32_t)fdiv((uint32_t)(L - 1 - phase), A.fdil) + 1;
+  const int32_t plen = (int32_t)fdiv((uint32_t)(L - 1 - phase), fd) + 1;
   int32_t s = slot > nh ? slot - nh : 0;
   if (slot + nh >= plen) s += plen - slot - nh - 1;
   w.s = s * d + phase;
@@ -97,15 +99,19 @@ __device__ __forceinline__ RWin rwin(const RpbProb &A, int32_t i, int32_t L) {
   if (i < nh * d)
     w.pb = K - 1 - slot;
   else if (i + nh * d >= L)
-    w.pb = (int32_t)fdiv((uint32_t)(L - i - 1), A.fdil);
+    w.pb = (int32_t)fdiv((uint32_t)(L - i - 1), fd);
   else
     w.pb = nh;
   return w;
 }
 
+__device__ __forceinline__ RWin rwin0(const RpbProb &A, int32_t i0) {
+  return rwin_axis(A.K0, A.d0, A.fd0, i0, A.L0);
+}
+
 // Axis-1 window (a single always-valid slot for rank 1).
 __device__ __forceinline__ RWin rwin1(const RpbProb &A, int32_t i1) {
-  if (A.rank == 2) return rwin(A, i1, A.L1);
+  if (A.rank == 2) return rwin_axis(A.K1, A.d1, A.fd1, i1, A.L1);
   return RWin{0, 1, 0};
 }
 
@@ -115,8 +121,8 @@ __device__ __forceinline__ int32_t clampi(int32_t x, int32_t lo, int32_t hi) {
 
 __device__ __forceinline__ int32_t bias_index(const RpbProb &A, int32_t h,
                                               int32_t r0, int32_t r1) {
-  const int32_t a = h * A.R + clampi(r0, 0, A.R - 1);
-  return A.rank == 2 ? a * A.R + clampi(r1, 0, A.R - 1) : a;
+  const int32_t a = h * A.R0 + clampi(r0, 0, A.R0 - 1);
+  return A.rank == 2 ? a * A.R1 + clampi(r1, 0, A.R1 - 1) : a;
 }
 
 // ---- row helpers (lane-local part of a D-row; element type per call) ------
@@ -192,7 +198,7 @@ __device__ __forceinline__ void scale_round(float (&v)[kNT][VEC], float s) {
 }
 
 
-// Rank 1: the keys (or values) of every row of a block lie within K*dil
+// Rank 1: the keys (or values) of every row of a block lie within K*d
 // positions of the block's rows, i.e. in the row range [lo, hi) below;
 // the block copies that range into LDS with contiguous 16-byte loads
 // (`ystage`) so the per-slot row reads hit LDS.  Returns lo.
@@ -202,7 +208,7 @@ __device__ __forceinline__ int64_t stage_window(const RpbProb &A, const T *y,
   const int64_t step = A.heads_first ? 1 : A.H;
   const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
   const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
-  const int64_t reach = (int64_t)A.K * A.dil * step;
+  const int64_t reach = (int64_t)A.K0 * A.d0 * step;
   const int64_t lo = max((int64_t)0, row0 - reach);
   const int64_t hi = min((int64_t)A.n_rows, row0 + rows + reach);
   const int64_t n16 = (hi - lo) * A.D * (int64_t)sizeof(T) / 16;
@@ -216,7 +222,7 @@ __device__ __forceinline__ int64_t stage_window(const RpbProb &A, const T *y,
 // Rows of the staged window per block (bounds the LDS it needs).
 inline int64_t window_rows(const RpbProb &A, int lgG) {
   const int64_t step = A.heads_first ? 1 : A.H;
-  return (256 >> lgG) + 2 * (int64_t)A.K * A.dil * step;
+  return (256 >> lgG) + 2 * (int64_t)A.K0 * A.d0 * step;
 }
 
 // ---- kernels ---------------------------------------------------------------
@@ -235,7 +241,7 @@ __global__ void __launch_bounds__(256)
   float xv[kNT][VEC];
   ld_row<TX, VEC>(xv, x + g.id * A.D, g.lane, G, A.D);
   if (scale_x) scale_round<TX, VEC>(xv, A.scale);
-  const RWin w0 = rwin(A, p.i0, A.L0);
+  const RWin w0 = rwin0(A, p.i0);
   const RWin w1 = rwin1(A, p.i1);
   // rows of this block are consecutive in memory: stage them in LDS and
   // write the block's slot values as one contiguous range
@@ -245,7 +251,7 @@ __global__ void __launch_bounds__(256)
   if (A.rank == 1) {
     // one axis: the row of key position j is this row + (j - i) * step
     const int64_t step = A.heads_first ? 1 : A.H;
-    const float *rb = rpb != nullptr ? rpb + p.h * A.R : nullptr;
+    const float *rb = rpb != nullptr ? rpb + p.h * A.R0 : nullptr;
     const TY *ybase = y;
     int64_t ylo = 0;
     if constexpr (YS) {
@@ -253,23 +259,23 @@ __global__ void __launch_bounds__(256)
       ylo = stage_window<TY>(A, y, ys, lgG);
       ybase = ys;
     }
-    for (int k0 = 0; k0 < A.K; ++k0) {
-      const int32_t j0 = w0.s + k0 * A.dil;
+    for (int k0 = 0; k0 < A.K0; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.d0;
       float s = fill;
       if (j0 >= 0 && j0 < w0.e) {
         const TY *yr = ybase + (g.id - ylo + (int64_t)(j0 - p.i0) * step) * A.D;
         s = group_sum(dot_row<TY, VEC>(xv, yr, g.lane, G, A.D), G);
-        if (rb != nullptr) s += rb[clampi(w0.pb + k0, 0, A.R - 1)];
+        if (rb != nullptr) s += rb[clampi(w0.pb + k0, 0, A.R0 - 1)];
       }
       if (g.live && g.lane == 0) dst[k0] = s;
     }
   } else {
     int n = 0;
-    for (int k0 = 0; k0 < A.K; ++k0) {
-      const int32_t j0 = w0.s + k0 * A.dil;
+    for (int k0 = 0; k0 < A.K0; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.d0;
       const bool v0 = j0 >= 0 && j0 < w0.e;
       for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
-        const int32_t j1 = w1.s + k1 * A.dil;
+        const int32_t j1 = w1.s + k1 * A.d1;
         float s = fill;
         if (v0 && j1 >= 0 && j1 < w1.e) {
           const TY *yr = y + rrow(A, p.b, p.h, j0, j1) * A.D;
@@ -300,7 +306,7 @@ __global__ void __launch_bounds__(256)
                  int staged, int G, int lgG) {
   const Group g = make_group(lgG, A.n_rows);
   const RPos p = rpos(A, (uint32_t)g.id);
-  const RWin w0 = rwin(A, p.i0, A.L0);
+  const RWin w0 = rwin0(A, p.i0);
   const RWin w1 = rwin1(A, p.i1);
   // the block's weight rows are one contiguous range: read it coalesced
   extern __shared__ __align__(16) float stage[];
@@ -328,8 +334,8 @@ __global__ void __launch_bounds__(256)
       ylo = stage_window<TY>(A, y, ys, lgG);
       ybase = ys;
     }
-    for (int k0 = 0; k0 < A.K; ++k0) {
-      const int32_t j0 = w0.s + k0 * A.dil;
+    for (int k0 = 0; k0 < A.K0; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.d0;
       if (j0 >= 0 && j0 < w0.e)
         axpy_row<TY, VEC>(acc, wr[k0],
                           ybase + (g.id - ylo + (int64_t)(j0 - p.i0) * step) * A.D,
@@ -337,11 +343,11 @@ __global__ void __launch_bounds__(256)
     }
   } else {
     int n = 0;
-    for (int k0 = 0; k0 < A.K; ++k0) {
-      const int32_t j0 = w0.s + k0 * A.dil;
+    for (int k0 = 0; k0 < A.K0; ++k0) {
+      const int32_t j0 = w0.s + k0 * A.d0;
       const bool v0 = j0 >= 0 && j0 < w0.e;
       for (int k1 = 0; k1 < A.K1; ++k1, ++n) {
-        const int32_t j1 = w1.s + k1 * A.dil;
+        const int32_t j1 = w1.s + k1 * A.d1;
         if (v0 && j1 >= 0 && j1 < w1.e)
           axpy_row<TY, VEC>(acc, wr[n], y + rrow(A, p.b, p.h, j0, j1) * A.D,
                             g.lane, G, A.D);
@@ -353,8 +359,9 @@ __global__ void __launch_bounds__(256)
 
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
 // transpose of k_rpb_gather, evaluated per key row.  A query i can hold key
-// j only on j's dilation phase and within K*dil of it, so the candidates
-// are i = j + t*dil, |t| <= K, kept when j lies in [start(i), end(i)).
+// j only on j's dilation phase and within K*d of it, so the candidates
+// are i = j + t*d, |t| <= K, per axis, kept when j lies in
+// [start(i), end(i)).
 // QK backward's dk (w = dlogits, x = q scaled as in the forward) and AV
 // backward's dv (w = attn, x = dout).
 template <typename TX, typename TO, int VEC>
@@ -369,19 +376,19 @@ __global__ void __launch_bounds__(256)
   for (int t = 0; t < kNT; ++t)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[t][e] = 0.f;
-  const int32_t t1max = A.rank == 2 ? A.K : 0;
-  for (int32_t t0 = -A.K; t0 <= A.K; ++t0) {
-    const int32_t i0 = p.i0 + t0 * A.dil;
+  const int32_t t1max = A.rank == 2 ? A.K1 : 0;
+  for (int32_t t0 = -A.K0; t0 <= A.K0; ++t0) {
+    const int32_t i0 = p.i0 + t0 * A.d0;
     if (i0 < 0 || i0 >= A.L0) continue;
-    const RWin w0 = rwin(A, i0, A.L0);
+    const RWin w0 = rwin0(A, i0);
     if (p.i0 < w0.s || p.i0 >= w0.e) continue;
-    const int32_t k0 = (p.i0 - w0.s) / A.dil;
+    const int32_t k0 = (p.i0 - w0.s) / A.d0;
     for (int32_t t1 = -t1max; t1 <= t1max; ++t1) {
-      const int32_t i1 = p.i1 + t1 * A.dil;
+      const int32_t i1 = p.i1 + t1 * A.d1;
       if (i1 < 0 || i1 >= A.L1) continue;
       const RWin w1 = rwin1(A, i1);
       if (p.i1 < w1.s || p.i1 >= w1.e) continue;
-      const int32_t k1 = (p.i1 - w1.s) / A.dil;
+      const int32_t k1 = (p.i1 - w1.s) / A.d1;
       const int64_t r = rrow(A, p.b, p.h, i0, i1);
       const float wt = w[r * A.KK + k0 * A.K1 + k1];
       float xv[kNT][VEC];
@@ -431,35 +438,35 @@ __global__ void __launch_bounds__(256)
     const int32_t i1 = qi - rest * A.L1;
     const int32_t b = (int32_t)fdiv((uint32_t)rest, A.fL0);
     const int32_t i0 = rest - b * A.L0;
-    sw0[tid] = rwin(A, i0, A.L0);
+    sw0[tid] = rwin0(A, i0);
     sw1[tid] = rwin1(A, i1);
     sb[tid] = b;
     si0[tid] = i0;
     si1[tid] = i1;
   }
   __syncthreads();
-  const int32_t nb = A.H * (A.rank == 2 ? A.R * A.R : A.R);
+  const int32_t per_h = A.R0 * A.R1;
+  const int32_t nb = A.H * per_h;
   for (int32_t bin = tid; bin < nb; bin += blockDim.x) {
-    const int32_t per_h = A.rank == 2 ? A.R * A.R : A.R;
     const int32_t h = bin / per_h;
     const int32_t rb = bin - h * per_h;
-    const int32_t r0 = A.rank == 2 ? rb / A.R : rb;
-    const int32_t r1 = A.rank == 2 ? rb - r0 * A.R : 0;
+    const int32_t r0 = rb / A.R1;
+    const int32_t r1 = rb - r0 * A.R1;
     float acc = 0.f;
     for (int32_t t = 0; t < nqc; ++t) {
       const RWin w0 = sw0[t];
       int32_t a0, b0;
-      slots_of_bias_row(r0, w0.pb, A.K, A.R, &a0, &b0);
+      slots_of_bias_row(r0, w0.pb, A.K0, A.R0, &a0, &b0);
       if (a0 > b0) continue;
       const RWin w1 = sw1[t];
       int32_t a1 = 0, b1 = 0;
-      if (A.rank == 2) slots_of_bias_row(r1, w1.pb, A.K, A.R, &a1, &b1);
+      if (A.rank == 2) slots_of_bias_row(r1, w1.pb, A.K1, A.R1, &a1, &b1);
       const float *row = dl + rrow(A, sb[t], h, si0[t], si1[t]) * A.KK;
       for (int32_t k0 = a0; k0 <= b0; ++k0) {
-        const int32_t j0 = w0.s + k0 * A.dil;
+        const int32_t j0 = w0.s + k0 * A.d0;
         if (j0 < 0 || j0 >= w0.e) continue;
         for (int32_t k1 = a1; k1 <= b1; ++k1) {
-          const int32_t j1 = w1.s + k1 * A.dil;
+          const int32_t j1 = w1.s + k1 * A.d1;
           if (j1 < 0 || j1 >= w1.e) continue;
           acc += row[k0 * A.K1 + k1];
         }
@@ -633,7 +640,7 @@ void rpb_av_fwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
 size_t rpb_bias_workspace_bytes(const RpbProb &A) {
   int32_t chunk, n_chunks;
   bias_chunking(A, &chunk, &n_chunks);
-  const size_t nb = (size_t)A.H * (A.rank == 2 ? A.R * A.R : A.R);
+  const size_t nb = (size_t)A.H * A.R0 * A.R1;
   return (size_t)n_chunks * nb * sizeof(float);
 }
 
@@ -651,7 +658,7 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
   if (drpb != nullptr) {
     int32_t chunk, n_chunks;
     bias_chunking(A, &chunk, &n_chunks);
-    const int32_t nb = A.H * (A.rank == 2 ? A.R * A.R : A.R);
+    const int32_t nb = A.H * A.R0 * A.R1;
     if (n_chunks > 0)
       hipLaunchKernelGGL(k_rpb_bias_partial, dim3((unsigned)n_chunks), dim3(256),
                          0, st, A, dlogits, workspace, chunk, n_chunks);

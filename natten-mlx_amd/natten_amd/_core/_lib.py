@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 NA_F32, NA_F16, NA_BF16 = 0, 1, 2
 NA_FLAG_DENSE = 1
 NA_FLAG_GENERIC = 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "launch failure",
            4: "workspace"}
@@ -60,8 +60,8 @@ class NaRpbParams(ctypes.Structure):
         ("heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("extent", ctypes.c_int32 * 2),
-        ("kernel", ctypes.c_int32),
-        ("dilation", ctypes.c_int32),
+        ("kernel", ctypes.c_int32 * 2),
+        ("dilation", ctypes.c_int32 * 2),
         ("heads_first", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("scale", ctypes.c_float),
@@ -175,14 +175,19 @@ def make_params(rank: int, batch: int, heads: int, kv_heads: int, head_dim: int,
     return p
 
 
-def make_rpb_params(rank: int, batch: int, heads: int, head_dim: int, extent, kernel: int,
-                    dilation: int, heads_first: bool, dtype: int,
+def make_rpb_params(rank: int, batch: int, heads: int, head_dim: int, extent, kernel,
+                    dilation, heads_first: bool, dtype: int,
                     scale: float | None) -> NaRpbParams:
+    """``kernel`` / ``dilation``: an int (every axis) or one value per axis."""
     p = NaRpbParams()
     p.rank, p.batch, p.heads, p.head_dim = rank, batch, heads, head_dim
     p.extent[0] = int(extent[0])
     p.extent[1] = int(extent[1]) if rank == 2 else 1
-    p.kernel, p.dilation = int(kernel), int(dilation)
+    ks = (kernel,) * rank if isinstance(kernel, int) else tuple(kernel)
+    ds = (dilation,) * rank if isinstance(dilation, int) else tuple(dilation)
+    for a in range(2):
+        p.kernel[a] = int(ks[a]) if a < rank else 1
+        p.dilation[a] = int(ds[a]) if a < rank else 1
     p.heads_first = 1 if heads_first else 0
     p.dtype = dtype
     p.scale = 1.0 if scale is None else float(scale)

@@ -307,15 +307,28 @@ def _rpb_geometry(x: torch.Tensor, heads_first: bool):
     return rank, x.shape[0], x.shape[-2], tuple(x.shape[1:-2]), x.shape[-1]
 
 
+def _per_axis(v, rank):
+    """An int (every axis) or a per-axis tuple, as a rank-long int tuple."""
+    if isinstance(v, (tuple, list)):
+        if len(v) != rank:
+            raise ValueError(f"expected {rank} per-axis values, got {tuple(v)}")
+        return tuple(int(x) for x in v)
+    return (int(v),) * rank
+
+
 def _rpb_params(x, kernel_size, dilation, heads_first, scale=None):
     rank, B, H, ext, D = _rpb_geometry(x, heads_first)
-    return _lib.make_rpb_params(rank, B, H, D, ext, int(kernel_size), int(dilation),
-                                heads_first, _lib.dtype_code(x.dtype), scale)
+    return _lib.make_rpb_params(rank, B, H, D, ext, _per_axis(kernel_size, rank),
+                                _per_axis(dilation, rank), heads_first,
+                                _lib.dtype_code(x.dtype), scale)
 
 
 def _slots_shape(x, kernel_size, heads_first):
     rank = x.dim() - 3
-    return tuple(x.shape[:-1]) + (int(kernel_size) ** rank,)
+    n = 1
+    for k in _per_axis(kernel_size, rank):
+        n *= k
+    return tuple(x.shape[:-1]) + (n,)
 
 
 def _check_same_layout(a, b, what):
@@ -325,8 +338,7 @@ def _check_same_layout(a, b, what):
 
 
 def _bias_shape(rank, heads, kernel_size):
-    r = 2 * int(kernel_size) - 1
-    return (heads, r) if rank == 1 else (heads, r, r)
+    return (heads,) + tuple(2 * k - 1 for k in _per_axis(kernel_size, rank))
 
 
 def rpb_qk_forward(q, k, rpb, kernel_size, dilation, scale=None, heads_first=False):

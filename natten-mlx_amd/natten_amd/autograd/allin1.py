@@ -53,15 +53,23 @@ class _AVRPB(torch.autograd.Function):
         return da, dv, None, None, None, None
 
 
+def _axes(v):
+    """An int, or a per-axis tuple of ints (non-square windows)."""
+    return tuple(int(x) for x in v) if isinstance(v, (tuple, list)) else int(v)
+
+
 def qk_rpb_with_grad(q, k, rpb, kernel_size, dilation, scale=None, heads_first=False):
-    """float32 logits of the fused QK + RPB op, differentiable in q, k, rpb."""
-    return _QKRPB.apply(q, k, rpb, int(kernel_size), int(dilation), scale, bool(heads_first))
+    """float32 logits of the fused QK + RPB op, differentiable in q, k, rpb.
+    kernel_size / dilation: an int or one value per axis."""
+    return _QKRPB.apply(q, k, rpb, _axes(kernel_size), _axes(dilation), scale,
+                        bool(heads_first))
 
 
 def av_rpb_with_grad(attn, v, kernel_size, dilation, heads_first=False,
                      out_dtype=torch.float32):
     """AV op output, differentiable in attn and v."""
-    return _AVRPB.apply(attn, v, int(kernel_size), int(dilation), bool(heads_first), out_dtype)
+    return _AVRPB.apply(attn, v, _axes(kernel_size), _axes(dilation), bool(heads_first),
+                        out_dtype)
 
 
 __all__ = ["qk_rpb_with_grad", "av_rpb_with_grad"]

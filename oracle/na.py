@@ -212,31 +212,39 @@ def _allin1_axis(L, K, d):
     return np.clip(pos, 0, L - 1), valid, bias
 
 
+def _axes_param(v, rank):
+    return tuple(int(x) for x in v) if isinstance(v, (tuple, list)) else (int(v),) * rank
+
+
 def _allin1_tables(spatial, K, d):
     """Flattened neighbor index, validity and bias index over all query
-    positions of a rank-1/2 grid: arrays [prod(spatial), K^rank]."""
-    axes = [_allin1_axis(L, K, d) for L in spatial]
+    positions of a rank-1/2 grid: arrays [prod(spatial), K0*K1].  K and d are
+    ints (every axis) or per-axis tuples; the 2D bias index is
+    r0 * (2*K1 - 1) + r1 (``compat/v014.py:26-49``)."""
+    Ks, ds = _axes_param(K, len(spatial)), _axes_param(d, len(spatial))
+    axes = [_allin1_axis(L, k, dd) for L, k, dd in zip(spatial, Ks, ds)]
     if len(spatial) == 1:
         pos, valid, bias = axes[0]
         return pos, valid, bias
     (p0, v0, b0), (p1, v1, b1) = axes
     L0, L1 = spatial
-    R = 2 * K - 1
-    lin = (p0[:, None, :, None] * L1 + p1[None, :, None, :]).reshape(L0 * L1, K * K)
-    val = (v0[:, None, :, None] & v1[None, :, None, :]).reshape(L0 * L1, K * K)
-    bia = (b0[:, None, :, None] * R + b1[None, :, None, :]).reshape(L0 * L1, K * K)
+    K0, K1 = Ks
+    R1 = 2 * K1 - 1
+    lin = (p0[:, None, :, None] * L1 + p1[None, :, None, :]).reshape(L0 * L1, K0 * K1)
+    val = (v0[:, None, :, None] & v1[None, :, None, :]).reshape(L0 * L1, K0 * K1)
+    bia = (b0[:, None, :, None] * R1 + b1[None, :, None, :]).reshape(L0 * L1, K0 * K1)
     return lin, val, bia
 
 
 def qk_rpb(q, k, rpb, kernel_size, dilation=1, scale=None, compute_dtype=torch.float64):
     """allin1 ``na{1,2}d_qk_rpb``: q ``[B, *L, H, D]`` -> logits
-    ``[B, *L, H, K^rank]``; rpb ``[H, 2K-1]`` or ``[H, 2K-1, 2K-1]``."""
+    ``[B, *L, H, K^rank]``; rpb ``[H, 2K-1]`` or ``[H, 2K0-1, 2K1-1]``.
+    kernel_size / dilation: int or per-axis tuple; scale None = no scaling."""
     if scale is not None:
         q = q * scale  # in the storage dtype, before the dot (``__init__.py:61-62``)
     B, H, D = q.shape[0], q.shape[-2], q.shape[-1]
     sp = tuple(q.shape[1:-2])
-    K, d = int(kernel_size), int(dilation)
-    lin, valid, bidx = _allin1_tables(sp, K, d)
+    lin, valid, bidx = _allin1_tables(sp, kernel_size, dilation)
     n, kk = lin.shape
     qf = q.to(compute_dtype).reshape(B, n, H, D)
     kn = k.to(compute_dtype).reshape(B, n, H, D)[:, torch.from_numpy(lin.reshape(-1))]
@@ -255,8 +263,7 @@ def av_rpb(attn, v, kernel_size, dilation=1, compute_dtype=torch.float64):
     """allin1 ``na{1,2}d_av_fused``: attn ``[B, *L, H, K^rank]``, v ``[B, *L, H, D]``."""
     B, H, D = v.shape[0], v.shape[-2], v.shape[-1]
     sp = tuple(v.shape[1:-2])
-    K, d = int(kernel_size), int(dilation)
-    lin, valid, _ = _allin1_tables(sp, K, d)
+    lin, valid, _ = _allin1_tables(sp, kernel_size, dilation)
     n, kk = lin.shape
     vn = v.to(compute_dtype).reshape(B, n, H, D)[:, torch.from_numpy(lin.reshape(-1))]
     vn = vn.reshape(B, n, kk, H, D)
