@@ -220,6 +220,18 @@ def profile_calls(n: int, workload: str = "cfg2") -> None:
         torch.cuda.synchronize()
         print(f"profile-calls: {n} x allin1 K=7 d=1 forward and backward done", flush=True)
         return
+    if workload == "merge":
+        shape = (1, 16, 32, 32, 8, 64)
+        outs = [_gen(shape, torch.bfloat16, s) for s in range(2)]
+        lses = [_gen(shape[:-1], torch.float32, 20 + s) for s in range(2)]
+        dout, dlse = _gen(shape, torch.bfloat16, 40), _gen(shape[:-1], torch.float32, 41)
+        for _ in range(n):
+            hip.merge_forward(outs, lses)
+            hip.merge_backward(outs, lses, dout, dlse, [True] * 2, [True] * 2)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x merge forward and backward (2 parts, config-3 size) done",
+              flush=True)
+        return
     a = ((K, K), (1, 1), (1, 1), (False, False), None)
     out, lse = hip.fused_forward(q, k, v, *a)
     # calibration for the HBM byte counters: a plain device copy of a known
@@ -422,6 +434,56 @@ def wl_cfg5(args):
                  cfg, rq if rq["call_ms"] >= ra["call_ms"] else ra, {"sweep": table})
 
 
+def wl_merge(args):
+    """merge_attentions of 2 and 4 parts with their LSEs at the config-3
+    output size [1,16,32,32,8,64] bf16 (and config 2's [4,56,56,4,32]),
+    forward and backward kernels; the torch composition of the reference's
+    sigmoid form (merge.py:56-66) timed beside."""
+    import torch.nn.functional as tF
+
+    from natten_amd._core import hip
+
+    def torch_merge(outs, lses):
+        ls = [l.unsqueeze(-1) for l in lses]
+        os_ = [o.float() for o in outs]
+        out = os_[0] - torch.sigmoid(ls[1] - ls[0]) * (os_[0] - os_[1])
+        acc = ls[0] - tF.logsigmoid(ls[0] - ls[1])
+        for i in range(2, len(os_)):
+            out = out - torch.sigmoid(ls[i] - acc) * (out - os_[i])
+            acc = acc - tF.logsigmoid(acc - ls[i])
+        return out.to(outs[0].dtype), acc.squeeze(-1)
+
+    table = {}
+    main = None
+    for name, shape in (("cfg3", (1, 16, 32, 32, 8, 64)), ("cfg2", (4, 56, 56, 4, 32))):
+        rows = 1
+        for x in shape[:-1]:
+            rows *= x
+        Dm = shape[-1]
+        for n in (2, 4):
+            outs = [_gen(shape, torch.bfloat16, s) for s in range(n)]
+            lses = [_gen(shape[:-1], torch.float32, 20 + s) for s in range(n)]
+            dout = _gen(shape, torch.bfloat16, 40)
+            dlse = _gen(shape[:-1], torch.float32, 41)
+            part = rows * Dm * 2 + rows * 4
+            fwd_b = (n + 1) * part
+            bwd_b = (2 * n + 1) * part
+            f_ms = time_calls(lambda: hip.merge_forward(outs, lses), args.steps)
+            b_ms = time_calls(lambda: hip.merge_backward(outs, lses, dout, dlse, [True] * n,
+                                                         [True] * n), args.steps)
+            t_ms = time_calls(lambda: torch_merge(outs, lses), args.steps)
+            rf = _roof("na_merge_fwd", fwd_b, 2 * n * rows * Dm, f_ms, 157.3)
+            rb = _roof("na_merge_bwd", bwd_b, 4 * n * rows * Dm, b_ms, 157.3)
+            table[f"{name}_n{n}"] = {"fwd": rf, "bwd": rb, "torch_sigmoid_form_ms": round(t_ms, 5)}
+            if name == "cfg3" and n == 2:
+                main = (rf, rb, f_ms + b_ms, (fwd_b + bwd_b) / ((f_ms + b_ms) * 1e-3) / 1e9)
+    rf, rb, ms, gbs = main
+    cfg = {"workload": "merge_attentions, 2 bf16 parts [1,16,32,32,8,64] + fp32 LSEs, "
+                       "forward + backward (other sizes in 'sweep')", "global_batch": 1}
+    return _line("merge_attentions bf16 fwd+bwd HBM GB/s, 1 MI355X", gbs, "GB/s", ms, "bf16",
+                 cfg, rf if rf["call_ms"] >= rb["call_ms"] else rb, {"sweep": table})
+
+
 def _eager_ms(step, args):
     for _ in range(args.warmup):
         step()
@@ -433,7 +495,8 @@ def _eager_ms(step, args):
     return (time.perf_counter() - t0) * 1e3 / args.steps
 
 
-WORKLOADS = {"split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4, "cfg5": wl_cfg5}
+WORKLOADS = {"split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4, "cfg5": wl_cfg5,
+             "merge": wl_merge}
 
 
 def run_cpu_baseline():

@@ -230,6 +230,40 @@ int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,
                   const void *dout, int32_t out_dtype, float *dattn,
                   void *dvalue, void *stream);
 
+/* ---- merge of attention outputs --------------------------------------- */
+
+#define NA_MERGE_MAX_PARTS 8
+
+typedef struct na_merge_params {
+  int32_t n_parts;  /* 2 .. NA_MERGE_MAX_PARTS */
+  int32_t head_dim; /* D, the last axis of every output */
+  int64_t rows;     /* product of the leading axes ([B, *spatial, H]) */
+  int32_t dtype;    /* storage type of the outputs, the merged output and
+                       their gradients */
+} na_merge_params;
+
+/*
+ * Merges outputs that share their queries as if their key/value sets had
+ * been concatenated: L = logsumexp_i lse_i, out = sum_i exp(lse_i - L) out_i
+ * (the closed form of the reference's sigmoid merge), one pass.  outs / lses
+ * are host arrays of n_parts device pointers ([rows, D] in dtype, [rows]
+ * float32); lse receives L (float32).  Replaces merge.py:20-68
+ * (merge_attentions).
+ */
+int na_merge_fwd(const na_merge_params *p, const void *const *outs,
+                 const float *const *lses, void *out, float *lse,
+                 void *stream);
+/*
+ * Gradients of na_merge_fwd: d_outs[i] = w_i * dout and
+ * d_lses[i] = w_i * (<dout, out_i> - sum_j w_j <dout, out_j> + dlse) with
+ * w_i = exp(lse_i - L).  dlse may be NULL (zero); d_outs / d_lses may be
+ * NULL, as may any of their entries (not computed).  The MLX autodiff of
+ * merge.py:56-68 is what this replaces.
+ */
+int na_merge_bwd(const na_merge_params *p, const void *const *outs,
+                 const float *const *lses, const void *dout, const float *dlse,
+                 void *const *d_outs, float *const *d_lses, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

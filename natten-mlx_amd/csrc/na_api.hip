@@ -189,6 +189,32 @@ int check_out_dtype(const na_rpb_params *p, int32_t out_dtype) {
   return NA_OK;
 }
 
+int check_merge(const na_merge_params *p, const void *const *outs,
+                const float *const *lses) {
+  static_assert(NA_MERGE_MAX_PARTS == na::kMergeMaxParts,
+                "merge part limit of the header and the kernels");
+  if (p == nullptr) return fail(NA_ERR_INVALID, "params is NULL");
+  if (p->n_parts < 2 || p->n_parts > NA_MERGE_MAX_PARTS)
+    return fail(NA_ERR_INVALID, "n_parts must be in [2, %d], got %d",
+                NA_MERGE_MAX_PARTS, p->n_parts);
+  if (p->dtype != NA_F32 && p->dtype != NA_F16 && p->dtype != NA_BF16)
+    return fail(NA_ERR_INVALID, "unknown dtype %d", p->dtype);
+  if (p->rows < 0 || p->head_dim < 1)
+    return fail(NA_ERR_INVALID, "rows must be >= 0 and head_dim positive");
+  if ((p->head_dim % 8 != 0 && p->head_dim > 128) ||
+      p->head_dim > kMaxHeadDim)
+    return fail(NA_ERR_UNSUPPORTED, "head_dim %d is not supported",
+                p->head_dim);
+  if (p->rows * p->head_dim > ((int64_t)1 << 38))
+    return fail(NA_ERR_UNSUPPORTED, "merge problem too large");
+  if (outs == nullptr || lses == nullptr)
+    return fail(NA_ERR_INVALID, "outs/lses must be non-NULL");
+  for (int i = 0; i < p->n_parts; ++i)
+    if (outs[i] == nullptr || lses[i] == nullptr)
+      return fail(NA_ERR_INVALID, "outs[%d]/lses[%d] is NULL", i, i);
+  return NA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -448,6 +474,31 @@ int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,
   na::rpb_av_bwd(A, p->dtype, out_dtype, attn, value, dout, dattn, dvalue,
                  as_stream(stream));
   return launch_status("na_rpb_av_bwd");
+}
+
+int na_merge_fwd(const na_merge_params *p, const void *const *outs,
+                 const float *const *lses, void *out, float *lse,
+                 void *stream) {
+  const int rc = check_merge(p, outs, lses);
+  if (rc != NA_OK) return rc;
+  if (p->rows == 0) return NA_OK;
+  if (out == nullptr || lse == nullptr)
+    return fail(NA_ERR_INVALID, "out/lse must be non-NULL");
+  na::merge_fwd(p->dtype, p->n_parts, p->rows, p->head_dim, outs, lses, out,
+                lse, as_stream(stream));
+  return launch_status("na_merge_fwd");
+}
+
+int na_merge_bwd(const na_merge_params *p, const void *const *outs,
+                 const float *const *lses, const void *dout, const float *dlse,
+                 void *const *d_outs, float *const *d_lses, void *stream) {
+  const int rc = check_merge(p, outs, lses);
+  if (rc != NA_OK) return rc;
+  if (p->rows == 0) return NA_OK;
+  if (dout == nullptr) return fail(NA_ERR_INVALID, "dout must be non-NULL");
+  na::merge_bwd(p->dtype, p->n_parts, p->rows, p->head_dim, outs, lses, dout,
+                dlse, d_outs, d_lses, as_stream(stream));
+  return launch_status("na_merge_bwd");
 }
 
 }  // extern "C"

@@ -82,6 +82,16 @@ void msplit_av(const Prob &P, int dtype, const void *a, const void *y,
 void msplit_inv(const Prob &P, int dtype, const void *a, const void *x,
                 void *out, float scale, hipStream_t st);
 
+// Merge of attention outputs sharing their queries (na_merge.hip): up to
+// kMergeMaxParts parts of rows x D elements in `dtype`, LSEs float32.
+constexpr int kMergeMaxParts = 8;
+void merge_fwd(int dtype, int n, int64_t rows, int D, const void *const *outs,
+               const float *const *lses, void *out, float *lse,
+               hipStream_t st);
+void merge_bwd(int dtype, int n, int64_t rows, int D, const void *const *outs,
+               const float *const *lses, const void *dout, const float *dlse,
+               void *const *d_outs, float *const *d_lses, hipStream_t st);
+
 // Generic pieces reused around the MFMA backward.
 void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
                 const float *dlse, float *delta, hipStream_t st);

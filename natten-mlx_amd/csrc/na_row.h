@@ -106,4 +106,60 @@ __device__ __forceinline__ Group make_group(int lgG, int64_t n_groups) {
   return g;
 }
 
+// ---- launch shape ----------------------------------------------------------
+// 16-byte accesses when D allows, NT = 4 chunks per lane past 32 chunks, and
+// the fewest lanes per row (a power of two) that cover D.
+struct Shape {
+  int vec, nt, G, lgG;
+};
+
+template <typename T>
+Shape pick_shape(int D) {
+  Shape s;
+  const int vmax = 16 / (int)sizeof(T);
+  s.vec = (D % vmax == 0) ? vmax : 1;
+  const int chunks = (D + s.vec - 1) / s.vec;
+  s.nt = chunks > 32 ? 4 : 1;
+  const int per = (chunks + s.nt - 1) / s.nt;
+  s.G = 1;
+  s.lgG = 0;
+  while (s.G < per) {
+    s.G <<= 1;
+    ++s.lgG;
+  }
+  return s;
+}
+
+inline dim3 grid_for(int64_t n_groups, int lgG) {
+  const int64_t threads = n_groups << lgG;
+  return dim3((unsigned)((threads + 255) / 256));
+}
+
+// Expands `body` with the compile-time (VEC, NT) matching shape s.
+#define NA_VALU_DISPATCH(T, s, LAUNCH)                                  \
+  do {                                                                  \
+    constexpr int VMAX = 16 / (int)sizeof(T);                           \
+    if ((s).vec == VMAX && (s).nt == 1) {                               \
+      LAUNCH(T, VMAX, 1);                                               \
+    } else if ((s).vec == VMAX) {                                       \
+      LAUNCH(T, VMAX, 4);                                               \
+    } else if ((s).nt == 1) {                                           \
+      LAUNCH(T, 1, 1);                                                  \
+    } else {                                                            \
+      LAUNCH(T, 1, 4);                                                  \
+    }                                                                   \
+  } while (0)
+
+// Calls FN<storage type of dtype code dt>(...).
+#define NA_BY_DTYPE(dt, FN, ...)             \
+  do {                                       \
+    if ((dt) == NA_F32) {                    \
+      FN<float>(__VA_ARGS__);                \
+    } else if ((dt) == NA_F16) {             \
+      FN<f16_t>(__VA_ARGS__);                \
+    } else {                                 \
+      FN<bf16_t>(__VA_ARGS__);               \
+    }                                        \
+  } while (0)
+
 }  // namespace na

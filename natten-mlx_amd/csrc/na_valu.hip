@@ -546,48 +546,7 @@ __global__ void k_table(Prob P, int32_t *__restrict__ index,
 }
 
 // ---------------------------------------------------------------------------
-// Launch helpers.
-
-struct Shape {
-  int vec, nt, G, lgG;
-};
-
-template <typename T>
-Shape pick_shape(int D) {
-  Shape s;
-  const int vmax = 16 / (int)sizeof(T);
-  s.vec = (D % vmax == 0) ? vmax : 1;
-  const int chunks = (D + s.vec - 1) / s.vec;
-  s.nt = chunks > 32 ? 4 : 1;
-  const int per = (chunks + s.nt - 1) / s.nt;
-  s.G = 1;
-  s.lgG = 0;
-  while (s.G < per) {
-    s.G <<= 1;
-    ++s.lgG;
-  }
-  return s;
-}
-
-inline dim3 grid_for(int64_t n_groups, int lgG) {
-  const int64_t threads = n_groups << lgG;
-  return dim3((unsigned)((threads + 255) / 256));
-}
-
-// Expands `body` with the compile-time (VEC, NT) matching shape s.
-#define NA_VALU_DISPATCH(T, s, LAUNCH)                                  \
-  do {                                                                  \
-    constexpr int VMAX = 16 / (int)sizeof(T);                           \
-    if ((s).vec == VMAX && (s).nt == 1) {                               \
-      LAUNCH(T, VMAX, 1);                                               \
-    } else if ((s).vec == VMAX) {                                       \
-      LAUNCH(T, VMAX, 4);                                               \
-    } else if ((s).nt == 1) {                                           \
-      LAUNCH(T, 1, 1);                                                  \
-    } else {                                                            \
-      LAUNCH(T, 1, 4);                                                  \
-    }                                                                   \
-  } while (0)
+// Launch helpers (launch shapes: na_row.h).
 
 template <typename T>
 void fwd_t(const Prob &P, const void *q, const void *k, const void *v,
@@ -734,17 +693,6 @@ void av_bwd_t(const Prob &P, const void *attn, const void *v, const void *dout,
 }
 
 }  // namespace
-
-#define NA_BY_DTYPE(dt, FN, ...)             \
-  do {                                       \
-    if ((dt) == NA_F32) {                    \
-      FN<float>(__VA_ARGS__);                \
-    } else if ((dt) == NA_F16) {             \
-      FN<f16_t>(__VA_ARGS__);                \
-    } else {                                 \
-      FN<bf16_t>(__VA_ARGS__);               \
-    }                                        \
-  } while (0)
 
 void valu_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,

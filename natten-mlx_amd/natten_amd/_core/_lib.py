@@ -69,8 +69,23 @@ class NaRpbParams(ctypes.Structure):
     ]
 
 
+class NaMergeParams(ctypes.Structure):
+    """Mirror of ``na_merge_params`` (include/natten_amd.h)."""
+
+    _fields_ = [
+        ("n_parts", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
+MERGE_MAX_PARTS = 8
+
 _P = ctypes.POINTER(NaParams)
 _R = ctypes.POINTER(NaRpbParams)
+_M = ctypes.POINTER(NaMergeParams)
+_PP = ctypes.POINTER(ctypes.c_void_p)  # host array of device pointers
 _V = ctypes.c_void_p
 _I = ctypes.c_int32
 
@@ -96,6 +111,8 @@ SIGNATURES = {
     "na_rpb_bwd_workspace_bytes": (ctypes.c_size_t, [_R]),
     "na_rpb_qk_bwd": (ctypes.c_int, [_R, _V, _V, _V, _V, _V, _V, _V, ctypes.c_size_t, _V]),
     "na_rpb_av_bwd": (ctypes.c_int, [_R, _V, _V, _V, _I, _V, _V, _V]),
+    "na_merge_fwd": (ctypes.c_int, [_M, _PP, _PP, _V, _V, _V]),
+    "na_merge_bwd": (ctypes.c_int, [_M, _PP, _PP, _V, _V, _PP, _PP, _V]),
 }
 
 _lib = None
@@ -152,6 +169,14 @@ def dtype_code(dt: torch.dtype) -> int:
 
 def ptr(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def ptr_array(tensors):
+    """Host array of device pointers (NULL for None entries)."""
+    arr = (ctypes.c_void_p * len(tensors))()
+    for i, t in enumerate(tensors):
+        arr[i] = None if t is None else t.data_ptr()
+    return arr
 
 
 def stream_of(t: torch.Tensor):

@@ -428,3 +428,56 @@ def rpb_av_backward(attn, v, d_out, kernel_size, dilation, heads_first=False, ne
                                  _lib.dtype_code(do.dtype), _lib.ptr(da), _lib.ptr(dv),
                                  _lib.stream_of(v)), "na_rpb_av_bwd")
     return da, dv
+
+
+# ---------------------------------------------------------------------------
+# merge of attention outputs (C ABI na_merge_fwd / na_merge_bwd)
+
+def _merge_params(outs, lses):
+    n = len(outs)
+    if not 2 <= n <= _lib.MERGE_MAX_PARTS:
+        raise ValueError(f"a merge call takes 2..{_lib.MERGE_MAX_PARTS} parts, got {n}")
+    o0 = outs[0]
+    for o, l in zip(outs, lses):
+        if o.dtype != o0.dtype or tuple(o.shape) != tuple(o0.shape):
+            raise ValueError("merge parts must share shape and dtype")
+        if l.dtype != torch.float32 or tuple(l.shape) != tuple(o0.shape[:-1]):
+            raise ValueError("merge LSEs must be float32 with the outputs' leading shape")
+    p = _lib.NaMergeParams()
+    p.n_parts = n
+    p.head_dim = int(o0.shape[-1])
+    p.rows = int(o0.numel() // max(int(o0.shape[-1]), 1))
+    p.dtype = _lib.dtype_code(o0.dtype)
+    return p
+
+
+def merge_forward(outs, lses):
+    """(out, lse float32) of the concatenated-keys merge, one kernel pass."""
+    _require_device(*outs, *lses)
+    outs = [_c(o) for o in outs]
+    lses = [_c(l) for l in lses]
+    p = _merge_params(outs, lses)
+    out = torch.empty_like(outs[0])
+    lse = torch.empty(outs[0].shape[:-1], dtype=torch.float32, device=outs[0].device)
+    lib = _lib.load()
+    _lib.check(lib.na_merge_fwd(p, _lib.ptr_array(outs), _lib.ptr_array(lses), _lib.ptr(out),
+                                _lib.ptr(lse), _lib.stream_of(out)), "na_merge_fwd")
+    return out, lse
+
+
+def merge_backward(outs, lses, d_out, d_lse, need_outs, need_lses):
+    """Per-part gradients of ``merge_forward``: d_outs in the parts' dtype,
+    d_lses float32; entries not needed come back as None."""
+    _require_device(*outs, *lses, d_out, d_lse)
+    outs = [_c(o) for o in outs]
+    lses = [_c(l) for l in lses]
+    p = _merge_params(outs, lses)
+    do = _c(d_out.to(outs[0].dtype))
+    dl = None if d_lse is None else _c(d_lse.to(torch.float32))
+    d_outs = [torch.empty_like(o) if need else None for o, need in zip(outs, need_outs)]
+    d_lses = [torch.empty_like(l) if need else None for l, need in zip(lses, need_lses)]
+    lib = _lib.load()
+    _lib.check(lib.na_merge_bwd(p, _lib.ptr_array(outs), _lib.ptr_array(lses), _lib.ptr(do),
+                                _lib.ptr(dl), _lib.ptr_array(d_outs), _lib.ptr_array(d_lses),
+                                _lib.stream_of(do)), "na_merge_bwd")
+    return d_outs, d_lses

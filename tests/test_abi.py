@@ -27,6 +27,7 @@ def test_header_declares_expected_entry_points():
     for n in ("na_fwd", "na_bwd", "na_bwd_workspace_bytes", "na_qk_fwd", "na_av_fwd",
               "na_qk_bwd", "na_av_bwd", "na_rpb_qk_fwd", "na_rpb_av_fwd", "na_rpb_qk_bwd",
               "na_rpb_av_bwd", "na_rpb_bwd_workspace_bytes",
+              "na_merge_fwd", "na_merge_bwd",
               "na_neighbor_table", "na_last_error", "na_abi_version"):
         assert n in names
 
