@@ -58,6 +58,7 @@ def sources() -> list[str]:
 # their softmax arithmetic would otherwise need.
 EXTRA_FLAGS = {
     "na_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "na_lean.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -116,6 +116,10 @@ bool use_mfma(const na_params *p, const na::Prob &P) {
   return (p->flags & NA_FLAG_GENERIC) == 0 && na::mfma_eligible(P, p->dtype);
 }
 
+bool use_lean(const na_params *p, const na::Prob &P) {
+  return (p->flags & NA_FLAG_GENERIC) == 0 && na::lean_eligible(P, p->dtype);
+}
+
 bool use_msplit(const na_params *p, const na::Prob &P) {
   return (p->flags & NA_FLAG_GENERIC) == 0 && na::msplit_eligible(P, p->dtype);
 }
@@ -278,7 +282,9 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
     return fail(NA_ERR_INVALID, "q/k/v/out must be non-NULL");
   if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
     return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
-  if (use_mfma(p, P))
+  if (use_lean(p, P))
+    na::lean_fwd(P, p->dtype, q, k, v, out, lse, as_stream(stream));
+  else if (use_mfma(p, P))
     na::mfma_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
                  as_stream(stream));
   else

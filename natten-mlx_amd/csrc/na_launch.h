@@ -69,6 +69,13 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
               hipStream_t st);
 void mfma_selftest(int dtype, float *out, hipStream_t st);
 
+// Lean matrix-core fused forward (na_lean.hip): the MFMA-eligible problems
+// with one extent per sample, no additional tokens, not dense, and d*K <= L
+// on every non-causal axis.
+bool lean_eligible(const Prob &P, int dtype);
+void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, void *out, float *lse, hipStream_t st);
+
 // Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with
 // d*K <= L on every non-causal axis and at most 512 kernel slots.
 bool msplit_eligible(const Prob &P, int dtype);

@@ -1,0 +1,712 @@
+// na_lean.hip — lean matrix-core (gfx950) fused kernels for the common
+// neighborhood problems.
+//
+// Problem class (lean_eligible): bf16/fp16, head_dim 32/64/128, stride 1,
+// one extent for every sample, no additional tokens, not dense, and on every
+// non-causal axis an odd K with d*K <= L.  On such an axis the window of the
+// query at index i of its dilation phase (Lr points, sub-grid coordinates)
+// is [clamp(i - K/2, 0, Lr - K), + K); on a causal axis [max(i - K + 1, 0),
+// i].  Both are monotone in i, so the windows of a box of queries cover a
+// box of keys and the queries whose windows hold a key form a box too.
+//
+// Tiling.  A wave owns 16 queries of one phase: a T0 x T1 x T2 box of
+// powers of two (product 16).  The union of their windows is a box of keys
+// whose innermost extent is padded to 16 * CPR slots, so a chunk of 16 keys
+// lies inside one box row and its row is wave-uniform.  Per chunk:
+//   S^T = K . Q^T            mfma_f32_16x16x32 (A = K rows, B = Q rows, both
+//                            straight from global memory); lane l holds the
+//                            scores of query l%16 with keys 4(l/16) + r
+//   masked online softmax   the row test is one compare per lane and chunk,
+//                            the column tests are per lane and fixed
+//   O^T += V^T . P^T         V rows are written to LDS with 16-byte stores and
+//                            come back transposed (ds_read_tr16_b64) as the A
+//                            operand; two chunks per MFMA, the scores of both
+//                            packed as the B operand with the same k order.
+// A group of NB = 256/D chunks is loaded at once; the next group's loads are
+// issued as soon as the current group's K and V registers are consumed.
+#include <cmath>
+#include <cstdlib>
+
+#include "na_common.h"
+#include "na_launch.h"
+
+namespace na {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct L16;
+template <>
+struct L16<bf16_t> {
+  typedef __bf16 e;
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v4 tr(const e *p) {
+    typedef __attribute__((address_space(3))) v4 lv4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lv4 *)(p));
+  }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+template <>
+struct L16<f16_t> {
+  typedef _Float16 e;
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v4 tr(const e *p) {
+    typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+    typedef __attribute__((address_space(3))) h4 lh4;
+    return __builtin_bit_cast(v4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lh4 *)(p)));
+  }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+};
+
+// One spatial axis of a lean problem (unit axes: L = K = T = d = 1).
+struct LAx {
+  int32_t L, K, d, causal, nh;
+  int32_t Lq, Lrem;   // L / d and L % d: phase r holds Lq + (r < Lrem) points
+  int32_t T, lgT;     // wave tile extent (power of two)
+  int32_t TW, lgTW;   // workgroup tile extent: T, times W on the stack axis
+  int32_t nt;         // workgroup tiles per phase (of the longest phase)
+  int32_t Em;         // workgroup key-box extent of the LDS layout (maximum)
+  int32_t tok;        // token stride of one position step along this axis
+  FastDiv fG;         // tile-grid extent d * nt
+  FastDiv fnt;        // nt
+};
+
+struct LProb {
+  LAx ax[3];
+  int32_t B, H, Hkv, D;
+  int32_t Ltot;       // tokens per sample
+  float sl2;          // scale * log2(e)
+  int32_t n_tiles, n_launch;
+  int32_t sa;         // stack axis: the workgroup's waves tile this axis
+  int32_t ebox;       // Em0 * Em1 * Em2
+  FastDiv fH, fRep;
+  FastDiv fE2, fE1;   // box decode: key index -> (e0, e1, e2)
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ int xcd_tile(int bid, int n_launch) {
+  // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a
+  // contiguous range of tiles so neighbouring tiles share its L2.
+  return (bid & 7) * (n_launch >> 3) + (bid >> 3);
+}
+
+// Window [start, end) of sub-grid index i on an axis whose phase has Lr
+// points (branch-free: both rules are evaluated and one is selected).
+__device__ __forceinline__ int wstart(const LAx &x, int i, int Lr) {
+  const int nc = min(max(i - x.nh, 0), Lr - x.K);
+  const int ca = max(i - x.K + 1, 0);
+  const int sel = -x.causal;
+  return (ca & sel) | (nc & ~sel);
+}
+__device__ __forceinline__ int wend(const LAx &x, int i, int Lr) {
+  const int nc = min(max(i - x.nh, 0), Lr - x.K) + x.K;
+  const int sel = -x.causal;
+  return ((i + 1) & sel) | (nc & ~sel);
+}
+
+// LDS row stride (elements) of staged rows: 16 bytes of skew keep the
+// 16-byte stores, the 16-byte operand reads and the transposing reads at
+// the minimum number of bank passes.
+constexpr int lds_row(int D) { return D + 8; }
+// Key rows of slack after a staged box: a chunk read near the box end may
+// run up to 15 rows past it.
+constexpr int kSlack = 16;
+
+// Workgroup tile: everything wave-uniform about a tile of 16 W queries and
+// its key box [lo, lo + E) per axis.
+struct LTile {
+  int b, head, hk;
+  int r[3], i0[3], nv[3], Lr[3];
+  int lo[3], E[3];
+  int kbase;          // element offset of box point (0,0,0), head hk
+  int SK[3];          // element stride of one box step per axis (K/V)
+};
+
+template <int R>
+__device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
+                                            LTile &t) {
+  // tiles at or beyond n_tiles decode to a batch index >= B
+  uint32_t rest = (uint32_t)tile;
+  int g[3] = {0, 0, 0};
+#pragma unroll
+  for (int a = 2; a >= 3 - R; --a) {
+    const uint32_t qd = fdiv(rest, P.ax[a].fG);
+    g[a] = (int)(rest - qd * P.ax[a].fG.d);
+    rest = qd;
+  }
+  const uint32_t bq = fdiv(rest, P.fH);
+  t.head = (int)(rest - bq * P.fH.d);
+  t.b = (int)bq;
+  t.hk = (int)fdiv((uint32_t)t.head, P.fRep);
+  int tok0 = t.b * P.Ltot;
+  bool any = t.b < P.B;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const LAx &x = P.ax[a];
+    if (a < 3 - R) {
+      t.r[a] = 0; t.i0[a] = 0; t.nv[a] = 1; t.Lr[a] = 1; t.lo[a] = 0; t.E[a] = 1;
+      t.SK[a] = 0;
+      continue;
+    }
+    const int rr = (int)fdiv((uint32_t)g[a], x.fnt);
+    t.r[a] = rr;
+    t.i0[a] = (g[a] - rr * x.nt) << x.lgTW;
+    t.Lr[a] = x.Lq + (rr < x.Lrem ? 1 : 0);
+    t.nv[a] = min(t.Lr[a] - t.i0[a], x.TW);
+    any = any & (t.nv[a] > 0);
+    const int nvc = max(t.nv[a], 1);
+    t.lo[a] = wstart(x, t.i0[a], t.Lr[a]);
+    t.E[a] = wend(x, t.i0[a] + nvc - 1, t.Lr[a]) - t.lo[a];
+    tok0 += (rr + x.d * t.lo[a]) * x.tok;
+    t.SK[a] = x.d * x.tok * P.Hkv * P.D;
+  }
+  t.kbase = (tok0 * P.Hkv + t.hk) * P.D;
+  return any;
+}
+
+// A wave's part of a workgroup tile: its 16 queries (wave tile w along the
+// stack axis) and the sub-box of the workgroup box their windows cover,
+// walked as rows (e0, e1) x column segments of 16 keys from ws2.
+struct WSub {
+  int i0[3], nv[3];
+  int ws[3], we[3];
+  int cpr, nchunks;
+  bool any;
+};
+
+template <int R>
+__device__ __forceinline__ WSub wave_sub(const LProb &P, const LTile &t,
+                                         int w) {
+  WSub s;
+  s.any = true;
+  int rows = 1;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (a < 3 - R) {
+      s.i0[a] = 0; s.nv[a] = 1; s.ws[a] = 0; s.we[a] = 1;
+      continue;
+    }
+    const LAx &x = P.ax[a];
+    const int off = a == P.sa ? w * x.T : 0;
+    s.i0[a] = t.i0[a] + off;
+    s.nv[a] = min(t.nv[a] - off, x.T);
+    s.any = s.any & (s.nv[a] > 0);
+    const int nvc = max(s.nv[a], 1);
+    s.ws[a] = wstart(x, s.i0[a], t.Lr[a]) - t.lo[a];
+    s.we[a] = wend(x, s.i0[a] + nvc - 1, t.Lr[a]) - t.lo[a];
+    if (a < 2) rows *= s.we[a] - s.ws[a];
+  }
+  s.cpr = (s.we[2] - s.ws[2] + 15) >> 4;
+  s.nchunks = rows * s.cpr;
+  return s;
+}
+
+// Chunk cursor over a wave's sub-box (chunks are visited in order).
+struct Cursor {
+  int e0, e1, cs;
+};
+
+__device__ __forceinline__ void advance(Cursor &cu, const WSub &s) {
+  // branch-free: selects on wave-uniform values
+  const int cs = cu.cs + 1;
+  const bool w1 = cs == s.cpr;
+  cu.cs = w1 ? 0 : cs;
+  const int e1 = cu.e1 + (w1 ? 1 : 0);
+  const bool w2 = e1 == s.we[1];
+  cu.e1 = w2 ? s.ws[1] : e1;
+  cu.e0 += w2 ? 1 : 0;
+}
+
+template <typename T>
+__device__ __forceinline__ typename L16<T>::v8 ld8(const T *p) {
+  return *reinterpret_cast<const typename L16<T>::v8 *>(p);
+}
+
+__device__ __forceinline__ f32x4 zero4() {
+  f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return z;
+}
+
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 that hold one
+// query's scores (two lane-swap butterflies, no LDS traffic).
+__device__ __forceinline__ float quad_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                                  __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x),
+                                                  __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                                  __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x),
+                                                  __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// In-wave LDS ordering: this wave's LDS operations are complete.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Stage a workgroup's box of rows of two tensors (x, y: K and V, or Q and
+// dO) into LDS: row kk = (e0 * Em1 + e1) * Em2 + e2 of the box layout at
+// element kk * lds_row(D), points past the tile's true box clamped onto it
+// (their rows are real rows, so every staged value is finite).  Loads go
+// four 16-byte units per lane at a time, all in flight together.
+template <typename T, int D>
+__device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
+                                          const T *__restrict__ x,
+                                          const T *__restrict__ y,
+                                          typename L16<T>::e *xs,
+                                          typename L16<T>::e *ys, int tid,
+                                          int nthr) {
+  typedef typename L16<T>::v8 v8;
+  constexpr int OCT = D / 8;  // 16-byte units per row
+  constexpr int RSE = lds_row(D);
+  const int nun = P.ebox * OCT;
+  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
+    v8 xr[4], yr[4];
+    int la[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = min(u0 + j * nthr + tid, nun - 1);
+      const int kk = u / OCT, o = u % OCT;
+      const uint32_t t1 = fdiv((uint32_t)kk, P.fE2);
+      const int e2 = kk - (int)t1 * P.ax[2].Em;
+      const uint32_t e0 = fdiv(t1, P.fE1);
+      const int e1 = (int)t1 - (int)e0 * P.ax[1].Em;
+      const int g = t.kbase + min((int)e0, t.E[0] - 1) * t.SK[0] +
+                    min(e1, t.E[1] - 1) * t.SK[1] + min(e2, t.E[2] - 1) * t.SK[2] +
+                    8 * o;
+      xr[j] = ld8(x + g);
+      yr[j] = ld8(y + g);
+      la[j] = kk * RSE + 8 * o;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<v8 *>(xs + la[j]) = xr[j];
+      *reinterpret_cast<v8 *>(ys + la[j]) = yr[j];
+    }
+  }
+  // slack rows after the box: zero (a chunk read near the end of the box
+  // may include them; zero rows keep every MFMA operand finite)
+  constexpr int SLU = kSlack * RSE / 8;  // 16-byte units of slack
+  for (int u = tid; u < SLU; u += nthr) {
+    v8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (typename L16<T>::e)0.f;
+    *reinterpret_cast<v8 *>(xs + P.ebox * RSE + 8 * u) = z;
+    *reinterpret_cast<v8 *>(ys + P.ebox * RSE + 8 * u) = z;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  A workgroup of W waves owns W wave tiles stacked along the
+// stack axis; its K/V box is staged in LDS once, then each wave runs the
+// chunks of its own sub-box.  R: rank; CPR1: every wave sub-box row is one
+// chunk (at most 16 keys wide), so the per-lane column tests are fixed.
+template <typename T, int D, int R, bool CPR1>
+__global__ void __launch_bounds__(256)
+    k_wfwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
+           const T *__restrict__ v, T *__restrict__ out,
+           float *__restrict__ lse) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::v2 v2;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;    // 32-wide k-steps over head_dim
+  constexpr int NB = 256 / D;   // chunks per softmax group
+  constexpr int NDB = D / 16;   // 16-row blocks of O^T
+  constexpr int RSE = lds_row(D);
+  extern __shared__ __align__(16) char smem[];
+
+  // setup is straight-line arithmetic on kernel arguments (so their loads
+  // issue together); the exit test comes after it
+  LTile t;
+  const bool tile_any = decode_tile<R>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  const WSub ws = wave_sub<R>(P, t, w);
+
+  // ---- the lane's query (column n of the score tiles) ----
+  int u[3];
+  {
+    const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+    u[2] = n & (P.ax[2].T - 1);
+    u[1] = (n >> lg2) & (P.ax[1].T - 1);
+    u[0] = n >> (lg2 + lg1);
+  }
+  bool qv = ws.any;
+  int qtok = t.b * P.Ltot;
+  int wl[3], ww[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (a < 3 - R) {
+      wl[a] = 0;
+      ww[a] = 1;
+      continue;
+    }
+    const LAx &x = P.ax[a];
+    qv = qv && u[a] < ws.nv[a];
+    const int i = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
+    qtok += (t.r[a] + x.d * i) * x.tok;
+    const int s = wstart(x, i, t.Lr[a]);
+    wl[a] = s - t.lo[a];
+    ww[a] = wend(x, i, t.Lr[a]) - s;
+  }
+  if (!qv) ww[2] = 0;
+  const int qoff = (qtok * P.H + t.head) * D;
+  if (!tile_any) return;  // uniform over the workgroup
+  v8 qf[NT];
+#pragma unroll
+  for (int st = 0; st < NT; ++st) qf[st] = ld8(q + qoff + 32 * st + 8 * gq);
+
+  // ---- the workgroup's K / V box to LDS ----
+  E *ks = reinterpret_cast<E *>(smem);
+  E *vs = ks + (P.ebox + kSlack) * RSE;
+  stage_box<T, D>(P, t, k, v, ks, vs, tid, nthr);
+  __syncthreads();
+  if (!ws.any) return;
+
+  // column tests of the lane's 4 keys per chunk (fixed when CPR1)
+  bool colok0[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    colok0[r] = (unsigned)(ws.ws[2] + 4 * gq + r - wl[2]) < (unsigned)ww[2];
+
+  f32x4 o[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) o[j] = zero4();
+  float m = -INFINITY, l = 0.f;
+  const float sl2 = P.sl2;
+  const int Em1 = P.ax[1].Em, Em2 = P.ax[2].Em;
+  // operand-read lane offsets inside a chunk: K rows (key n, 8 elements at
+  // 8 gq) and the transposing read (row 4 gq + n / 4, column 4 (n % 4))
+  const int ka_off = n * RSE + 8 * gq;
+  const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
+  const int ngroups = (ws.nchunks + NB - 1) / NB;
+  Cursor cc{ws.ws[0], ws.ws[1], 0};
+  const int key0 = (ws.ws[0] * Em1 + ws.ws[1]) * Em2 + ws.ws[2];
+
+  for (int grp = 0; grp < ngroups; ++grp) {
+    // ---- scores of the group: chunk rows, operand reads, MFMAs, masks ----
+    int kb[NB];       // first LDS row of each chunk
+    bool rok[NB];
+    int csj[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const bool real = grp * NB + j < ws.nchunks;
+      kb[j] = real ? (cc.e0 * Em1 + cc.e1) * Em2 + ws.ws[2] + 16 * cc.cs : key0;
+      csj[j] = cc.cs;
+      bool ok = real;
+      if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+      if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+      rok[j] = ok;
+      advance(cc, ws);
+    }
+    v8 ka[NB][NT];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+        ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
+    f32x4 sc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      sc[j] = zero4();
+#pragma unroll
+      for (int st = 0; st < NT; ++st) sc[j] = M::mma(ka[j][st], qf[st], sc[j]);
+    }
+    float sv[NB][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      bool cok[4];
+      if (CPR1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cok[r] = colok0[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cok[r] = (unsigned)(ws.ws[2] + 16 * csj[j] + 4 * gq + r - wl[2]) <
+                   (unsigned)ww[2];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[j][r] = (rok[j] && cok[r]) ? sc[j][r] : -INFINITY;
+        mx = fmaxf(mx, sv[j][r]);
+      }
+    }
+    // ---- online softmax ----
+    mx = quad_max(mx) * sl2;
+    // The reference point m may trail the running max by up to 8 (a factor
+    // 2^8 in P): exact after the final division by l, and it spares the O
+    // rescale on groups that do not raise any query's max by more.
+    if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+      l *= alpha;
+#pragma unroll
+      for (int j = 0; j < NDB; ++j) o[j] *= alpha;
+      m = mn;
+    }
+    const float mu = m == -INFINITY ? 0.f : m;
+    v8 bp[NB / 2];
+#pragma unroll
+    for (int jj = 0; jj < NB / 2; ++jj)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
+          l += p;
+          bp[jj][4 * h + r] = (E)p;
+        }
+    // ---- O^T += V^T . P^T, two chunks per MFMA ----
+#pragma unroll
+    for (int jj = 0; jj < NB / 2; ++jj) {
+      const E *ca = vs + kb[2 * jj] * RSE + tr_off;
+      const E *cb = vs + kb[2 * jj + 1] * RSE + tr_off;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const v4 lo4 = M::tr(ca + 16 * db);
+        const v4 hi4 = M::tr(cb + 16 * db);
+        const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[db] = M::mma(a, bp[jj], o[db]);
+      }
+    }
+  }
+
+  // ---- epilogue: sum l over the query's 4 lanes, normalise, store ----
+  l = quad_sum(l);
+  if (!qv) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    v4 wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r] = (E)(o[db][r] * inv);
+    *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = wv;
+  }
+  if (lse != nullptr && gq == 0)
+    lse[qoff / D] = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+int ilog2c(int x) {
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+constexpr size_t kLdsBudget = 80 * 1024;  // per workgroup: >= 2 per CU
+
+struct LChoice {
+  int T[3];      // wave tile (product 16 over the active axes)
+  int W, sa;     // waves per workgroup and the axis they are stacked along
+  int Em[3];     // workgroup key box (largest over tiles)
+  bool cpr1;     // every wave sub-box row is at most 16 keys wide
+  bool ok;
+};
+
+size_t box_lds_bytes(int ebox, int D) {
+  return 2 * (size_t)(ebox + kSlack) * lds_row(D) * 2;
+}
+
+// Wave tile: the power-of-two shape with the fewest (waves x chunks);
+// workgroup: up to 4 waves stacked along the axis with the smallest staged
+// box per wave whose K/V box fits the LDS budget.
+LChoice lean_choice(const Prob &P) {
+  const int R = P.rank, lead = 3 - R;
+  LChoice best{};
+  best.ok = false;
+  double best_cost = 1e300;
+  int Lr[3];
+  for (int a = 0; a < 3; ++a) Lr[a] = (P.ax[a].L + P.ax[a].d - 1) / P.ax[a].d;
+  auto box_ext = [&](int a, int t) {
+    return std::min(std::min(t, Lr[a]) + P.ax[a].K - 1, Lr[a]);
+  };
+  for (int l0 = 0; l0 <= 4; ++l0)
+    for (int l1 = 0; l0 + l1 <= 4; ++l1) {
+      const int Tt[3] = {1 << l0, 1 << l1, 1 << (4 - l0 - l1)};
+      bool ok = true;
+      for (int a = 0; a < lead; ++a)
+        if (Tt[a] != 1) ok = false;
+      if (!ok) continue;
+      double waves = 1.0, rows = 1.0;
+      for (int a = lead; a < 3; ++a) {
+        waves *= (double)P.ax[a].d * ((Lr[a] + Tt[a] - 1) / Tt[a]);
+        if (a < 2) rows *= box_ext(a, Tt[a]);
+      }
+      const double chunks = rows * std::ceil(box_ext(2, Tt[2]) / 16.0);
+      const double cost = waves * chunks;
+      if (cost < best_cost) {
+        best_cost = cost;
+        for (int a = 0; a < 3; ++a) best.T[a] = Tt[a];
+        best.cpr1 = R > 1 && box_ext(2, Tt[2]) <= 16;
+      }
+    }
+  // workgroup shape
+  double best_per_wave = 1e300;
+  for (int W = 4; W >= 1; W >>= 1)
+    for (int sa = lead; sa < 3; ++sa) {
+      if (W > 1 && best.T[sa] >= Lr[sa]) continue;
+      int Em[3], ebox = 1;
+      for (int a = 0; a < 3; ++a) {
+        const int tw = best.T[a] * (a == sa ? W : 1);
+        Em[a] = a < lead ? 1 : box_ext(a, tw);
+        ebox *= Em[a];
+      }
+      if (box_lds_bytes(ebox, P.D) > kLdsBudget) continue;
+      const double per_wave = (double)ebox / W;
+      if (per_wave < best_per_wave * 0.999) {
+        best_per_wave = per_wave;
+        best.W = W;
+        best.sa = sa;
+        for (int a = 0; a < 3; ++a) best.Em[a] = Em[a];
+        best.ok = true;
+      }
+    }
+  return best;
+}
+
+LProb make_lprob(const Prob &P, const LChoice &C) {
+  LProb L{};
+  L.B = P.B;
+  L.H = P.H;
+  L.Hkv = P.Hkv;
+  L.D = P.D;
+  L.Ltot = P.ax[0].L * P.ax[1].L * P.ax[2].L;
+  L.sl2 = P.scale * kLog2e;
+  L.sa = C.sa;
+  int tok = 1;
+  int grid = 1;
+  for (int a = 2; a >= 0; --a) {
+    const Axis &x = P.ax[a];
+    LAx &y = L.ax[a];
+    y.L = x.L;
+    y.K = x.K;
+    y.d = x.d;
+    y.causal = x.causal;
+    y.nh = x.K / 2;
+    y.Lq = x.L / x.d;
+    y.Lrem = x.L % x.d;
+    y.T = C.T[a];
+    y.lgT = ilog2c(C.T[a]);
+    y.TW = C.T[a] * (a == C.sa ? C.W : 1);
+    y.lgTW = ilog2c(y.TW);
+    y.Em = C.Em[a];
+    const int Lr = (x.L + x.d - 1) / x.d;
+    y.nt = (Lr + y.TW - 1) / y.TW;
+    y.tok = tok;
+    tok *= x.L;
+    y.fG = make_fastdiv((uint32_t)(x.d * y.nt));
+    y.fnt = make_fastdiv((uint32_t)y.nt);
+    grid *= x.d * y.nt;
+  }
+  L.ebox = C.Em[0] * C.Em[1] * C.Em[2];
+  L.n_tiles = P.B * P.H * grid;
+  L.n_launch = (L.n_tiles + 7) & ~7;
+  L.fH = make_fastdiv((uint32_t)P.H);
+  L.fRep = make_fastdiv((uint32_t)P.rep);
+  L.fE2 = make_fastdiv((uint32_t)C.Em[2]);
+  L.fE1 = make_fastdiv((uint32_t)C.Em[1]);
+  return L;
+}
+
+bool lean_disabled() {
+  static const bool off = [] {
+    const char *e = std::getenv("NATTEN_AMD_NO_LEAN");
+    return e != nullptr && e[0] != '\0' && e[0] != '0';
+  }();
+  return off;
+}
+
+}  // namespace
+
+bool lean_eligible(const Prob &P, int dtype) {
+  if (lean_disabled()) return false;
+  if (dtype != NA_BF16 && dtype != NA_F16) return false;
+  if (P.D != 32 && P.D != 64 && P.D != 128) return false;
+  if (P.dense || P.n_extra > 0 || P.sample_extent != nullptr) return false;
+  if (!(P.scale > 0.f) || !std::isfinite(P.scale)) return false;
+  for (int a = 0; a < 3; ++a) {
+    const Axis &x = P.ax[a];
+    if (x.s != 1) return false;
+    if (!x.causal && ((x.K % 2) == 0 || (int64_t)x.d * x.K > x.L)) return false;
+  }
+  // 32-bit element offsets
+  const int64_t elems = (int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L *
+                        std::max(P.H, P.Hkv) * P.D;
+  if (elems >= (int64_t(1) << 31)) return false;
+  return lean_choice(P).ok;
+}
+
+#define LEAN_D(D_, BODY) \
+  do {                   \
+    if ((D_) == 32) {    \
+      BODY(32);          \
+    } else if ((D_) == 64) { \
+      BODY(64);          \
+    } else {             \
+      BODY(128);         \
+    }                    \
+  } while (0)
+
+void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, void *out, float *lse, hipStream_t st) {
+  const LChoice C = lean_choice(P);
+  const LProb L = make_lprob(P, C);
+  if (L.n_tiles == 0) return;
+  const size_t lds = box_lds_bytes(L.ebox, P.D);
+  const dim3 grid(L.n_launch), block(64 * C.W);
+#define LF_LAUNCH(TT, DD, RR, CC)                                              \
+  hipLaunchKernelGGL((k_wfwd<TT, DD, RR, CC>), grid, block, lds, st, L,        \
+                     (const TT *)q, (const TT *)k, (const TT *)v, (TT *)out, lse)
+#define LF_R(TT, DD)                                                          \
+  do {                                                                        \
+    if (P.rank == 1) LF_LAUNCH(TT, DD, 1, false);                             \
+    else if (P.rank == 2) {                                                   \
+      if (C.cpr1) LF_LAUNCH(TT, DD, 2, true); else LF_LAUNCH(TT, DD, 2, false); \
+    } else {                                                                  \
+      if (C.cpr1) LF_LAUNCH(TT, DD, 3, true); else LF_LAUNCH(TT, DD, 3, false); \
+    }                                                                         \
+  } while (0)
+#define LF_D(DD)                          \
+  do {                                    \
+    if (dtype == NA_BF16) LF_R(bf16_t, DD); \
+    else LF_R(f16_t, DD);                 \
+  } while (0)
+  LEAN_D(P.D, LF_D);
+#undef LF_D
+#undef LF_R
+#undef LF_LAUNCH
+}
+
+}  // namespace na
