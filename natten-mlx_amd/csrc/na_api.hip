@@ -320,7 +320,9 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                 delta_bytes(P), workspace == nullptr ? (size_t)0 : workspace_bytes);
   float *delta = static_cast<float *>(workspace);
   const hipStream_t st = as_stream(stream);
-  if (use_mfma(p, P)) {
+  if ((p->flags & NA_FLAG_GENERIC) == 0 && na::lean_bwd_eligible(P, p->dtype)) {
+    na::lean_bwd(P, p->dtype, q, k, v, out, lse, dout, dlse, dq, dk, dv, st);
+  } else if (use_mfma(p, P)) {
     const bool dextra =
         P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
     if (dextra || na::mfma_bwd_reads_delta(P))

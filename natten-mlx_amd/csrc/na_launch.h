@@ -75,6 +75,13 @@ void mfma_selftest(int dtype, float *out, hipStream_t st);
 bool lean_eligible(const Prob &P, int dtype);
 void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, void *out, float *lse, hipStream_t st);
+// Lean fused backward: one launch, no workspace (delta is computed in the
+// kernel); dlse may be null.
+bool lean_bwd_eligible(const Prob &P, int dtype);
+void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *out, const float *lse,
+              const void *dout, const float *dlse, void *dq, void *dk,
+              void *dv, hipStream_t st);
 
 // Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with
 // d*K <= L on every non-causal axis and at most 512 kernel slots.

@@ -93,9 +93,14 @@ struct LProb {
   float sl2;          // scale * log2(e)
   int32_t n_tiles, n_launch;
   int32_t sa;         // stack axis: the workgroup's waves tile this axis
-  int32_t ebox;       // Em0 * Em1 * Em2
+  int32_t ebox;       // staged rows: Em2 (rank 1) or Em0 * Em1 * 2^lgP2
+  int32_t lgP2;       // rank >= 2: staged box rows are 2^lgP2 >= Em2 wide
+  int32_t rep;        // query heads per key/value head
+  float scale;
   FastDiv fH, fRep;
-  FastDiv fE2, fE1;   // box decode: key index -> (e0, e1, e2)
+  FastDiv fHkv;       // key/value heads
+  FastDiv fGrid;      // spatial tiles per (batch, head): prod of d * nt
+  FastDiv fE1;        // rank 3: box row -> (e0, e1)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -121,10 +126,28 @@ __device__ __forceinline__ int wend(const LAx &x, int i, int Lr) {
   return ((i + 1) & sel) | (nc & ~sel);
 }
 
-// LDS row stride (elements) of staged rows: 16 bytes of skew keep the
-// 16-byte stores, the 16-byte operand reads and the transposing reads at
-// the minimum number of bank passes.
-constexpr int lds_row(int D) { return D + 8; }
+// Queries [start, end) whose windows hold sub-grid key j: on a non-causal
+// axis the clamped windows give [j <= K-1 ? 0 : j - K/2, j >= Lr-K ? Lr :
+// j + K/2 + 1); on a causal axis [j, min(j + K, Lr)).  Both bounds are
+// non-decreasing in j.
+__device__ __forceinline__ int iwstart(const LAx &x, int j, int Lr) {
+  const int nc = j <= x.K - 1 ? 0 : j - x.nh;
+  const int sel = -x.causal;
+  return (j & sel) | (nc & ~sel);
+}
+__device__ __forceinline__ int iwend(const LAx &x, int j, int Lr) {
+  const int nc = j >= Lr - x.K ? Lr : j + x.nh + 1;
+  const int ca = min(j + x.K, Lr);
+  const int sel = -x.causal;
+  return (ca & sel) | (nc & ~sel);
+}
+
+// Staged rows interleave two tensors: [x row | 8 | y row | 8] elements, so
+// both are addressed from one lane base with constant offsets.  The 16
+// bytes after each row spread the rows over the LDS banks; in a query box
+// the pair after the Q row holds (lse * log2(e), -delta) of the row.
+constexpr int lds_row(int D) { return 2 * (D + 8); }
+constexpr int lds_y(int D) { return D + 8; }
 // Key rows of slack after a staged box: a chunk read near the box end may
 // run up to 15 rows past it.
 constexpr int kSlack = 16;
@@ -139,30 +162,28 @@ struct LTile {
   int SK[3];          // element stride of one box step per axis (K/V)
 };
 
+// Origin of spatial tile `sp` (row-major over the per-axis grids d * nt):
+// phase, first sub-grid index and valid count per axis.
 template <int R>
-__device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
+__device__ __forceinline__ bool tile_origin(const LProb &P, uint32_t sp,
                                             LTile &t) {
-  // tiles at or beyond n_tiles decode to a batch index >= B
-  uint32_t rest = (uint32_t)tile;
   int g[3] = {0, 0, 0};
 #pragma unroll
   for (int a = 2; a >= 3 - R; --a) {
-    const uint32_t qd = fdiv(rest, P.ax[a].fG);
-    g[a] = (int)(rest - qd * P.ax[a].fG.d);
-    rest = qd;
+    if (a == 3 - R) {
+      g[a] = (int)sp;
+    } else {
+      const uint32_t qd = fdiv(sp, P.ax[a].fG);
+      g[a] = (int)(sp - qd * P.ax[a].fG.d);
+      sp = qd;
+    }
   }
-  const uint32_t bq = fdiv(rest, P.fH);
-  t.head = (int)(rest - bq * P.fH.d);
-  t.b = (int)bq;
-  t.hk = (int)fdiv((uint32_t)t.head, P.fRep);
-  int tok0 = t.b * P.Ltot;
-  bool any = t.b < P.B;
+  bool any = true;
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     const LAx &x = P.ax[a];
     if (a < 3 - R) {
-      t.r[a] = 0; t.i0[a] = 0; t.nv[a] = 1; t.Lr[a] = 1; t.lo[a] = 0; t.E[a] = 1;
-      t.SK[a] = 0;
+      t.r[a] = 0; t.i0[a] = 0; t.nv[a] = 1; t.Lr[a] = 1;
       continue;
     }
     const int rr = (int)fdiv((uint32_t)g[a], x.fnt);
@@ -171,14 +192,46 @@ __device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
     t.Lr[a] = x.Lq + (rr < x.Lrem ? 1 : 0);
     t.nv[a] = min(t.Lr[a] - t.i0[a], x.TW);
     any = any & (t.nv[a] > 0);
-    const int nvc = max(t.nv[a], 1);
-    t.lo[a] = wstart(x, t.i0[a], t.Lr[a]);
-    t.E[a] = wend(x, t.i0[a] + nvc - 1, t.Lr[a]) - t.lo[a];
-    tok0 += (rr + x.d * t.lo[a]) * x.tok;
-    t.SK[a] = x.d * x.tok * P.Hkv * P.D;
   }
-  t.kbase = (tok0 * P.Hkv + t.hk) * P.D;
   return any;
+}
+
+// The tile's box (INV: the queries whose windows hold its keys; else the
+// keys its queries' windows hold) and its addressing for rows of head
+// `head` in a tensor of `heads` heads.
+template <int R, bool INV>
+__device__ __forceinline__ void tile_box(const LProb &P, LTile &t, int head,
+                                         int heads) {
+  int tok0 = t.b * P.Ltot;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const LAx &x = P.ax[a];
+    if (a < 3 - R) {
+      t.lo[a] = 0; t.E[a] = 1; t.SK[a] = 0;
+      continue;
+    }
+    const int i1 = t.i0[a] + max(t.nv[a], 1) - 1;
+    t.lo[a] = INV ? iwstart(x, t.i0[a], t.Lr[a]) : wstart(x, t.i0[a], t.Lr[a]);
+    t.E[a] = (INV ? iwend(x, i1, t.Lr[a]) : wend(x, i1, t.Lr[a])) - t.lo[a];
+    tok0 += (t.r[a] + x.d * t.lo[a]) * x.tok;
+    t.SK[a] = x.d * x.tok * heads * P.D;
+  }
+  t.kbase = (tok0 * heads + head) * P.D;
+}
+
+template <int R>
+__device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
+                                            LTile &t) {
+  // tiles at or beyond n_tiles decode to a batch index >= B
+  const uint32_t rest = fdiv((uint32_t)tile, P.fGrid);
+  const uint32_t sp = (uint32_t)tile - rest * P.fGrid.d;
+  const uint32_t bq = fdiv(rest, P.fH);
+  t.head = (int)(rest - bq * P.fH.d);
+  t.b = (int)bq;
+  t.hk = (int)fdiv((uint32_t)t.head, P.fRep);
+  const bool any = tile_origin<R>(P, sp, t);
+  tile_box<R, false>(P, t, t.hk, P.Hkv);
+  return any & (t.b < P.B);
 }
 
 // A wave's part of a workgroup tile: its 16 queries (wave tile w along the
@@ -191,7 +244,7 @@ struct WSub {
   bool any;
 };
 
-template <int R>
+template <int R, bool INV = false>
 __device__ __forceinline__ WSub wave_sub(const LProb &P, const LTile &t,
                                          int w) {
   WSub s;
@@ -209,8 +262,10 @@ __device__ __forceinline__ WSub wave_sub(const LProb &P, const LTile &t,
     s.nv[a] = min(t.nv[a] - off, x.T);
     s.any = s.any & (s.nv[a] > 0);
     const int nvc = max(s.nv[a], 1);
-    s.ws[a] = wstart(x, s.i0[a], t.Lr[a]) - t.lo[a];
-    s.we[a] = wend(x, s.i0[a] + nvc - 1, t.Lr[a]) - t.lo[a];
+    s.ws[a] = (INV ? iwstart(x, s.i0[a], t.Lr[a]) : wstart(x, s.i0[a], t.Lr[a])) -
+              t.lo[a];
+    s.we[a] = (INV ? iwend(x, s.i0[a] + nvc - 1, t.Lr[a])
+                   : wend(x, s.i0[a] + nvc - 1, t.Lr[a])) - t.lo[a];
     if (a < 2) rows *= s.we[a] - s.ws[a];
   }
   s.cpr = (s.we[2] - s.ws[2] + 15) >> 4;
@@ -234,9 +289,40 @@ __device__ __forceinline__ void advance(Cursor &cu, const WSub &s) {
   cu.e0 += w2 ? 1 : 0;
 }
 
+// 16-byte load at a 32-bit element offset from a wave-uniform base (the
+// offset stays a 32-bit register operand, no 64-bit address arithmetic).
 template <typename T>
-__device__ __forceinline__ typename L16<T>::v8 ld8(const T *p) {
-  return *reinterpret_cast<const typename L16<T>::v8 *>(p);
+__device__ __forceinline__ typename L16<T>::v8 ld8(const T *base, int off) {
+  return *reinterpret_cast<const typename L16<T>::v8 *>(
+      reinterpret_cast<const char *>(base) + (size_t)((uint32_t)off * 2u));
+}
+__device__ __forceinline__ float ldf(const float *base, int off) {
+  return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) +
+                                          (size_t)((uint32_t)off * 4u));
+}
+
+// Element offset of staged-box unit (row kk of the LDS layout, 16-byte unit
+// o): box coordinates from the layout (shifts; rank 3 divides by Em1),
+// clamped onto the tile's true box, then 24-bit products with the strides.
+template <int R>
+__device__ __forceinline__ int unit_offset(const LProb &P, const LTile &t,
+                                           int kk, int o) {
+  int e0 = 0, e1 = 0, e2 = kk;
+  if (R >= 2) {
+    const int row = kk >> P.lgP2;
+    e2 = kk & ((1 << P.lgP2) - 1);
+    if (R == 2) {
+      e1 = row;
+    } else {
+      e0 = (int)fdiv((uint32_t)row, P.fE1);
+      e1 = row - e0 * P.ax[1].Em;
+    }
+  }
+  int off = t.kbase + 8 * o;
+  if (R == 3) off += __umul24((unsigned)min(e0, t.E[0] - 1), (unsigned)t.SK[0]);
+  if (R >= 2) off += __umul24((unsigned)min(e1, t.E[1] - 1), (unsigned)t.SK[1]);
+  off += __umul24((unsigned)min(e2, t.E[2] - 1), (unsigned)t.SK[2]);
+  return off;
 }
 
 __device__ __forceinline__ f32x4 zero4() {
@@ -263,6 +349,22 @@ __device__ __forceinline__ float quad_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Window mask carried by the score accumulator: the MFMA starts from 0 for
+// the lane's 4 elements inside the window and from -inf outside, so S comes
+// out masked (-inf plus a finite product is -inf).  cb: the column part
+// (0 / -inf per element), rowok: the chunk row is inside the window.
+__device__ __forceinline__ void col_bias(int x0, int ww2, float cb[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    cb[r] = (unsigned)(x0 + r) < (unsigned)ww2 ? 0.f : -INFINITY;
+}
+__device__ __forceinline__ f32x4 mask_init(bool rowok, const float cb[4]) {
+  f32x4 c;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) c[r] = rowok ? cb[r] : -INFINITY;
+  return c;
+}
+
 // In-wave LDS ordering: this wave's LDS operations are complete.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -270,12 +372,29 @@ __device__ __forceinline__ void wave_lds_sync() {
   asm volatile("" ::: "memory");
 }
 
-// Stage a workgroup's box of rows of two tensors (x, y: K and V, or Q and
-// dO) into LDS: row kk = (e0 * Em1 + e1) * Em2 + e2 of the box layout at
-// element kk * lds_row(D), points past the tile's true box clamped onto it
-// (their rows are real rows, so every staged value is finite).  Loads go
-// four 16-byte units per lane at a time, all in flight together.
+// Slack rows after a staged box: zero (a chunk read near the end of the box
+// may include them; zero rows keep every MFMA operand finite).
 template <typename T, int D>
+__device__ __forceinline__ void zero_slack(const LProb &P,
+                                           typename L16<T>::e *xs, int tid,
+                                           int nthr) {
+  typedef typename L16<T>::v8 v8;
+  constexpr int SLU = kSlack * lds_row(D) / 8;  // 16-byte units of slack
+  for (int u = tid; u < SLU; u += nthr) {
+    v8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (typename L16<T>::e)0.f;
+    *reinterpret_cast<v8 *>(xs + P.ebox * lds_row(D) + 8 * u) = z;
+  }
+}
+
+// Stage a workgroup's box of rows of two tensors (x, y: K and V, or Q and
+// dO) into LDS: box point (e0, e1, e2) at layout row ((e0 * Em1 + e1) <<
+// lgP2) + e2 (rank 1: e2), element row * lds_row(D); layout points past the
+// tile's true box are clamped onto it (their rows are real rows, so every
+// staged value is finite).  Four 16-byte units per lane at a time, all in
+// flight together.
+template <typename T, int D, int R>
 __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
                                           const T *__restrict__ x,
                                           const T *__restrict__ y,
@@ -293,15 +412,9 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
     for (int j = 0; j < 4; ++j) {
       const int u = min(u0 + j * nthr + tid, nun - 1);
       const int kk = u / OCT, o = u % OCT;
-      const uint32_t t1 = fdiv((uint32_t)kk, P.fE2);
-      const int e2 = kk - (int)t1 * P.ax[2].Em;
-      const uint32_t e0 = fdiv(t1, P.fE1);
-      const int e1 = (int)t1 - (int)e0 * P.ax[1].Em;
-      const int g = t.kbase + min((int)e0, t.E[0] - 1) * t.SK[0] +
-                    min(e1, t.E[1] - 1) * t.SK[1] + min(e2, t.E[2] - 1) * t.SK[2] +
-                    8 * o;
-      xr[j] = ld8(x + g);
-      yr[j] = ld8(y + g);
+      const int g = unit_offset<R>(P, t, kk, o);
+      xr[j] = ld8(x, g);
+      yr[j] = ld8(y, g);
       la[j] = kk * RSE + 8 * o;
     }
 #pragma unroll
@@ -310,16 +423,7 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
       *reinterpret_cast<v8 *>(ys + la[j]) = yr[j];
     }
   }
-  // slack rows after the box: zero (a chunk read near the end of the box
-  // may include them; zero rows keep every MFMA operand finite)
-  constexpr int SLU = kSlack * RSE / 8;  // 16-byte units of slack
-  for (int u = tid; u < SLU; u += nthr) {
-    v8 z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (typename L16<T>::e)0.f;
-    *reinterpret_cast<v8 *>(xs + P.ebox * RSE + 8 * u) = z;
-    *reinterpret_cast<v8 *>(ys + P.ebox * RSE + 8 * u) = z;
-  }
+  zero_slack<T, D>(P, xs, tid, nthr);
 }
 
 // ---------------------------------------------------------------------------
@@ -383,34 +487,32 @@ __global__ void __launch_bounds__(256)
   if (!tile_any) return;  // uniform over the workgroup
   v8 qf[NT];
 #pragma unroll
-  for (int st = 0; st < NT; ++st) qf[st] = ld8(q + qoff + 32 * st + 8 * gq);
+  for (int st = 0; st < NT; ++st) qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
 
   // ---- the workgroup's K / V box to LDS ----
   E *ks = reinterpret_cast<E *>(smem);
-  E *vs = ks + (P.ebox + kSlack) * RSE;
-  stage_box<T, D>(P, t, k, v, ks, vs, tid, nthr);
+  E *vs = ks + lds_y(D);
+  stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr);
   __syncthreads();
   if (!ws.any) return;
 
-  // column tests of the lane's 4 keys per chunk (fixed when CPR1)
-  bool colok0[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    colok0[r] = (unsigned)(ws.ws[2] + 4 * gq + r - wl[2]) < (unsigned)ww[2];
+  // column part of the mask of the lane's 4 keys per chunk (fixed when CPR1)
+  float cb0[4];
+  col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
 
   f32x4 o[NDB];
 #pragma unroll
   for (int j = 0; j < NDB; ++j) o[j] = zero4();
   float m = -INFINITY, l = 0.f;
   const float sl2 = P.sl2;
-  const int Em1 = P.ax[1].Em, Em2 = P.ax[2].Em;
+  const int Em1 = P.ax[1].Em;
   // operand-read lane offsets inside a chunk: K rows (key n, 8 elements at
   // 8 gq) and the transposing read (row 4 gq + n / 4, column 4 (n % 4))
   const int ka_off = n * RSE + 8 * gq;
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
   const int ngroups = (ws.nchunks + NB - 1) / NB;
   Cursor cc{ws.ws[0], ws.ws[1], 0};
-  const int key0 = (ws.ws[0] * Em1 + ws.ws[1]) * Em2 + ws.ws[2];
+  const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
 
   for (int grp = 0; grp < ngroups; ++grp) {
     // ---- scores of the group: chunk rows, operand reads, MFMAs, masks ----
@@ -420,7 +522,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const bool real = grp * NB + j < ws.nchunks;
-      kb[j] = real ? (cc.e0 * Em1 + cc.e1) * Em2 + ws.ws[2] + 16 * cc.cs : key0;
+      kb[j] = real ? ((cc.e0 * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs : key0;
       csj[j] = cc.cs;
       bool ok = real;
       if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
@@ -434,33 +536,25 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int st = 0; st < NT; ++st)
         ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
-    f32x4 sc[NB];
+    f32x4 sv[NB];  // masked raw scores
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      sc[j] = zero4();
-#pragma unroll
-      for (int st = 0; st < NT; ++st) sc[j] = M::mma(ka[j][st], qf[st], sc[j]);
-    }
-    float sv[NB][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      bool cok[4];
+      float cb[4];
       if (CPR1) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cok[r] = colok0[r];
+        for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
       } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          cok[r] = (unsigned)(ws.ws[2] + 16 * csj[j] + 4 * gq + r - wl[2]) <
-                   (unsigned)ww[2];
+        col_bias(ws.ws[2] + 16 * csj[j] + 4 * gq - wl[2], ww[2], cb);
       }
+      sv[j] = mask_init(rok[j], cb);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sv[j][r] = (rok[j] && cok[r]) ? sc[j][r] : -INFINITY;
-        mx = fmaxf(mx, sv[j][r]);
-      }
+      for (int st = 0; st < NT; ++st) sv[j] = M::mma(ka[j][st], qf[st], sv[j]);
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][r]);
     // ---- online softmax ----
     mx = quad_max(mx) * sl2;
     // The reference point m may trail the running max by up to 8 (a factor
@@ -517,6 +611,386 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
+// Backward.
+
+// Stage the dK/dV role's query box: Q and dO rows to LDS (layout as
+// stage_box) and per row the pair (lse * log2(e), rowsum(dO * O) - dlse),
+// the row sum reduced over the D/8 consecutive lanes holding one row.
+template <typename T, int D, int R>
+__device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
+                                           const T *__restrict__ q,
+                                           const T *__restrict__ dout,
+                                           const T *__restrict__ out,
+                                           const float *__restrict__ lse,
+                                           const float *__restrict__ dlse,
+                                           typename L16<T>::e *qs,
+                                           typename L16<T>::e *os, int tid,
+                                           int nthr) {
+  typedef typename L16<T>::v8 v8;
+  constexpr int OCT = D / 8;
+  constexpr int RSE = lds_row(D);
+  const int nun = P.ebox * OCT;
+  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
+    v8 qr[4], dr[4], orr[4];
+    float lr[4], dl[4];
+    int kk[4], o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = min(u0 + j * nthr + tid, nun - 1);
+      kk[j] = u / OCT;
+      o[j] = u % OCT;
+      const int g = unit_offset<R>(P, t, kk[j], o[j]);
+      const int row = (g - 8 * o[j]) / D;
+      qr[j] = ld8(q, g);
+      dr[j] = ld8(dout, g);
+      orr[j] = ld8(out, g);
+      lr[j] = ldf(lse, row);
+      dl[j] = dlse != nullptr ? ldf(dlse, row) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<v8 *>(qs + kk[j] * RSE + 8 * o[j]) = qr[j];
+      *reinterpret_cast<v8 *>(os + kk[j] * RSE + 8 * o[j]) = dr[j];
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        typename L16<T>::v2 a2, b2;
+        a2[0] = dr[j][e];
+        a2[1] = dr[j][e + 1];
+        b2[0] = orr[j][e];
+        b2[1] = orr[j][e + 1];
+        part = L16<T>::dot2(a2, b2, part);
+      }
+#pragma unroll
+      for (int m = 1; m < OCT; m <<= 1) part += __shfl_xor(part, m);
+      if (o[j] == 0)
+        *reinterpret_cast<float2 *>(qs + kk[j] * RSE + D) =
+            make_float2(lr[j] * kLog2e, dl[j] - part);
+    }
+  }
+  zero_slack<T, D>(P, qs, tid, nthr);
+}
+
+// Lane-window of a wave's 16 rows (queries in the dQ role, keys in the
+// dK/dV role) inside the staged box: [wl, wl + ww) per axis, ww = 0 on
+// every axis for rows outside the tensor.  Returns the row's element offset.
+template <int R, bool INV>
+__device__ __forceinline__ int lane_rows(const LProb &P, const LTile &t,
+                                         const WSub &ws, int n, int head,
+                                         int heads, bool &valid, int wl[3],
+                                         int ww[3]) {
+  int u[3];
+  const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+  u[2] = n & (P.ax[2].T - 1);
+  u[1] = (n >> lg2) & (P.ax[1].T - 1);
+  u[0] = n >> (lg2 + lg1);
+  valid = ws.any;
+  int tok = t.b * P.Ltot;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (a < 3 - R) {
+      wl[a] = 0;
+      ww[a] = 1;
+      continue;
+    }
+    const LAx &x = P.ax[a];
+    valid = valid && u[a] < ws.nv[a];
+    const int i = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
+    tok += (t.r[a] + x.d * i) * x.tok;
+    const int s0 = INV ? iwstart(x, i, t.Lr[a]) : wstart(x, i, t.Lr[a]);
+    const int s1 = INV ? iwend(x, i, t.Lr[a]) : wend(x, i, t.Lr[a]);
+    wl[a] = s0 - t.lo[a];
+    ww[a] = s1 - s0;
+  }
+  if (!valid) ww[2] = 0;
+  return (tok * heads + head) * P.D;
+}
+
+// Rows of chunk pair (a, b) of a wave's sub-box: first LDS row, row test
+// and column segment of each (padding chunks: row 0 of the sub-box, masked).
+template <int R>
+__device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
+                                          int Em1, int lgP2, int key0,
+                                          const int wl[3], const int ww[3],
+                                          int kb[2], bool rok[2], int cs[2]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const bool real = c0 + h < ws.nchunks;
+    kb[h] = real ? ((cc.e0 * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
+    cs[h] = cc.cs;
+    bool ok = real;
+    if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+    if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+    rok[h] = ok;
+    advance(cc, ws);
+  }
+}
+
+// A workgroup owns one spatial tile of one key/value head and runs both
+// halves of the backward for it in sequence, in the same LDS: the K/V box
+// of the tile's queries is staged and each wave computes dQ of its 16
+// queries (per query head of the group); then, per query head, the query
+// box of the tile's keys (Q, dO, lse, delta) is staged and each wave
+// accumulates dK and dV of its 16 keys.  One workgroup per tile keeps the
+// whole launch resident at once.
+template <typename T, int D, int R, bool CPR1>
+__global__ void __launch_bounds__(256)
+    k_wbwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
+           const T *__restrict__ v, const T *__restrict__ out,
+           const float *__restrict__ lse, const T *__restrict__ dout,
+           const float *__restrict__ dlse, T *__restrict__ dq,
+           T *__restrict__ dk, T *__restrict__ dv) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;
+  constexpr int NDB = D / 16;
+  constexpr int RSE = lds_row(D);
+  extern __shared__ __align__(16) char smem[];
+
+  const uint32_t tile = (uint32_t)xcd_tile(blockIdx.x, P.n_launch);
+  const uint32_t rest = fdiv(tile, P.fGrid);
+  const uint32_t sp = tile - rest * P.fGrid.d;
+  const uint32_t bq = fdiv(rest, P.fHkv);
+  LTile t;
+  t.hk = (int)(rest - bq * P.fHkv.d);
+  t.b = (int)bq;
+  const bool tile_any = tile_origin<R>(P, sp, t) & (t.b < P.B);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  const float sl2 = P.sl2;
+  const int Em1 = P.ax[1].Em;
+  const int ka_off = n * RSE + 8 * gq;
+  const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
+  if (!tile_any) return;  // uniform over the workgroup
+  E *xs = reinterpret_cast<E *>(smem);
+  E *ys = xs + lds_y(D);
+
+  // =============================== dQ ===============================
+  {
+    tile_box<R, false>(P, t, t.hk, P.Hkv);
+    const WSub ws = wave_sub<R, false>(P, t, w);
+    stage_box<T, D, R>(P, t, k, v, xs, ys, tid, nthr);
+    const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    for (int hr = 0; hr < P.rep; ++hr) {
+      const int hq = t.hk * P.rep + hr;
+      bool qv;
+      int wl[3], ww[3];
+      const int qoff = lane_rows<R, false>(P, t, ws, n, hq, P.H, qv, wl, ww);
+      v8 qf[NT], df[NT];
+      float dsum = 0.f;
+#pragma unroll
+      for (int st = 0; st < NT; ++st) {
+        qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
+        df[st] = ld8(dout, qoff + 32 * st + 8 * gq);
+        const v8 of = ld8(out, qoff + 32 * st + 8 * gq);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum = fmaf((float)df[st][e], (float)of[e], dsum);
+      }
+      const float lse2 = ldf(lse, qoff / D) * kLog2e;
+      const float dl = dlse != nullptr ? ldf(dlse, qoff / D) : 0.f;
+      if (hr == 0) __syncthreads();  // the K / V box is staged
+      if (!ws.any) continue;
+      const float delta = quad_sum(dsum) - dl;
+      float cb0[4];
+      col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
+      f32x4 acc[NDB];
+#pragma unroll
+      for (int j = 0; j < NDB; ++j) acc[j] = zero4();
+      Cursor cc{ws.ws[0], ws.ws[1], 0};
+      for (int c0 = 0; c0 < ws.nchunks; c0 += 2) {
+        int kb[2], cs[2];
+        bool rok[2];
+        pair_rows<R>(ws, cc, c0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        v8 kr[2][NT], vr[2][NT];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int st = 0; st < NT; ++st) {
+            kr[h][st] = *reinterpret_cast<const v8 *>(xs + kb[h] * RSE + ka_off + 32 * st);
+            vr[h][st] = *reinterpret_cast<const v8 *>(ys + kb[h] * RSE + ka_off + 32 * st);
+          }
+        // S^T masked through its initial value, dP^T - delta through its
+        f32x4 sc[2], dp[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float cb[4];
+          if (CPR1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
+          } else {
+            col_bias(ws.ws[2] + 16 * cs[h] + 4 * gq - wl[2], ww[2], cb);
+          }
+          sc[h] = mask_init(rok[h], cb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dp[h][r] = -delta;
+#pragma unroll
+          for (int st = 0; st < NT; ++st) {
+            sc[h] = M::mma(kr[h][st], qf[st], sc[h]);
+            dp[h] = M::mma(vr[h][st], df[st], dp[h]);
+          }
+        }
+        v8 bs;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sc[h][r], sl2, -lse2));
+            bs[4 * h + r] = (E)(p * dp[h][r]);
+          }
+        // dQ^T += K^T . dS^T (K^T through the transposing read)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const v4 lo4 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
+          const v4 hi4 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+          const v8 a8 = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[db] = M::mma(a8, bs, acc[db]);
+        }
+      }
+      if (qv) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          v4 wv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) wv[r] = (E)(acc[db][r] * P.scale);
+          *reinterpret_cast<v4 *>(dq + qoff + 16 * db + 4 * gq) = wv;
+        }
+      }
+    }
+  }
+
+  // ============================= dK / dV =============================
+  // keys of the tile (head hk); the query box of each query head of the group
+  tile_box<R, true>(P, t, t.hk * P.rep, P.H);
+  const WSub ws = wave_sub<R, true>(P, t, w);
+  bool kv;
+  int wl[3], ww[3];
+  int koff;
+  {
+    int u[3];
+    const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+    u[2] = n & (P.ax[2].T - 1);
+    u[1] = (n >> lg2) & (P.ax[1].T - 1);
+    u[0] = n >> (lg2 + lg1);
+    kv = ws.any;
+    int tok = t.b * P.Ltot;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      if (a < 3 - R) {
+        wl[a] = 0;
+        ww[a] = 1;
+        continue;
+      }
+      const LAx &x = P.ax[a];
+      kv = kv && u[a] < ws.nv[a];
+      const int j = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
+      tok += (t.r[a] + x.d * j) * x.tok;
+      const int s0 = iwstart(x, j, t.Lr[a]);
+      wl[a] = s0 - t.lo[a];
+      ww[a] = iwend(x, j, t.Lr[a]) - s0;
+    }
+    if (!kv) ww[2] = 0;
+    koff = (tok * P.Hkv + t.hk) * D;
+  }
+  v8 kf[NT], vf[NT];
+#pragma unroll
+  for (int st = 0; st < NT; ++st) {
+    kf[st] = ld8(k, koff + 32 * st + 8 * gq);
+    vf[st] = ld8(v, koff + 32 * st + 8 * gq);
+  }
+  float cb0[4];
+  col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
+  f32x4 adk[NDB], adv[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) {
+    adk[j] = zero4();
+    adv[j] = zero4();
+  }
+  const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+  const int qbase0 = t.kbase;  // query box rows of head hk * rep
+  for (int hr = 0; hr < P.rep; ++hr) {
+    t.kbase = qbase0 + hr * D;  // query head hk * rep + hr
+    __syncthreads();  // the LDS reads of the previous box are done
+    stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr);
+    __syncthreads();
+    if (!ws.any) continue;
+    Cursor cc{ws.ws[0], ws.ws[1], 0};
+    for (int c0 = 0; c0 < ws.nchunks; c0 += 2) {
+      int kb[2], cs[2];
+      bool rok[2];
+      pair_rows<R>(ws, cc, c0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+      v8 qr[2][NT], orr[2][NT];
+      float ls2[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int st = 0; st < NT; ++st) {
+          qr[h][st] = *reinterpret_cast<const v8 *>(xs + kb[h] * RSE + ka_off + 32 * st);
+          orr[h][st] = *reinterpret_cast<const v8 *>(ys + kb[h] * RSE + ka_off + 32 * st);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ls2[h][r] = *reinterpret_cast<const float *>(xs + (kb[h] + 4 * gq + r) * RSE + D);
+      }
+      // S masked through its initial value, dP - delta through its
+      f32x4 sc[2], dp[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float cb[4];
+        if (CPR1) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
+        } else {
+          col_bias(ws.ws[2] + 16 * cs[h] + 4 * gq - wl[2], ww[2], cb);
+        }
+        sc[h] = mask_init(rok[h], cb);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)  // -delta of the row, read into the accumulator
+          dp[h][r] = *reinterpret_cast<const float *>(xs + (kb[h] + 4 * gq + r) * RSE + D + 2);
+#pragma unroll
+        for (int st = 0; st < NT; ++st) {
+          sc[h] = M::mma(qr[h][st], kf[st], sc[h]);
+          dp[h] = M::mma(orr[h][st], vf[st], dp[h]);
+        }
+      }
+      v8 bp, bs;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(sc[h][r], sl2, -ls2[h][r]));
+          bp[4 * h + r] = (E)p;
+          bs[4 * h + r] = (E)(p * dp[h][r]);
+        }
+      // dV^T += dO^T . P, dK^T += Q^T . dS (transposing reads)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const v4 o0 = M::tr(ys + kb[0] * RSE + tr_off + 16 * db);
+        const v4 o1 = M::tr(ys + kb[1] * RSE + tr_off + 16 * db);
+        adv[db] = M::mma(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), bp, adv[db]);
+        const v4 q0 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
+        const v4 q1 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+        adk[db] = M::mma(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), bs, adk[db]);
+      }
+    }
+  }
+  if (!kv) return;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    v4 wk, wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wk[r] = (E)(adk[db][r] * P.scale);
+      wv[r] = (E)adv[db][r];
+    }
+    *reinterpret_cast<v4 *>(dk + koff + 16 * db + 4 * gq) = wk;
+    *reinterpret_cast<v4 *>(dv + koff + 16 * db + 4 * gq) = wv;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 int ilog2c(int x) {
@@ -535,22 +1009,63 @@ struct LChoice {
   bool ok;
 };
 
+// Staged rows of a box layout (rank >= 2: rows padded to a power of two).
+int lds_rows(int R, const int Em[3]) {
+  if (R == 1) return Em[2];
+  int p2 = 1;
+  while (p2 < Em[2]) p2 <<= 1;
+  return Em[0] * Em[1] * p2;
+}
+
 size_t box_lds_bytes(int ebox, int D) {
-  return 2 * (size_t)(ebox + kSlack) * lds_row(D) * 2;
+  return (size_t)(ebox + kSlack) * lds_row(D) * 2;
+}
+
+// Host twins of the window rules.
+int h_ws(const Axis &x, int i, int Lr) {
+  return x.causal ? std::max(i - x.K + 1, 0)
+                  : std::min(std::max(i - x.K / 2, 0), Lr - x.K);
+}
+int h_we(const Axis &x, int i, int Lr) {
+  return x.causal ? i + 1 : h_ws(x, i, Lr) + x.K;
+}
+int h_iws(const Axis &x, int j, int Lr) {
+  return x.causal ? j : (j <= x.K - 1 ? 0 : j - x.K / 2);
+}
+int h_iwe(const Axis &x, int j, int Lr) {
+  return x.causal ? std::min(j + x.K, Lr) : (j >= Lr - x.K ? Lr : j + x.K / 2 + 1);
+}
+
+// Largest box (forward: keys of a tile's queries; inverse: queries of a
+// tile's keys) over every tile of extent t on axis x, by enumeration.
+int box_max(const Axis &x, int t, bool inverse) {
+  int best = 1;
+  for (int r = 0; r < x.d && r < x.L; ++r) {
+    const int Lr = (x.L - 1 - r) / x.d + 1;
+    for (int i0 = 0; i0 < Lr; i0 += t) {
+      const int i1 = std::min(i0 + t, Lr) - 1;
+      const int e = inverse ? h_iwe(x, i1, Lr) - h_iws(x, i0, Lr)
+                            : h_we(x, i1, Lr) - h_ws(x, i0, Lr);
+      best = std::max(best, e);
+    }
+  }
+  return best;
 }
 
 // Wave tile: the power-of-two shape with the fewest (waves x chunks);
 // workgroup: up to 4 waves stacked along the axis with the smallest staged
-// box per wave whose K/V box fits the LDS budget.
-LChoice lean_choice(const Prob &P) {
+// box per wave whose box fits the LDS budget.  For the backward the boxes
+// also cover the inverse windows (query boxes of key tiles) and the LDS
+// holds a (lse, delta) pair per staged row.
+LChoice lean_choice(const Prob &P, bool bwd) {
   const int R = P.rank, lead = 3 - R;
   LChoice best{};
   best.ok = false;
   double best_cost = 1e300;
-  int Lr[3];
-  for (int a = 0; a < 3; ++a) Lr[a] = (P.ax[a].L + P.ax[a].d - 1) / P.ax[a].d;
-  auto box_ext = [&](int a, int t) {
-    return std::min(std::min(t, Lr[a]) + P.ax[a].K - 1, Lr[a]);
+  auto ext = [&](int a, int t) {
+    if (a < lead) return 1;
+    const int f = box_max(P.ax[a], t, false);
+    return bwd ? std::max(f, box_max(P.ax[a], t, true)) : f;
   };
   for (int l0 = 0; l0 <= 4; ++l0)
     for (int l1 = 0; l0 + l1 <= 4; ++l1) {
@@ -561,29 +1076,29 @@ LChoice lean_choice(const Prob &P) {
       if (!ok) continue;
       double waves = 1.0, rows = 1.0;
       for (int a = lead; a < 3; ++a) {
-        waves *= (double)P.ax[a].d * ((Lr[a] + Tt[a] - 1) / Tt[a]);
-        if (a < 2) rows *= box_ext(a, Tt[a]);
+        const Axis &x = P.ax[a];
+        const int Lr = (x.L + x.d - 1) / x.d;
+        waves *= (double)x.d * ((Lr + Tt[a] - 1) / Tt[a]);
+        if (a < 2) rows *= ext(a, Tt[a]);
       }
-      const double chunks = rows * std::ceil(box_ext(2, Tt[2]) / 16.0);
-      const double cost = waves * chunks;
+      const int e2 = ext(2, Tt[2]);
+      const double cost = waves * rows * std::ceil(e2 / 16.0);
       if (cost < best_cost) {
         best_cost = cost;
         for (int a = 0; a < 3; ++a) best.T[a] = Tt[a];
-        best.cpr1 = R > 1 && box_ext(2, Tt[2]) <= 16;
+        best.cpr1 = R > 1 && e2 <= 16;
       }
     }
-  // workgroup shape
   double best_per_wave = 1e300;
   for (int W = 4; W >= 1; W >>= 1)
     for (int sa = lead; sa < 3; ++sa) {
-      if (W > 1 && best.T[sa] >= Lr[sa]) continue;
-      int Em[3], ebox = 1;
-      for (int a = 0; a < 3; ++a) {
-        const int tw = best.T[a] * (a == sa ? W : 1);
-        Em[a] = a < lead ? 1 : box_ext(a, tw);
-        ebox *= Em[a];
-      }
-      if (box_lds_bytes(ebox, P.D) > kLdsBudget) continue;
+      const Axis &x = P.ax[sa];
+      if (W > 1 && best.T[sa] >= (x.L + x.d - 1) / x.d) continue;
+      int Em[3];
+      for (int a = 0; a < 3; ++a) Em[a] = ext(a, best.T[a] * (a == sa ? W : 1));
+      const int ebox = lds_rows(R, Em);
+      size_t bytes = box_lds_bytes(ebox, P.D);
+      if (bytes > kLdsBudget) continue;
       const double per_wave = (double)ebox / W;
       if (per_wave < best_per_wave * 0.999) {
         best_per_wave = per_wave;
@@ -630,13 +1145,17 @@ LProb make_lprob(const Prob &P, const LChoice &C) {
     y.fnt = make_fastdiv((uint32_t)y.nt);
     grid *= x.d * y.nt;
   }
-  L.ebox = C.Em[0] * C.Em[1] * C.Em[2];
+  L.ebox = lds_rows(P.rank, C.Em);
+  L.lgP2 = P.rank == 1 ? 0 : ilog2c(C.Em[2]);
+  L.fGrid = make_fastdiv((uint32_t)grid);
   L.n_tiles = P.B * P.H * grid;
   L.n_launch = (L.n_tiles + 7) & ~7;
   L.fH = make_fastdiv((uint32_t)P.H);
   L.fRep = make_fastdiv((uint32_t)P.rep);
-  L.fE2 = make_fastdiv((uint32_t)C.Em[2]);
   L.fE1 = make_fastdiv((uint32_t)C.Em[1]);
+  L.rep = P.rep;
+  L.scale = P.scale;
+  L.fHkv = make_fastdiv((uint32_t)P.Hkv);
   return L;
 }
 
@@ -665,7 +1184,18 @@ bool lean_eligible(const Prob &P, int dtype) {
   const int64_t elems = (int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L *
                         std::max(P.H, P.Hkv) * P.D;
   if (elems >= (int64_t(1) << 31)) return false;
-  return lean_choice(P).ok;
+  // per-axis element strides fit the 24-bit multiplies of the staging code
+  int64_t tok = 1;
+  for (int a = 2; a >= 0; --a) {
+    if ((int64_t)P.ax[a].d * tok * std::max(P.H, P.Hkv) * P.D >= (int64_t(1) << 24))
+      return false;
+    tok *= P.ax[a].L;
+  }
+  return lean_choice(P, false).ok;
+}
+
+bool lean_bwd_eligible(const Prob &P, int dtype) {
+  return lean_eligible(P, dtype) && lean_choice(P, true).ok;
 }
 
 #define LEAN_D(D_, BODY) \
@@ -681,7 +1211,7 @@ bool lean_eligible(const Prob &P, int dtype) {
 
 void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, void *out, float *lse, hipStream_t st) {
-  const LChoice C = lean_choice(P);
+  const LChoice C = lean_choice(P, false);
   const LProb L = make_lprob(P, C);
   if (L.n_tiles == 0) return;
   const size_t lds = box_lds_bytes(L.ebox, P.D);
@@ -707,6 +1237,43 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef LF_D
 #undef LF_R
 #undef LF_LAUNCH
+}
+
+void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *out, const float *lse,
+              const void *dout, const float *dlse, void *dq, void *dk,
+              void *dv, hipStream_t st) {
+  const LChoice C = lean_choice(P, true);
+  LProb L = make_lprob(P, C);
+  const int grid_sp = (int)L.fGrid.d;
+  L.n_tiles = P.B * P.Hkv * grid_sp;
+  L.n_launch = (L.n_tiles + 7) & ~7;
+  if (L.n_tiles == 0) return;
+  const size_t lds = box_lds_bytes(L.ebox, P.D);
+  const dim3 grid(L.n_launch), block(64 * C.W);
+#define LB_LAUNCH(TT, DD, RR, CC)                                              \
+  hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC>), grid, block, lds, st, L,        \
+                     (const TT *)q, (const TT *)k, (const TT *)v,              \
+                     (const TT *)out, lse, (const TT *)dout, dlse, (TT *)dq,   \
+                     (TT *)dk, (TT *)dv)
+#define LB_R(TT, DD)                                                          \
+  do {                                                                        \
+    if (P.rank == 1) LB_LAUNCH(TT, DD, 1, false);                             \
+    else if (P.rank == 2) {                                                   \
+      if (C.cpr1) LB_LAUNCH(TT, DD, 2, true); else LB_LAUNCH(TT, DD, 2, false); \
+    } else {                                                                  \
+      if (C.cpr1) LB_LAUNCH(TT, DD, 3, true); else LB_LAUNCH(TT, DD, 3, false); \
+    }                                                                         \
+  } while (0)
+#define LB_D(DD)                          \
+  do {                                    \
+    if (dtype == NA_BF16) LB_R(bf16_t, DD); \
+    else LB_R(f16_t, DD);                 \
+  } while (0)
+  LEAN_D(P.D, LB_D);
+#undef LB_D
+#undef LB_R
+#undef LB_LAUNCH
 }
 
 }  // namespace na
