@@ -812,6 +812,16 @@ __global__ void __launch_bounds__(256)
             kr[h][st] = *reinterpret_cast<const v8 *>(xs + kb[h] * RSE + ka_off + 32 * st);
             vr[h][st] = *reinterpret_cast<const v8 *>(ys + kb[h] * RSE + ka_off + 32 * st);
           }
+        // K^T operands of dQ^T += K^T . dS^T, read now so their latency
+        // overlaps the score MFMAs and exponentials
+        v8 kt[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const v4 lo4 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
+          const v4 hi4 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+          kt[db] = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep every read of the pair ahead
         // S^T masked through its initial value, dP^T - delta through its
         f32x4 sc[2], dp[2];
 #pragma unroll
@@ -840,14 +850,9 @@ __global__ void __launch_bounds__(256)
             const float p = __builtin_amdgcn_exp2f(fmaf(sc[h][r], sl2, -lse2));
             bs[4 * h + r] = (E)(p * dp[h][r]);
           }
-        // dQ^T += K^T . dS^T (K^T through the transposing read)
+        // dQ^T += K^T . dS^T
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const v4 lo4 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
-          const v4 hi4 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
-          const v8 a8 = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[db] = M::mma(a8, bs, acc[db]);
-        }
+        for (int db = 0; db < NDB; ++db) acc[db] = M::mma(kt[db], bs, acc[db]);
       }
       if (qv) {
 #pragma unroll
@@ -934,6 +939,19 @@ __global__ void __launch_bounds__(256)
         for (int r = 0; r < 4; ++r)
           ls2[h][r] = *reinterpret_cast<const float *>(xs + (kb[h] + 4 * gq + r) * RSE + D);
       }
+      // dO^T and Q^T operands of the dV / dK MFMAs, read now so their
+      // latency overlaps the score MFMAs and exponentials
+      v8 ot[NDB], qt[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const v4 o0 = M::tr(ys + kb[0] * RSE + tr_off + 16 * db);
+        const v4 o1 = M::tr(ys + kb[1] * RSE + tr_off + 16 * db);
+        ot[db] = __builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const v4 q0 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
+        const v4 q1 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+        qt[db] = __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep every read of the pair ahead
       // S masked through its initial value, dP - delta through its
       f32x4 sc[2], dp[2];
 #pragma unroll
@@ -964,15 +982,11 @@ __global__ void __launch_bounds__(256)
           bp[4 * h + r] = (E)p;
           bs[4 * h + r] = (E)(p * dp[h][r]);
         }
-      // dV^T += dO^T . P, dK^T += Q^T . dS (transposing reads)
+      // dV^T += dO^T . P, dK^T += Q^T . dS
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const v4 o0 = M::tr(ys + kb[0] * RSE + tr_off + 16 * db);
-        const v4 o1 = M::tr(ys + kb[1] * RSE + tr_off + 16 * db);
-        adv[db] = M::mma(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), bp, adv[db]);
-        const v4 q0 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
-        const v4 q1 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
-        adk[db] = M::mma(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), bs, adk[db]);
+        adv[db] = M::mma(ot[db], bp, adv[db]);
+        adk[db] = M::mma(qt[db], bs, adk[db]);
       }
     }
   }
