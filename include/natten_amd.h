@@ -51,7 +51,10 @@ enum na_flags {
   NA_FLAG_DENSE = 1,
   /* Run the generic vector-ALU kernels even where the matrix-core kernels
    * apply (for A/B comparison of the two implementations). */
-  NA_FLAG_GENERIC = 2
+  NA_FLAG_GENERIC = 2,
+  /* Run the 32-query matrix-core kernels where the lean workgroup kernels
+   * would apply (A/B comparison; see na_kernel_path). */
+  NA_FLAG_NO_LEAN = 4
 };
 
 /*
@@ -117,6 +120,19 @@ int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
  * B[k][n] = (3k + n) % 5 - 2.
  */
 int na_mfma_selftest(int32_t dtype, float *out, void *stream);
+
+/*
+ * Diagnostic with no counterpart in the reference: the kernel family that
+ * na_fwd (backward = 0) or na_bwd (backward = 1) runs for these parameters,
+ * one of na_kernel_path_t, or the negated na_status of invalid parameters.
+ * Launches nothing and reads no device memory.
+ */
+enum na_kernel_path_t {
+  NA_PATH_GENERIC = 0, /* vector-ALU kernels: every dtype / head_dim / stride */
+  NA_PATH_MFMA = 1,    /* 32-query matrix-core kernels */
+  NA_PATH_LEAN = 2     /* workgroup-staged 16x16x32 matrix-core kernels */
+};
+int na_kernel_path(const na_params *p, int32_t backward);
 
 /* ---- fused neighborhood attention --------------------------------------- */
 /*

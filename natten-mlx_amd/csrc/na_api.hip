@@ -117,7 +117,13 @@ bool use_mfma(const na_params *p, const na::Prob &P) {
 }
 
 bool use_lean(const na_params *p, const na::Prob &P) {
-  return (p->flags & NA_FLAG_GENERIC) == 0 && na::lean_eligible(P, p->dtype);
+  return (p->flags & (NA_FLAG_GENERIC | NA_FLAG_NO_LEAN)) == 0 &&
+         na::lean_eligible(P, p->dtype);
+}
+
+bool use_lean_bwd(const na_params *p, const na::Prob &P) {
+  return (p->flags & (NA_FLAG_GENERIC | NA_FLAG_NO_LEAN)) == 0 &&
+         na::lean_bwd_eligible(P, p->dtype);
 }
 
 bool use_msplit(const na_params *p, const na::Prob &P) {
@@ -259,6 +265,15 @@ int na_mfma_selftest(int32_t dtype, float *out, void *stream) {
   return launch_status("na_mfma_selftest");
 }
 
+int na_kernel_path(const na_params *p, int32_t backward) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, true);
+  if (rc != NA_OK) return -rc;
+  if (backward ? use_lean_bwd(p, P) : use_lean(p, P)) return NA_PATH_LEAN;
+  if (use_mfma(p, P)) return NA_PATH_MFMA;
+  return NA_PATH_GENERIC;
+}
+
 int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
                       void *stream) {
   na::Prob P;
@@ -320,7 +335,7 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                 delta_bytes(P), workspace == nullptr ? (size_t)0 : workspace_bytes);
   float *delta = static_cast<float *>(workspace);
   const hipStream_t st = as_stream(stream);
-  if ((p->flags & NA_FLAG_GENERIC) == 0 && na::lean_bwd_eligible(P, p->dtype)) {
+  if (use_lean_bwd(p, P)) {
     na::lean_bwd(P, p->dtype, q, k, v, out, lse, dout, dlse, dq, dk, dv, st);
   } else if (use_mfma(p, P)) {
     const bool dextra =

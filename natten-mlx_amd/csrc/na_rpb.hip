@@ -198,6 +198,38 @@ __device__ __forceinline__ void scale_round(float (&v)[kNT][VEC], float s) {
 }
 
 
+// Block-wide copy of n 16-byte units, four per thread in flight at a time
+// (every load of a batch is issued before its stores), so a copy of a few
+// units per thread costs one memory latency rather than one per unit.  The
+// trip count is uniform and indices past the end are clamped onto the last
+// unit (its copies write the same value), so nothing branches per lane.
+__device__ __forceinline__ void block_copy16(uint4 *dst, const uint4 *src,
+                                             int64_t n) {
+  constexpr int kB = 4;
+  if (n <= 0) return;
+  const int nn = (int)n, nt = (int)blockDim.x, tid = (int)threadIdx.x;
+  for (int base = 0; base < nn; base += kB * nt) {
+    uint4 r[kB];
+    int ix[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      ix[j] = min(base + j * nt + tid, nn - 1);
+      r[j] = src[ix[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) dst[ix[j]] = r[j];
+  }
+}
+
+// Block-wide copy of n floats between 16-byte aligned ranges: 16-byte
+// units through block_copy16, then the tail.
+__device__ __forceinline__ void block_copy_f32(float *dst, const float *src,
+                                               int64_t n) {
+  const int64_t n4 = n >> 2;
+  block_copy16(reinterpret_cast<uint4 *>(dst), reinterpret_cast<const uint4 *>(src), n4);
+  for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+}
+
 // Rank 1: the keys (or values) of every row of a block lie within K*d
 // positions of the block's rows, i.e. in the row range [lo, hi) below;
 // the block copies that range into LDS with contiguous 16-byte loads
@@ -212,9 +244,8 @@ __device__ __forceinline__ int64_t stage_window(const RpbProb &A, const T *y,
   const int64_t lo = max((int64_t)0, row0 - reach);
   const int64_t hi = min((int64_t)A.n_rows, row0 + rows + reach);
   const int64_t n16 = (hi - lo) * A.D * (int64_t)sizeof(T) / 16;
-  const uint4 *src = reinterpret_cast<const uint4 *>(y + lo * A.D);
-  uint4 *dst = reinterpret_cast<uint4 *>(ystage);
-  for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
+  block_copy16(reinterpret_cast<uint4 *>(ystage),
+               reinterpret_cast<const uint4 *>(y + lo * A.D), n16);
   __syncthreads();
   return lo;
 }
@@ -291,8 +322,7 @@ __global__ void __launch_bounds__(256)
     const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
     const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
     const int64_t nv = rows * A.KK;
-    float *o = out + row0 * A.KK;
-    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) o[i] = stage[i];
+    block_copy_f32(out + row0 * A.KK, stage, nv);
   }
 }
 
@@ -315,8 +345,7 @@ __global__ void __launch_bounds__(256)
     const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
     const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
     const int64_t nv = rows * A.KK;
-    const float *src = w + row0 * A.KK;
-    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) stage[i] = src[i];
+    block_copy_f32(stage, w + row0 * A.KK, nv);
     __syncthreads();
     wr = stage + (int)(threadIdx.x >> lgG) * A.KK;
   }

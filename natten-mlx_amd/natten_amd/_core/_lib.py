@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 NA_F32, NA_F16, NA_BF16 = 0, 1, 2
 NA_FLAG_DENSE = 1
 NA_FLAG_GENERIC = 2
+NA_FLAG_NO_LEAN = 4
 ABI_VERSION = 2
 
 _STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "launch failure",
@@ -99,6 +100,7 @@ SIGNATURES = {
     "na_window_start_partition": (_I, [_I, _I, _I, _I, _I]),
     "na_neighbor_table": (ctypes.c_int, [_P, _V, _V, _V]),
     "na_mfma_selftest": (ctypes.c_int, [_I, _V, _V]),
+    "na_kernel_path": (ctypes.c_int, [_P, _I]),
     "na_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V, _V, _V]),
     "na_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
     "na_bwd": (ctypes.c_int, [_P] + [_V] * 15 + [ctypes.c_size_t, _V]),

@@ -24,6 +24,7 @@ from . import _lib
 # NATTEN_AMD_GENERIC=1 (or the generic_kernels() context) runs the fused op on
 # the generic vector-ALU kernels even where the matrix-core kernels apply.
 _force_generic = os.environ.get("NATTEN_AMD_GENERIC", "0") == "1"
+_no_lean = False
 
 
 @contextlib.contextmanager
@@ -36,6 +37,19 @@ def generic_kernels(enabled: bool = True):
         yield
     finally:
         _force_generic = prev
+
+
+@contextlib.contextmanager
+def no_lean_kernels(enabled: bool = True):
+    """Temporarily route the fused op to the 32-query matrix-core kernels
+    where the lean workgroup kernels would run (A/B comparison)."""
+    global _no_lean
+    prev = _no_lean
+    _no_lean = enabled
+    try:
+        yield
+    finally:
+        _no_lean = prev
 
 
 def is_available() -> bool:
@@ -74,7 +88,8 @@ def _params(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_
         rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
         tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
         tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra,
-        (_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0),
+        (_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0)
+        | (_lib.NA_FLAG_NO_LEAN if _no_lean else 0),
         sample_extent)
 
 
@@ -103,6 +118,22 @@ def fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale,
                           _lib.ptr(extra_v), _lib.ptr(out), _lib.ptr(lse), _lib.stream_of(q)),
                "na_fwd")
     return out, lse
+
+
+KERNEL_PATHS = {0: "generic", 1: "mfma", 2: "lean"}
+
+
+def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_extra=0,
+                dense=False, sample_extent=None, backward=False):
+    """Name of the kernel family na_fwd (or na_bwd) runs for this problem:
+    "generic", "mfma" or "lean" (a diagnostic; launches nothing)."""
+    lib = _lib.load()
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                sample_extent)
+    r = int(lib.na_kernel_path(p, 1 if backward else 0))
+    if r < 0:
+        _lib.check(-r, "na_kernel_path")
+    return KERNEL_PATHS[r]
 
 
 def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, dilation,

@@ -80,7 +80,14 @@ def test_mfma_parity(case, dtype):
     ref = O.grads(lambda a, b, c: O.na_functional(a, b, c, ks, 1, dil, caus), (q, k, v), (go,))
     for g, r, nm in zip(grads, ref, ("dq", "dk", "dv")):
         assert_close(g, r, dtype, f"{name} {nm}")
-    # the generic kernels meet the same bar on the same inputs
+    # the 32-query matrix-core kernels (where the lean ones run by default)
+    # and the generic kernels meet the same bar on the same inputs
+    with hip.no_lean_kernels():
+        out1, lse1, grads1 = _run(fn, q, k, v, go, kernel_size=ks, dilation=dil, is_causal=caus)
+    assert_close(out1, ref_out, dtype, f"{name} mfma out")
+    assert_close(lse1, ref_lse, dtype, f"{name} mfma lse")
+    for g, r, nm in zip(grads1, ref, ("dq", "dk", "dv")):
+        assert_close(g, r, dtype, f"{name} mfma {nm}")
     with hip.generic_kernels():
         out2, lse2, grads2 = _run(fn, q, k, v, go, kernel_size=ks, dilation=dil, is_causal=caus)
     assert_close(out2, ref_out, dtype, f"{name} generic out")

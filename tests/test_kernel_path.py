@@ -1,0 +1,48 @@
+"""Kernel selection (na_kernel_path, no GPU needed): which family each
+BASELINE configuration and each eligibility boundary dispatches to.  The
+lean workgroup kernels take the common problems; varlen, additional tokens
+and over-budget boxes stay on the 32-query matrix-core kernels; fp32, even
+kernels and strides on the generic kernels."""
+
+import torch
+
+from natten_amd._core import hip
+
+
+def _path(shape_q, hkv, ks, dil, caus, dtype=torch.bfloat16, stride=None, backward=False,
+          **kw):
+    q = torch.empty(shape_q, dtype=dtype)
+    k = torch.empty((*shape_q[:-2], hkv, shape_q[-1]), dtype=dtype)
+    st = stride or (1,) * len(ks)
+    return hip.kernel_path(q, k, ks, st, dil, caus, backward=backward, **kw)
+
+
+def test_config2_runs_lean_both_ways():
+    for d in ((1, 1), (4, 4)):
+        for bwd in (False, True):
+            assert _path((4, 56, 56, 4, 32), 4, (7, 7), d, (False, False), backward=bwd) == "lean"
+
+
+def test_config3_box_exceeds_lds_budget():
+    assert _path((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False)) == "mfma"
+
+
+def test_lean_boundaries():
+    base = ((2, 40, 40, 4, 32), 4, (7, 7), (1, 1), (False, False))
+    assert _path(*base) == "lean"
+    assert _path(*base, dtype=torch.float32) == "generic"       # fp32: vector ALU
+    assert _path(*base, stride=(2, 1)) == "generic"             # strided
+    assert _path((2, 40, 40, 4, 32), 4, (6, 7), (1, 1), (False, False)) == "generic"  # even K
+    assert _path((2, 40, 40, 4, 48), 4, (7, 7), (1, 1), (False, False)) == "generic"  # head_dim 48
+    assert _path((2, 40, 40, 4, 32), 4, (7, 7), (1, 1), (False, False),
+                 n_extra=3) == "mfma"                            # additional tokens
+    ext = torch.tensor([[40, 40], [20, 30]], dtype=torch.int32)
+    assert _path((2, 40, 40, 4, 32), 4, (7, 7), (1, 1), (False, False),
+                 sample_extent=ext) == "mfma"                    # varlen
+    # d * K > L on a non-causal axis (the legacy boundary windows)
+    assert _path((2, 40, 12, 4, 32), 4, (7, 7), (1, 2), (False, False)) == "mfma"
+    with hip.generic_kernels():
+        assert _path(*base) == "generic"
+    with hip.no_lean_kernels():
+        assert _path(*base) == "mfma"
+        assert _path(*base, backward=True) == "mfma"
