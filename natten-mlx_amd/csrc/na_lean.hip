@@ -10,20 +10,23 @@
 // box of keys and the queries whose windows hold a key form a box too.
 //
 // Tiling.  A wave owns 16 queries of one phase: a T0 x T1 x T2 box of
-// powers of two (product 16).  The union of their windows is a box of keys
-// whose innermost extent is padded to 16 * CPR slots, so a chunk of 16 keys
-// lies inside one box row and its row is wave-uniform.  Per chunk:
-//   S^T = K . Q^T            mfma_f32_16x16x32 (A = K rows, B = Q rows, both
-//                            straight from global memory); lane l holds the
-//                            scores of query l%16 with keys 4(l/16) + r
-//   masked online softmax   the row test is one compare per lane and chunk,
-//                            the column tests are per lane and fixed
-//   O^T += V^T . P^T         V rows are written to LDS with 16-byte stores and
-//                            come back transposed (ds_read_tr16_b64) as the A
-//                            operand; two chunks per MFMA, the scores of both
-//                            packed as the B operand with the same k order.
-// A group of NB = 256/D chunks is loaded at once; the next group's loads are
-// issued as soon as the current group's K and V registers are consumed.
+// powers of two (product 16); W waves stacked along one axis form a
+// workgroup.  The workgroup stages the box of keys its queries' windows
+// cover in LDS once (innermost extent padded to a power of two), and each
+// wave walks the chunks of 16 keys of its own sub-box (one box row each when
+// that row is at most 16 keys wide).  Per chunk:
+//   S^T = K . Q^T            mfma_f32_16x16x32 (A = staged K rows, B = Q
+//                            rows in registers); lane l holds the scores of
+//                            query l%16 with keys 4(l/16) + r; the window
+//                            mask is the accumulator's initial value
+//   masked online softmax   over a group of 256/D chunks, max and sum over
+//                            the query's four lanes by lane swaps
+//   O^T += V^T . P^T         V^T from the staged V rows through the
+//                            transposing LDS read (ds_read_tr16_b64); two
+//                            chunks per MFMA, their probabilities packed as
+//                            the B operand in the same k order.
+// The backward (k_wbwd) runs dQ over the staged K/V box and then, in the
+// same LDS, dK/dV over the staged query box of the tile's keys.
 #include <cmath>
 #include <cstdlib>
 
