@@ -99,6 +99,7 @@ struct LProb {
   int32_t ebox;       // staged rows: Em2 (rank 1) or Em0 * Em1 * 2^lgP2
   int32_t lgP2;       // rank >= 2: staged box rows are 2^lgP2 >= Em2 wide
   int32_t rep;        // query heads per key/value head
+  int32_t sl;         // rank 3: box layers (axis 0) staged at a time
   float scale;
   FastDiv fH, fRep;
   FastDiv fHkv;       // key/value heads
@@ -305,11 +306,12 @@ __device__ __forceinline__ float ldf(const float *base, int off) {
 }
 
 // Element offset of staged-box unit (row kk of the LDS layout, 16-byte unit
-// o): box coordinates from the layout (shifts; rank 3 divides by Em1),
-// clamped onto the tile's true box, then 24-bit products with the strides.
+// o): box coordinates from the layout (shifts; rank 3 divides by Em1 and
+// adds the first staged layer s0), clamped onto the tile's true box, then
+// 24-bit products with the strides.
 template <int R>
 __device__ __forceinline__ int unit_offset(const LProb &P, const LTile &t,
-                                           int kk, int o) {
+                                           int kk, int o, int s0) {
   int e0 = 0, e1 = 0, e2 = kk;
   if (R >= 2) {
     const int row = kk >> P.lgP2;
@@ -319,6 +321,7 @@ __device__ __forceinline__ int unit_offset(const LProb &P, const LTile &t,
     } else {
       e0 = (int)fdiv((uint32_t)row, P.fE1);
       e1 = row - e0 * P.ax[1].Em;
+      e0 += s0;
     }
   }
   int off = t.kbase + 8 * o;
@@ -403,7 +406,7 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
                                           const T *__restrict__ y,
                                           typename L16<T>::e *xs,
                                           typename L16<T>::e *ys, int tid,
-                                          int nthr) {
+                                          int nthr, int s0) {
   typedef typename L16<T>::v8 v8;
   constexpr int OCT = D / 8;  // 16-byte units per row
   constexpr int RSE = lds_row(D);
@@ -415,7 +418,7 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
     for (int j = 0; j < 4; ++j) {
       const int u = min(u0 + j * nthr + tid, nun - 1);
       const int kk = u / OCT, o = u % OCT;
-      const int g = unit_offset<R>(P, t, kk, o);
+      const int g = unit_offset<R>(P, t, kk, o, s0);
       xr[j] = ld8(x, g);
       yr[j] = ld8(y, g);
       la[j] = kk * RSE + 8 * o;
@@ -492,12 +495,10 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int st = 0; st < NT; ++st) qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
 
-  // ---- the workgroup's K / V box to LDS ----
+  // ---- the workgroup's K / V box to LDS, in slabs of P.sl layers along
+  // axis 0 for rank 3 (one slab otherwise) ----
   E *ks = reinterpret_cast<E *>(smem);
   E *vs = ks + lds_y(D);
-  stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr);
-  __syncthreads();
-  if (!ws.any) return;
 
   // column part of the mask of the lane's 4 keys per chunk (fixed when CPR1)
   float cb0[4];
@@ -513,87 +514,99 @@ __global__ void __launch_bounds__(256)
   // 8 gq) and the transposing read (row 4 gq + n / 4, column 4 (n % 4))
   const int ka_off = n * RSE + 8 * gq;
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
-  const int ngroups = (ws.nchunks + NB - 1) / NB;
-  Cursor cc{ws.ws[0], ws.ws[1], 0};
-  const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
-
-  for (int grp = 0; grp < ngroups; ++grp) {
-    // ---- scores of the group: chunk rows, operand reads, MFMAs, masks ----
-    int kb[NB];       // first LDS row of each chunk
-    bool rok[NB];
-    int csj[NB];
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const bool real = grp * NB + j < ws.nchunks;
-      kb[j] = real ? ((cc.e0 * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs : key0;
-      csj[j] = cc.cs;
-      bool ok = real;
-      if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
-      if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
-      rok[j] = ok;
-      advance(cc, ws);
-    }
-    v8 ka[NB][NT];
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int st = 0; st < NT; ++st)
-        ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
-    f32x4 sv[NB];  // masked raw scores
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      float cb[4];
-      if (CPR1) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
-      } else {
-        col_bias(ws.ws[2] + 16 * csj[j] + 4 * gq - wl[2], ww[2], cb);
+  const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  for (int si = 0; si < nsl; ++si) {
+    const int s0 = si * P.sl;
+    if (si > 0) __syncthreads();  // the previous slab's reads are done
+    stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+    __syncthreads();
+    if (!ws.any) continue;
+    // the wave's box rows inside this slab
+    const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+    const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+    const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+    const int ngroups = (nch + NB - 1) / NB;
+    Cursor cc{a0, ws.ws[1], 0};
+    const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    for (int grp = 0; grp < ngroups; ++grp) {
+      // ---- scores of the group: chunk rows, operand reads, MFMAs, masks ----
+      int kb[NB];       // first LDS row of each chunk
+      bool rok[NB];
+      int csj[NB];
+  #pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const bool real = grp * NB + j < nch;
+        kb[j] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs : key0;
+        csj[j] = cc.cs;
+        bool ok = real;
+        if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+        if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+        rok[j] = ok;
+        advance(cc, ws);
       }
-      sv[j] = mask_init(rok[j], cb);
-#pragma unroll
-      for (int st = 0; st < NT; ++st) sv[j] = M::mma(ka[j][st], qf[st], sv[j]);
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][r]);
-    // ---- online softmax ----
-    mx = quad_max(mx) * sl2;
-    // The reference point m may trail the running max by up to 8 (a factor
-    // 2^8 in P): exact after the final division by l, and it spares the O
-    // rescale on groups that do not raise any query's max by more.
-    if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
-      const float mn = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
-      l *= alpha;
-#pragma unroll
-      for (int j = 0; j < NDB; ++j) o[j] *= alpha;
-      m = mn;
-    }
-    const float mu = m == -INFINITY ? 0.f : m;
-    v8 bp[NB / 2];
-#pragma unroll
-    for (int jj = 0; jj < NB / 2; ++jj)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
-          l += p;
-          bp[jj][4 * h + r] = (E)p;
+      v8 ka[NB][NT];
+  #pragma unroll
+      for (int j = 0; j < NB; ++j)
+  #pragma unroll
+        for (int st = 0; st < NT; ++st)
+          ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
+      f32x4 sv[NB];  // masked raw scores
+  #pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        float cb[4];
+        if (CPR1) {
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
+        } else {
+          col_bias(ws.ws[2] + 16 * csj[j] + 4 * gq - wl[2], ww[2], cb);
         }
-    // ---- O^T += V^T . P^T, two chunks per MFMA ----
-#pragma unroll
-    for (int jj = 0; jj < NB / 2; ++jj) {
-      const E *ca = vs + kb[2 * jj] * RSE + tr_off;
-      const E *cb = vs + kb[2 * jj + 1] * RSE + tr_off;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const v4 lo4 = M::tr(ca + 16 * db);
-        const v4 hi4 = M::tr(cb + 16 * db);
-        const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        o[db] = M::mma(a, bp[jj], o[db]);
+        sv[j] = mask_init(rok[j], cb);
+  #pragma unroll
+        for (int st = 0; st < NT; ++st) sv[j] = M::mma(ka[j][st], qf[st], sv[j]);
+      }
+      float mx = -INFINITY;
+  #pragma unroll
+      for (int j = 0; j < NB; ++j)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][r]);
+      // ---- online softmax ----
+      mx = quad_max(mx) * sl2;
+      // The reference point m may trail the running max by up to 8 (a factor
+      // 2^8 in P): exact after the final division by l, and it spares the O
+      // rescale on groups that do not raise any query's max by more.
+      if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+        const float mn = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+        l *= alpha;
+  #pragma unroll
+        for (int j = 0; j < NDB; ++j) o[j] *= alpha;
+        m = mn;
+      }
+      const float mu = m == -INFINITY ? 0.f : m;
+      v8 bp[NB / 2];
+  #pragma unroll
+      for (int jj = 0; jj < NB / 2; ++jj)
+  #pragma unroll
+        for (int h = 0; h < 2; ++h)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
+            l += p;
+            bp[jj][4 * h + r] = (E)p;
+          }
+      // ---- O^T += V^T . P^T, two chunks per MFMA ----
+  #pragma unroll
+      for (int jj = 0; jj < NB / 2; ++jj) {
+        const E *ca = vs + kb[2 * jj] * RSE + tr_off;
+        const E *cb = vs + kb[2 * jj + 1] * RSE + tr_off;
+  #pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const v4 lo4 = M::tr(ca + 16 * db);
+          const v4 hi4 = M::tr(cb + 16 * db);
+          const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[db] = M::mma(a, bp[jj], o[db]);
+        }
       }
     }
   }
@@ -628,7 +641,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
                                            const float *__restrict__ dlse,
                                            typename L16<T>::e *qs,
                                            typename L16<T>::e *os, int tid,
-                                           int nthr) {
+                                           int nthr, int s0) {
   typedef typename L16<T>::v8 v8;
   constexpr int OCT = D / 8;
   constexpr int RSE = lds_row(D);
@@ -642,7 +655,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
       const int u = min(u0 + j * nthr + tid, nun - 1);
       kk[j] = u / OCT;
       o[j] = u % OCT;
-      const int g = unit_offset<R>(P, t, kk[j], o[j]);
+      const int g = unit_offset<R>(P, t, kk[j], o[j], s0);
       const int row = (g - 8 * o[j]) / D;
       qr[j] = ld8(q, g);
       dr[j] = ld8(dout, g);
@@ -713,13 +726,14 @@ __device__ __forceinline__ int lane_rows(const LProb &P, const LTile &t,
 // and column segment of each (padding chunks: row 0 of the sub-box, masked).
 template <int R>
 __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
-                                          int Em1, int lgP2, int key0,
+                                          int nch, int s0, int Em1, int lgP2,
+                                          int key0,
                                           const int wl[3], const int ww[3],
                                           int kb[2], bool rok[2], int cs[2]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const bool real = c0 + h < ws.nchunks;
-    kb[h] = real ? ((cc.e0 * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
+    const bool real = c0 + h < nch;
+    kb[h] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
     cs[h] = cc.cs;
     bool ok = real;
     if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
@@ -775,8 +789,10 @@ __global__ void __launch_bounds__(256)
   {
     tile_box<R, false>(P, t, t.hk, P.Hkv);
     const WSub ws = wave_sub<R, false>(P, t, w);
-    stage_box<T, D, R>(P, t, k, v, xs, ys, tid, nthr);
-    const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    // the K / V box in slabs of P.sl layers along axis 0 (rank 3); a single
+    // slab is staged once for every query head of the group
+    const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+    const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
     for (int hr = 0; hr < P.rep; ++hr) {
       const int hq = t.hk * P.rep + hr;
       bool qv;
@@ -794,19 +810,30 @@ __global__ void __launch_bounds__(256)
       }
       const float lse2 = ldf(lse, qoff / D) * kLog2e;
       const float dl = dlse != nullptr ? ldf(dlse, qoff / D) : 0.f;
-      if (hr == 0) __syncthreads();  // the K / V box is staged
-      if (!ws.any) continue;
-      const float delta = quad_sum(dsum) - dl;
+      float delta = 0.f;
       float cb0[4];
       col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
       f32x4 acc[NDB];
 #pragma unroll
       for (int j = 0; j < NDB; ++j) acc[j] = zero4();
-      Cursor cc{ws.ws[0], ws.ws[1], 0};
-      for (int c0 = 0; c0 < ws.nchunks; c0 += 2) {
+      for (int si = 0; si < nsl; ++si) {
+      const int s0 = si * P.sl;
+      if (nsl > 1 || hr == 0) {
+        if (hr > 0 || si > 0) __syncthreads();  // the previous slab's reads are done
+        stage_box<T, D, R>(P, t, k, v, xs, ys, tid, nthr, s0);
+        __syncthreads();
+      }
+      if (!ws.any) continue;
+      if (si == 0) delta = quad_sum(dsum) - dl;
+      const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+      const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+      const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+      const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+      Cursor cc{a0, ws.ws[1], 0};
+      for (int c0 = 0; c0 < nch; c0 += 2) {
         int kb[2], cs[2];
         bool rok[2];
-        pair_rows<R>(ws, cc, c0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        pair_rows<R>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
         v8 kr[2][NT], vr[2][NT];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -857,6 +884,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int db = 0; db < NDB; ++db) acc[db] = M::mma(kt[db], bs, acc[db]);
       }
+      }  // slabs
       if (qv) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
@@ -916,19 +944,26 @@ __global__ void __launch_bounds__(256)
     adk[j] = zero4();
     adv[j] = zero4();
   }
-  const int key0 = ((ws.ws[0] * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
   const int qbase0 = t.kbase;  // query box rows of head hk * rep
+  const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
   for (int hr = 0; hr < P.rep; ++hr) {
     t.kbase = qbase0 + hr * D;  // query head hk * rep + hr
-    __syncthreads();  // the LDS reads of the previous box are done
-    stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr);
+    for (int si = 0; si < nsl; ++si) {
+    const int s0 = si * P.sl;
+    __syncthreads();  // the LDS reads of the previous box or slab are done
+    stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr, s0);
     __syncthreads();
     if (!ws.any) continue;
-    Cursor cc{ws.ws[0], ws.ws[1], 0};
-    for (int c0 = 0; c0 < ws.nchunks; c0 += 2) {
+    const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+    const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+    const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+    const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    Cursor cc{a0, ws.ws[1], 0};
+    for (int c0 = 0; c0 < nch; c0 += 2) {
       int kb[2], cs[2];
       bool rok[2];
-      pair_rows<R>(ws, cc, c0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+      pair_rows<R>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
       v8 qr[2][NT], orr[2][NT];
       float ls2[2][4];
 #pragma unroll
@@ -993,6 +1028,7 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
+  }  // slabs
   if (!kv) return;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
@@ -1018,10 +1054,21 @@ int ilog2c(int x) {
 
 constexpr size_t kLdsBudget = 80 * 1024;  // per workgroup: >= 2 per CU
 
+// LDS budget per workgroup; NATTEN_AMD_LEAN_LDS_KB overrides it (tuning).
+size_t lds_budget() {
+  static const size_t b = [] {
+    const char *e = std::getenv("NATTEN_AMD_LEAN_LDS_KB");
+    const long v = e != nullptr ? std::atol(e) : 0;
+    return v > 0 && v <= 160 ? (size_t)v * 1024 : kLdsBudget;
+  }();
+  return b;
+}
+
 struct LChoice {
   int T[3];      // wave tile (product 16 over the active axes)
   int W, sa;     // waves per workgroup and the axis they are stacked along
   int Em[3];     // workgroup key box (largest over tiles)
+  int sl;        // rank 3: box layers staged at a time (Em[0]: all at once)
   bool cpr1;     // every wave sub-box row is at most 16 keys wide
   bool ok;
 };
@@ -1113,14 +1160,19 @@ LChoice lean_choice(const Prob &P, bool bwd) {
       if (W > 1 && best.T[sa] >= (x.L + x.d - 1) / x.d) continue;
       int Em[3];
       for (int a = 0; a < 3; ++a) Em[a] = ext(a, best.T[a] * (a == sa ? W : 1));
-      const int ebox = lds_rows(R, Em);
-      size_t bytes = box_lds_bytes(ebox, P.D);
-      if (bytes > kLdsBudget) continue;
-      const double per_wave = (double)ebox / W;
-      if (per_wave < best_per_wave * 0.999) {
+      // rank 3 may stage the box a few layers (axis 0) at a time
+      int sl = Em[0];
+      while (sl > 1 && box_lds_bytes(lds_rows(R, Em) / Em[0] * sl, P.D) > lds_budget()) --sl;
+      const int ebox = lds_rows(R, Em) / Em[0] * sl;
+      if (box_lds_bytes(ebox, P.D) > lds_budget()) continue;
+      // staged rows per wave over all slabs; fewer slabs break ties
+      const double per_wave = (double)lds_rows(R, Em) / W;
+      if (per_wave < best_per_wave * 0.999 ||
+          (per_wave < best_per_wave * 1.001 && sl > best.sl)) {
         best_per_wave = per_wave;
         best.W = W;
         best.sa = sa;
+        best.sl = sl;
         for (int a = 0; a < 3; ++a) best.Em[a] = Em[a];
         best.ok = true;
       }
@@ -1162,7 +1214,8 @@ LProb make_lprob(const Prob &P, const LChoice &C) {
     y.fnt = make_fastdiv((uint32_t)y.nt);
     grid *= x.d * y.nt;
   }
-  L.ebox = lds_rows(P.rank, C.Em);
+  L.ebox = lds_rows(P.rank, C.Em) / C.Em[0] * C.sl;
+  L.sl = C.sl;
   L.lgP2 = P.rank == 1 ? 0 : ilog2c(C.Em[2]);
   L.fGrid = make_fastdiv((uint32_t)grid);
   L.n_tiles = P.B * P.H * grid;

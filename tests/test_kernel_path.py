@@ -1,7 +1,9 @@
 """Kernel selection (na_kernel_path, no GPU needed): which family each
 BASELINE configuration and each eligibility boundary dispatches to.  The
-lean workgroup kernels take the common problems; varlen, additional tokens
-and over-budget boxes stay on the 32-query matrix-core kernels; fp32, even
+lean workgroup kernels take the common problems (rank 3 staging its box a
+few layers at a time when it is too large for LDS); varlen, additional
+tokens and over-budget rank-1/2 boxes stay on the 32-query matrix-core
+kernels; fp32, even
 kernels and strides on the generic kernels."""
 
 import torch
@@ -23,8 +25,15 @@ def test_config2_runs_lean_both_ways():
             assert _path((4, 56, 56, 4, 32), 4, (7, 7), d, (False, False), backward=bwd) == "lean"
 
 
-def test_config3_box_exceeds_lds_budget():
-    assert _path((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False)) == "mfma"
+def test_config3_runs_lean_in_depth_slabs():
+    # the whole box exceeds the LDS budget; rank 3 stages it layer by layer
+    for bwd in (False, True):
+        assert _path((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False),
+                     backward=bwd) == "lean"
+
+
+def test_rank2_box_beyond_lds_budget_stays_on_mfma():
+    assert _path((1, 64, 64, 2, 128), 2, (31, 31), (1, 1), (False, False)) == "mfma"
 
 
 def test_lean_boundaries():
