@@ -380,7 +380,8 @@ def wl_cfg4(args):
     step_ms = _eager_ms(step, args)
     se = lens_d.reshape(Bc, 1).contiguous()
     f_ms = time_calls(lambda: hip.fused_forward(q, k, v, (63,), (1,), (2,), (False,), None,
-                                                extra_k=ak, extra_v=av, sample_extent=se),
+                                                extra_k=ak, extra_v=av, sample_extent=se,
+                                                varlen_clamped=True),
                       args.steps)
     tokens = int(lens.sum())
     flops = tokens * H * 4 * Dc * (63 + nx)

@@ -54,7 +54,13 @@ enum na_flags {
   NA_FLAG_GENERIC = 2,
   /* Run the 32-query matrix-core kernels where the lean workgroup kernels
    * would apply (A/B comparison; see na_kernel_path). */
-  NA_FLAG_NO_LEAN = 4
+  NA_FLAG_NO_LEAN = 4,
+  /* With sample_extent: the caller has checked that every sample extent
+   * satisfies dilation * kernel_size <= extent on each non-causal axis.
+   * Lets na_fwd run such problems on the lean kernels; a sample that breaks
+   * the promise gets wrong values in its rows (every memory access stays
+   * inside the tensors). */
+  NA_FLAG_VARLEN_CLAMPED = 8
 };
 
 /*

@@ -68,6 +68,7 @@ int make_prob(const na_params *p, na::Prob *P, bool allow_varlen) {
   P->n_extra = p->n_extra;
   P->dense = dense ? 1 : 0;
   P->sample_extent = p->sample_extent;
+  P->varlen_clamped = (p->flags & NA_FLAG_VARLEN_CLAMPED) != 0 ? 1 : 0;
   P->kprod = 1;
   const int lead = 3 - p->rank;
   for (int a = 0; a < 3; ++a) {
@@ -298,7 +299,8 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
   if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
     return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
   if (use_lean(p, P))
-    na::lean_fwd(P, p->dtype, q, k, v, out, lse, as_stream(stream));
+    na::lean_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
+                 as_stream(stream));
   else if (use_mfma(p, P))
     na::mfma_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
                  as_stream(stream));

@@ -165,6 +165,7 @@ struct Prob {
   int32_t dense;   // every query sees every key of its sample
   float scale;
   const int32_t *sample_extent;  // [B, rank] or nullptr
+  int32_t varlen_clamped;  // caller: d * K <= sample extent, non-causal axes
 };
 
 // Division by a divisor fixed at launch (round-up multiply method of

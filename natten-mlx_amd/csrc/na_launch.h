@@ -70,13 +70,14 @@ void mfma_bwd(const Prob &P, int dtype, const void *q, const void *k,
 void mfma_selftest(int dtype, float *out, hipStream_t st);
 
 // Lean matrix-core fused forward (na_lean.hip): the MFMA-eligible problems
-// with one extent per sample, no additional tokens, not dense, and d*K <= L
-// on every non-causal axis.
+// that are not dense, with d*K <= L on every non-causal axis (and d*K <= L_b
+// for every sample when per-sample extents are given, Prob::varlen_clamped).
 bool lean_eligible(const Prob &P, int dtype);
 void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
-              const void *v, void *out, float *lse, hipStream_t st);
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st);
 // Lean fused backward: one launch, no workspace (delta is computed in the
-// kernel); dlse may be null.
+// kernel); dlse may be null.  No additional tokens, one extent per sample.
 bool lean_bwd_eligible(const Prob &P, int dtype);
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *out, const float *lse,

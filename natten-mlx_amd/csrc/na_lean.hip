@@ -29,6 +29,7 @@
 // same LDS, dK/dV over the staged query box of the tile's keys.
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 #include "na_common.h"
 #include "na_launch.h"
@@ -87,6 +88,7 @@ struct LAx {
   int32_t tok;        // token stride of one position step along this axis
   FastDiv fG;         // tile-grid extent d * nt
   FastDiv fnt;        // nt
+  FastDiv fd;         // d (per-sample phase extents)
 };
 
 struct LProb {
@@ -105,6 +107,9 @@ struct LProb {
   FastDiv fHkv;       // key/value heads
   FastDiv fGrid;      // spatial tiles per (batch, head): prod of d * nt
   FastDiv fE1;        // rank 3: box row -> (e0, e1)
+  const int32_t *se;  // per-sample extents [B, rank] or nullptr
+  int32_t nx;         // additional key/value tokens per sample
+  int32_t nxr;        // their LDS rows (nx rounded up to 16), before the box
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -161,14 +166,19 @@ constexpr int kSlack = 16;
 struct LTile {
   int b, head, hk;
   int r[3], i0[3], nv[3], Lr[3];
+  int nvt[3];         // rows of the tensor (nv: rows of the sample)
   int lo[3], E[3];
   int kbase;          // element offset of box point (0,0,0), head hk
   int SK[3];          // element stride of one box step per axis (K/V)
 };
 
 // Origin of spatial tile `sp` (row-major over the per-axis grids d * nt):
-// phase, first sub-grid index and valid count per axis.
-template <int R>
+// phase, first sub-grid index and valid count per axis.  VX: sample t.b
+// has its own extent per axis (P.se); its phase extent Lr is then that of
+// the sample (on a non-causal axis at least K, so every window stays inside
+// the tensor whatever the extents hold), nv counts the sample's rows and
+// nvt the tensor's.
+template <int R, bool VX = false>
 __device__ __forceinline__ bool tile_origin(const LProb &P, uint32_t sp,
                                             LTile &t) {
   int g[3] = {0, 0, 0};
@@ -194,6 +204,13 @@ __device__ __forceinline__ bool tile_origin(const LProb &P, uint32_t sp,
     t.r[a] = rr;
     t.i0[a] = (g[a] - rr * x.nt) << x.lgTW;
     t.Lr[a] = x.Lq + (rr < x.Lrem ? 1 : 0);
+    t.nvt[a] = min(t.Lr[a] - t.i0[a], x.TW);
+    if (VX && P.se != nullptr) {
+      const int Lb = min(max(P.se[min(t.b, P.B - 1) * R + a - (3 - R)], 0), x.L);
+      const int lq = (int)fdiv((uint32_t)Lb, x.fd);
+      const int lr = lq + (rr < Lb - lq * x.d ? 1 : 0);
+      t.Lr[a] = x.causal ? lr : max(lr, x.K);
+    }
     t.nv[a] = min(t.Lr[a] - t.i0[a], x.TW);
     any = any & (t.nv[a] > 0);
   }
@@ -223,7 +240,7 @@ __device__ __forceinline__ void tile_box(const LProb &P, LTile &t, int head,
   t.kbase = (tok0 * heads + head) * P.D;
 }
 
-template <int R>
+template <int R, bool VX = false>
 __device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
                                             LTile &t) {
   // tiles at or beyond n_tiles decode to a batch index >= B
@@ -233,7 +250,7 @@ __device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
   t.head = (int)(rest - bq * P.fH.d);
   t.b = (int)bq;
   t.hk = (int)fdiv((uint32_t)t.head, P.fRep);
-  const bool any = tile_origin<R>(P, sp, t);
+  const bool any = tile_origin<R, VX>(P, sp, t);
   tile_box<R, false>(P, t, t.hk, P.Hkv);
   return any & (t.b < P.B);
 }
@@ -242,7 +259,7 @@ __device__ __forceinline__ bool decode_tile(const LProb &P, int tile,
 // stack axis) and the sub-box of the workgroup box their windows cover,
 // walked as rows (e0, e1) x column segments of 16 keys from ws2.
 struct WSub {
-  int i0[3], nv[3];
+  int i0[3], nv[3], nvt[3];
   int ws[3], we[3];
   int cpr, nchunks;
   bool any;
@@ -257,13 +274,14 @@ __device__ __forceinline__ WSub wave_sub(const LProb &P, const LTile &t,
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     if (a < 3 - R) {
-      s.i0[a] = 0; s.nv[a] = 1; s.ws[a] = 0; s.we[a] = 1;
+      s.i0[a] = 0; s.nv[a] = 1; s.nvt[a] = 1; s.ws[a] = 0; s.we[a] = 1;
       continue;
     }
     const LAx &x = P.ax[a];
     const int off = a == P.sa ? w * x.T : 0;
     s.i0[a] = t.i0[a] + off;
     s.nv[a] = min(t.nv[a] - off, x.T);
+    s.nvt[a] = min(t.nvt[a] - off, x.T);
     s.any = s.any & (s.nv[a] > 0);
     const int nvc = max(s.nv[a], 1);
     s.ws[a] = (INV ? iwstart(x, s.i0[a], t.Lr[a]) : wstart(x, s.i0[a], t.Lr[a])) -
@@ -435,17 +453,95 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
 // ---------------------------------------------------------------------------
 // Forward.  A workgroup of W waves owns W wave tiles stacked along the
 // stack axis; its K/V box is staged in LDS once, then each wave runs the
-// chunks of its own sub-box.  R: rank; CPR1: every wave sub-box row is one
-// chunk (at most 16 keys wide), so the per-lane column tests are fixed.
-template <typename T, int D, int R, bool CPR1>
+// chunks of its own sub-box.
+
+// One group of NB (even) chunks of 16 staged keys (first LDS rows kb[j]
+// from the bases ks / vs; sv[j] holds the chunk's mask as the score
+// accumulator's initial value): scores, online softmax update of (m, l, o)
+// and O^T += V^T . P^T.
+template <typename T, int D, int NB>
+__device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
+                                          const typename L16<T>::e *vs,
+                                          const int (&kb)[NB], f32x4 (&sv)[NB],
+                                          const typename L16<T>::v8 (&qf)[D / 32],
+                                          f32x4 (&o)[D / 16], float &m, float &l,
+                                          float sl2, int ka_off, int tr_off) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;    // 32-wide k-steps over head_dim
+  constexpr int NDB = D / 16;   // 16-row blocks of O^T
+  constexpr int RSE = lds_row(D);
+  v8 ka[NB][NT];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int st = 0; st < NT; ++st)
+      ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int st = 0; st < NT; ++st) sv[j] = M::mma(ka[j][st], qf[st], sv[j]);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][r]);
+  // ---- online softmax ----
+  mx = quad_max(mx) * sl2;
+  // The reference point m may trail the running max by up to 8 (a factor
+  // 2^8 in P): exact after the final division by l, and it spares the O
+  // rescale on groups that do not raise any query's max by more.
+  if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+    const float mn = fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+    l *= alpha;
+#pragma unroll
+    for (int j = 0; j < NDB; ++j) o[j] *= alpha;
+    m = mn;
+  }
+  const float mu = m == -INFINITY ? 0.f : m;
+  v8 bp[NB / 2];
+#pragma unroll
+  for (int jj = 0; jj < NB / 2; ++jj)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
+        l += p;
+        bp[jj][4 * h + r] = (E)p;
+      }
+  // ---- O^T += V^T . P^T, two chunks per MFMA ----
+#pragma unroll
+  for (int jj = 0; jj < NB / 2; ++jj) {
+    const E *ca = vs + kb[2 * jj] * RSE + tr_off;
+    const E *cb = vs + kb[2 * jj + 1] * RSE + tr_off;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const v4 lo4 = M::tr(ca + 16 * db);
+      const v4 hi4 = M::tr(cb + 16 * db);
+      const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[db] = M::mma(a, bp[jj], o[db]);
+    }
+  }
+}
+
+// R: rank; CPR1: every wave sub-box row is one chunk (at most 16 keys wide),
+// so the per-lane column tests are fixed.  VX: per-sample extents (P.se)
+// and/or additional tokens (P.nx rows per sample of ek / ev, staged in LDS
+// before the box and attended after it); query rows of the tensor outside
+// their sample's extent get zero output and lse 0.
+template <typename T, int D, int R, bool CPR1, bool VX>
 __global__ void __launch_bounds__(256)
     k_wfwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
-           const T *__restrict__ v, T *__restrict__ out,
+           const T *__restrict__ v, const T *__restrict__ ek,
+           const T *__restrict__ ev, T *__restrict__ out,
            float *__restrict__ lse) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
-  typedef typename M::v2 v2;
   typedef typename M::e E;
   constexpr int NT = D / 32;    // 32-wide k-steps over head_dim
   constexpr int NB = 256 / D;   // chunks per softmax group
@@ -456,13 +552,14 @@ __global__ void __launch_bounds__(256)
   // setup is straight-line arithmetic on kernel arguments (so their loads
   // issue together); the exit test comes after it
   LTile t;
-  const bool tile_any = decode_tile<R>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  const bool tile_any = decode_tile<R, VX>(P, xcd_tile(blockIdx.x, P.n_launch), t);
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, gq = lane >> 4;
   const WSub ws = wave_sub<R>(P, t, w);
 
-  // ---- the lane's query (column n of the score tiles) ----
+  // ---- the lane's query (column n of the score tiles): qv, inside its
+  // sample; qt, a row of the tensor (the two differ only when VX) ----
   int u[3];
   {
     const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
@@ -470,7 +567,7 @@ __global__ void __launch_bounds__(256)
     u[1] = (n >> lg2) & (P.ax[1].T - 1);
     u[0] = n >> (lg2 + lg1);
   }
-  bool qv = ws.any;
+  bool qv = ws.any, qt = t.b < P.B;
   int qtok = t.b * P.Ltot;
   int wl[3], ww[3];
 #pragma unroll
@@ -482,23 +579,58 @@ __global__ void __launch_bounds__(256)
     }
     const LAx &x = P.ax[a];
     qv = qv && u[a] < ws.nv[a];
-    const int i = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
-    qtok += (t.r[a] + x.d * i) * x.tok;
+    qt = qt && u[a] < ws.nvt[a];
+    // rows past the end (lanes of a partial wave tile, waves past the
+    // tile) take the tile's last row
+    const int i = min(ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0)),
+                      t.i0[a] + t.nv[a] - 1);
+    const int it = VX ? min(ws.i0[a] + min(u[a], max(ws.nvt[a] - 1, 0)),
+                            t.i0[a] + t.nvt[a] - 1)
+                      : i;
+    qtok += (t.r[a] + x.d * it) * x.tok;
     const int s = wstart(x, i, t.Lr[a]);
     wl[a] = s - t.lo[a];
     ww[a] = wend(x, i, t.Lr[a]) - s;
   }
   if (!qv) ww[2] = 0;
   const int qoff = (qtok * P.H + t.head) * D;
-  if (!tile_any) return;  // uniform over the workgroup
+  if (!tile_any) {  // uniform over the workgroup
+    if (VX && qt) {  // rows of the tensor outside the sample: zeros
+      v4 z;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (E)0.f;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = z;
+      if (lse != nullptr && gq == 0) lse[qoff / D] = 0.f;
+    }
+    return;
+  }
   v8 qf[NT];
 #pragma unroll
   for (int st = 0; st < NT; ++st) qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
 
-  // ---- the workgroup's K / V box to LDS, in slabs of P.sl layers along
-  // axis 0 for rank 3 (one slab otherwise) ----
-  E *ks = reinterpret_cast<E *>(smem);
+  // ---- LDS: additional tokens (VX) in rows [0, nxr), then the K / V box,
+  // staged in slabs of P.sl layers along axis 0 for rank 3 (one slab
+  // otherwise) ----
+  E *xk = reinterpret_cast<E *>(smem);
+  E *xv = xk + lds_y(D);
+  const int nxr = VX ? P.nxr : 0;
+  E *ks = xk + nxr * RSE;
   E *vs = ks + lds_y(D);
+  if (VX && nxr > 0) {
+    // rows past nx repeat the last token (finite; masked below)
+    constexpr int OCT = D / 8;
+    const int xrow0 = (t.b * P.nx * P.Hkv + t.hk) * D;
+    for (int uu = tid; uu < nxr * OCT; uu += nthr) {
+      const int e = uu / OCT, oo = uu % OCT;
+      const int g = xrow0 + min(e, P.nx - 1) * P.Hkv * D + 8 * oo;
+      const v8 a = ld8(ek, g);
+      const v8 b = ld8(ev, g);
+      *reinterpret_cast<v8 *>(xk + e * RSE + 8 * oo) = a;
+      *reinterpret_cast<v8 *>(xv + e * RSE + 8 * oo) = b;
+    }
+  }
 
   // column part of the mask of the lane's 4 keys per chunk (fixed when CPR1)
   float cb0[4];
@@ -516,6 +648,9 @@ __global__ void __launch_bounds__(256)
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
   const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
   const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  // additional-token chunks, run after the last slab's box chunks; their
+  // rows sit before the box (LDS rows -nxr .. -1 from ks)
+  const int nxc = VX ? nxr >> 4 : 0;
   for (int si = 0; si < nsl; ++si) {
     const int s0 = si * P.sl;
     if (si > 0) __syncthreads();  // the previous slab's reads are done
@@ -525,96 +660,56 @@ __global__ void __launch_bounds__(256)
     // the wave's box rows inside this slab
     const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
     const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
-    const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
-    const int ngroups = (nch + NB - 1) / NB;
+    const int nchb = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+    const int nch = nchb + (si == nsl - 1 ? nxc : 0);
     Cursor cc{a0, ws.ws[1], 0};
     const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
-    for (int grp = 0; grp < ngroups; ++grp) {
-      // ---- scores of the group: chunk rows, operand reads, MFMAs, masks ----
-      int kb[NB];       // first LDS row of each chunk
-      bool rok[NB];
-      int csj[NB];
-  #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const bool real = grp * NB + j < nch;
-        kb[j] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs : key0;
-        csj[j] = cc.cs;
-        bool ok = real;
+    // chunk rows and masks of a group of G chunks from chunk c0
+    auto group = [&](int c0, auto g_) {
+      constexpr int G = decltype(g_)::value;
+      int kb[G];        // first LDS row of each chunk
+      f32x4 sv[G];      // score accumulators, initialised with the mask
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const int c = c0 + j;
+        const bool box = c < nchb;
+        const bool ext = VX && !box && c < nch;
+        bool ok = box;
         if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
         if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
-        rok[j] = ok;
+        float cb[4];
+        if (CPR1 && !VX) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
+          kb[j] = box ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] : key0;
+        } else {
+          // extra chunk c - nchb: keys 16 (c - nchb) + 4 gq + r < nx
+          const int xc = 16 * (c - nchb);
+          col_bias(box ? ws.ws[2] + 16 * cc.cs + 4 * gq - wl[2] : xc + 4 * gq,
+                   box ? ww[2] : (qv ? P.nx : 0), cb);
+          kb[j] = box ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
+                      : ext ? xc - nxr : key0;
+          ok = ok || ext;
+        }
+        sv[j] = mask_init(ok, cb);
         advance(cc, ws);
       }
-      v8 ka[NB][NT];
-  #pragma unroll
-      for (int j = 0; j < NB; ++j)
-  #pragma unroll
-        for (int st = 0; st < NT; ++st)
-          ka[j][st] = *reinterpret_cast<const v8 *>(ks + kb[j] * RSE + ka_off + 32 * st);
-      f32x4 sv[NB];  // masked raw scores
-  #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        float cb[4];
-        if (CPR1) {
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
-        } else {
-          col_bias(ws.ws[2] + 16 * csj[j] + 4 * gq - wl[2], ww[2], cb);
-        }
-        sv[j] = mask_init(rok[j], cb);
-  #pragma unroll
-        for (int st = 0; st < NT; ++st) sv[j] = M::mma(ka[j][st], qf[st], sv[j]);
-      }
-      float mx = -INFINITY;
-  #pragma unroll
-      for (int j = 0; j < NB; ++j)
-  #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][r]);
-      // ---- online softmax ----
-      mx = quad_max(mx) * sl2;
-      // The reference point m may trail the running max by up to 8 (a factor
-      // 2^8 in P): exact after the final division by l, and it spares the O
-      // rescale on groups that do not raise any query's max by more.
-      if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
-        const float mn = fmaxf(m, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
-        l *= alpha;
-  #pragma unroll
-        for (int j = 0; j < NDB; ++j) o[j] *= alpha;
-        m = mn;
-      }
-      const float mu = m == -INFINITY ? 0.f : m;
-      v8 bp[NB / 2];
-  #pragma unroll
-      for (int jj = 0; jj < NB / 2; ++jj)
-  #pragma unroll
-        for (int h = 0; h < 2; ++h)
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
-            l += p;
-            bp[jj][4 * h + r] = (E)p;
-          }
-      // ---- O^T += V^T . P^T, two chunks per MFMA ----
-  #pragma unroll
-      for (int jj = 0; jj < NB / 2; ++jj) {
-        const E *ca = vs + kb[2 * jj] * RSE + tr_off;
-        const E *cb = vs + kb[2 * jj + 1] * RSE + tr_off;
-  #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const v4 lo4 = M::tr(ca + 16 * db);
-          const v4 hi4 = M::tr(cb + 16 * db);
-          const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[db] = M::mma(a, bp[jj], o[db]);
-        }
-      }
+      fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, l, sl2, ka_off, tr_off);
+    };
+    if constexpr (NB >= 4) {
+      int c0 = 0;
+      for (; c0 + NB / 2 < nch; c0 += NB) group(c0, std::integral_constant<int, NB>());
+      // a tail of at most NB / 2 chunks runs as a half group
+      if (c0 < nch) group(c0, std::integral_constant<int, NB / 2>());
+    } else {
+      for (int c0 = 0; c0 < nch; c0 += NB) group(c0, std::integral_constant<int, NB>());
     }
   }
 
   // ---- epilogue: sum l over the query's 4 lanes, normalise, store ----
   l = quad_sum(l);
-  if (!qv) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (!(VX ? qt : qv)) return;
+  const float inv = qv && l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
     v4 wv;
@@ -623,7 +718,7 @@ __global__ void __launch_bounds__(256)
     *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = wv;
   }
   if (lse != nullptr && gq == 0)
-    lse[qoff / D] = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+    lse[qoff / D] = !qv ? 0.f : l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -711,7 +806,9 @@ __device__ __forceinline__ int lane_rows(const LProb &P, const LTile &t,
     }
     const LAx &x = P.ax[a];
     valid = valid && u[a] < ws.nv[a];
-    const int i = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
+    // rows past the end take the tile's last row
+    const int i = min(ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0)),
+                      t.i0[a] + t.nv[a] - 1);
     tok += (t.r[a] + x.d * i) * x.tok;
     const int s0 = INV ? iwstart(x, i, t.Lr[a]) : wstart(x, i, t.Lr[a]);
     const int s1 = INV ? iwend(x, i, t.Lr[a]) : wend(x, i, t.Lr[a]);
@@ -921,7 +1018,8 @@ __global__ void __launch_bounds__(256)
       }
       const LAx &x = P.ax[a];
       kv = kv && u[a] < ws.nv[a];
-      const int j = ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0));
+      const int j = min(ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0)),
+                        t.i0[a] + t.nv[a] - 1);
       tok += (t.r[a] + x.d * j) * x.tok;
       const int s0 = iwstart(x, j, t.Lr[a]);
       wl[a] = s0 - t.lo[a];
@@ -1081,8 +1179,11 @@ int lds_rows(int R, const int Em[3]) {
   return Em[0] * Em[1] * p2;
 }
 
-size_t box_lds_bytes(int ebox, int D) {
-  return (size_t)(ebox + kSlack) * lds_row(D) * 2;
+// LDS rows of the additional tokens (forward): n_extra rounded up to 16.
+int lean_nxr(const Prob &P) { return (P.n_extra + 15) & ~15; }
+
+size_t box_lds_bytes(int ebox, int D, int nxr) {
+  return (size_t)(nxr + ebox + kSlack) * lds_row(D) * 2;
 }
 
 // Host twins of the window rules.
@@ -1123,13 +1224,20 @@ int box_max(const Axis &x, int t, bool inverse) {
 // holds a (lse, delta) pair per staged row.
 LChoice lean_choice(const Prob &P, bool bwd) {
   const int R = P.rank, lead = 3 - R;
+  const int nxr = bwd ? 0 : lean_nxr(P);
   LChoice best{};
   best.ok = false;
   double best_cost = 1e300;
   auto ext = [&](int a, int t) {
     if (a < lead) return 1;
-    const int f = box_max(P.ax[a], t, false);
-    return bwd ? std::max(f, box_max(P.ax[a], t, true)) : f;
+    const Axis &x = P.ax[a];
+    if (P.sample_extent != nullptr) {
+      // any sample: a box spans at most t + K - 1 points of a phase no
+      // longer than the tensor's
+      return std::min((x.L + x.d - 1) / x.d, t + x.K - 1);
+    }
+    const int f = box_max(x, t, false);
+    return bwd ? std::max(f, box_max(x, t, true)) : f;
   };
   for (int l0 = 0; l0 <= 4; ++l0)
     for (int l1 = 0; l0 + l1 <= 4; ++l1) {
@@ -1162,9 +1270,10 @@ LChoice lean_choice(const Prob &P, bool bwd) {
       for (int a = 0; a < 3; ++a) Em[a] = ext(a, best.T[a] * (a == sa ? W : 1));
       // rank 3 may stage the box a few layers (axis 0) at a time
       int sl = Em[0];
-      while (sl > 1 && box_lds_bytes(lds_rows(R, Em) / Em[0] * sl, P.D) > lds_budget()) --sl;
+      while (sl > 1 && box_lds_bytes(lds_rows(R, Em) / Em[0] * sl, P.D, nxr) > lds_budget())
+        --sl;
       const int ebox = lds_rows(R, Em) / Em[0] * sl;
-      if (box_lds_bytes(ebox, P.D) > lds_budget()) continue;
+      if (box_lds_bytes(ebox, P.D, nxr) > lds_budget()) continue;
       // staged rows per wave over all slabs; fewer slabs break ties
       const double per_wave = (double)lds_rows(R, Em) / W;
       if (per_wave < best_per_wave * 0.999 ||
@@ -1212,6 +1321,7 @@ LProb make_lprob(const Prob &P, const LChoice &C) {
     tok *= x.L;
     y.fG = make_fastdiv((uint32_t)(x.d * y.nt));
     y.fnt = make_fastdiv((uint32_t)y.nt);
+    y.fd = make_fastdiv((uint32_t)x.d);
     grid *= x.d * y.nt;
   }
   L.ebox = lds_rows(P.rank, C.Em) / C.Em[0] * C.sl;
@@ -1226,6 +1336,9 @@ LProb make_lprob(const Prob &P, const LChoice &C) {
   L.rep = P.rep;
   L.scale = P.scale;
   L.fHkv = make_fastdiv((uint32_t)P.Hkv);
+  L.se = P.sample_extent;
+  L.nx = P.n_extra;
+  L.nxr = lean_nxr(P);
   return L;
 }
 
@@ -1243,7 +1356,10 @@ bool lean_eligible(const Prob &P, int dtype) {
   if (lean_disabled()) return false;
   if (dtype != NA_BF16 && dtype != NA_F16) return false;
   if (P.D != 32 && P.D != 64 && P.D != 128) return false;
-  if (P.dense || P.n_extra > 0 || P.sample_extent != nullptr) return false;
+  if (P.dense) return false;
+  // per-sample extents only when the caller states that every one of them
+  // satisfies d * K <= L_b on each non-causal axis
+  if (P.sample_extent != nullptr && !P.varlen_clamped) return false;
   if (!(P.scale > 0.f) || !std::isfinite(P.scale)) return false;
   for (int a = 0; a < 3; ++a) {
     const Axis &x = P.ax[a];
@@ -1254,6 +1370,7 @@ bool lean_eligible(const Prob &P, int dtype) {
   const int64_t elems = (int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L *
                         std::max(P.H, P.Hkv) * P.D;
   if (elems >= (int64_t(1) << 31)) return false;
+  if ((int64_t)P.B * P.n_extra * P.Hkv * P.D >= (int64_t(1) << 31)) return false;
   // per-axis element strides fit the 24-bit multiplies of the staging code
   int64_t tok = 1;
   for (int a = 2; a >= 0; --a) {
@@ -1265,7 +1382,9 @@ bool lean_eligible(const Prob &P, int dtype) {
 }
 
 bool lean_bwd_eligible(const Prob &P, int dtype) {
-  return lean_eligible(P, dtype) && lean_choice(P, true).ok;
+  // additional tokens and per-sample extents: forward only
+  return P.n_extra == 0 && P.sample_extent == nullptr && lean_eligible(P, dtype) &&
+         lean_choice(P, true).ok;
 }
 
 #define LEAN_D(D_, BODY) \
@@ -1280,15 +1399,23 @@ bool lean_bwd_eligible(const Prob &P, int dtype) {
   } while (0)
 
 void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
-              const void *v, void *out, float *lse, hipStream_t st) {
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st) {
   const LChoice C = lean_choice(P, false);
   const LProb L = make_lprob(P, C);
   if (L.n_tiles == 0) return;
-  const size_t lds = box_lds_bytes(L.ebox, P.D);
+  const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
+  const size_t lds = box_lds_bytes(L.ebox, P.D, vx ? L.nxr : 0);
   const dim3 grid(L.n_launch), block(64 * C.W);
+#define LF_LAUNCH1(TT, DD, RR, CC, VV)                                          \
+  hipLaunchKernelGGL((k_wfwd<TT, DD, RR, CC, VV>), grid, block, lds, st, L,     \
+                     (const TT *)q, (const TT *)k, (const TT *)v,              \
+                     (const TT *)ek, (const TT *)ev, (TT *)out, lse)
 #define LF_LAUNCH(TT, DD, RR, CC)                                              \
-  hipLaunchKernelGGL((k_wfwd<TT, DD, RR, CC>), grid, block, lds, st, L,        \
-                     (const TT *)q, (const TT *)k, (const TT *)v, (TT *)out, lse)
+  do {                                                                        \
+    if (vx) LF_LAUNCH1(TT, DD, RR, CC, true);                                 \
+    else LF_LAUNCH1(TT, DD, RR, CC, false);                                   \
+  } while (0)
 #define LF_R(TT, DD)                                                          \
   do {                                                                        \
     if (P.rank == 1) LF_LAUNCH(TT, DD, 1, false);                             \
@@ -1307,6 +1434,7 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef LF_D
 #undef LF_R
 #undef LF_LAUNCH
+#undef LF_LAUNCH1
 }
 
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
@@ -1319,7 +1447,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
   L.n_tiles = P.B * P.Hkv * grid_sp;
   L.n_launch = (L.n_tiles + 7) & ~7;
   if (L.n_tiles == 0) return;
-  const size_t lds = box_lds_bytes(L.ebox, P.D);
+  const size_t lds = box_lds_bytes(L.ebox, P.D, 0);
   const dim3 grid(L.n_launch), block(64 * C.W);
 #define LB_LAUNCH(TT, DD, RR, CC)                                              \
   hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC>), grid, block, lds, st, L,        \

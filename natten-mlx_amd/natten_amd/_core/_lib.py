@@ -22,6 +22,7 @@ NA_F32, NA_F16, NA_BF16 = 0, 1, 2
 NA_FLAG_DENSE = 1
 NA_FLAG_GENERIC = 2
 NA_FLAG_NO_LEAN = 4
+NA_FLAG_VARLEN_CLAMPED = 8
 ABI_VERSION = 2
 
 _STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "launch failure",

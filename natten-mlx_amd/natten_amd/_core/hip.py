@@ -82,14 +82,16 @@ def _scale(scale, head_dim: int) -> float:
 
 def _params(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_causal, scale,
             n_extra: int = 0, dense: bool = False,
-            sample_extent: Optional[torch.Tensor] = None) -> _lib.NaParams:
+            sample_extent: Optional[torch.Tensor] = None,
+            varlen_clamped: bool = False) -> _lib.NaParams:
     rank = q.dim() - 3
     return _lib.make_params(
         rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
         tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
         tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra,
         (_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0)
-        | (_lib.NA_FLAG_NO_LEAN if _no_lean else 0),
+        | (_lib.NA_FLAG_NO_LEAN if _no_lean else 0)
+        | (_lib.NA_FLAG_VARLEN_CLAMPED if varlen_clamped and sample_extent is not None else 0),
         sample_extent)
 
 
@@ -102,14 +104,16 @@ def _out_spatial(spatial: Sequence[int], stride: Sequence[int]) -> tuple[int, ..
 
 def fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale,
                   extra_k=None, extra_v=None, sample_extent=None, dense=False,
-                  want_lse=True):
-    """Returns ``(out, lse)``; lse is float32 ``[B, *O, H]`` (or None)."""
+                  want_lse=True, varlen_clamped=False):
+    """Returns ``(out, lse)``; lse is float32 ``[B, *O, H]`` (or None).
+    ``varlen_clamped``: the caller has checked that every sample extent is at
+    least dilation * kernel_size on each non-causal axis."""
     _require_device(q, k, v, extra_k, extra_v, sample_extent)
     q, k, v, extra_k, extra_v = map(_c, (q, k, v, extra_k, extra_v))
     lib = _lib.load()
     n_extra = 0 if extra_k is None else extra_k.shape[1]
     p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
-                sample_extent)
+                sample_extent, varlen_clamped)
     osp = _out_spatial(q.shape[1:-2], stride)
     B, H, D = q.shape[0], q.shape[-2], q.shape[-1]
     out = torch.empty((B, *osp, H, D), dtype=q.dtype, device=q.device)
@@ -124,12 +128,12 @@ KERNEL_PATHS = {0: "generic", 1: "mfma", 2: "lean"}
 
 
 def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_extra=0,
-                dense=False, sample_extent=None, backward=False):
+                dense=False, sample_extent=None, backward=False, varlen_clamped=False):
     """Name of the kernel family na_fwd (or na_bwd) runs for this problem:
     "generic", "mfma" or "lean" (a diagnostic; launches nothing)."""
     lib = _lib.load()
     p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
-                sample_extent)
+                sample_extent, varlen_clamped)
     r = int(lib.na_kernel_path(p, 1 if backward else 0))
     if r < 0:
         _lib.check(-r, "na_kernel_path")

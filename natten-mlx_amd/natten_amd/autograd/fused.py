@@ -23,6 +23,9 @@ class FusedSpec(NamedTuple):
     is_causal: tuple
     scale: Optional[float]
     dense: bool = False
+    # every per-sample extent satisfies dilation * kernel_size <= extent on
+    # each non-causal axis (checked by the caller on the host)
+    varlen_clamped: bool = False
 
 
 class _FusedNA(torch.autograd.Function):
@@ -31,7 +34,8 @@ class _FusedNA(torch.autograd.Function):
         be = ops.backend_module()
         out, lse = be.fused_forward(q, k, v, spec.kernel_size, spec.stride, spec.dilation,
                                     spec.is_causal, spec.scale, extra_k, extra_v,
-                                    sample_extent, spec.dense)
+                                    sample_extent, spec.dense,
+                                    varlen_clamped=spec.varlen_clamped)
         ctx.save_for_backward(q, k, v, extra_k, extra_v, out, lse, sample_extent)
         ctx.spec = spec
         ctx.set_materialize_grads(False)
@@ -79,8 +83,11 @@ def na3d_with_grad(q, k, v, kernel_size, stride, dilation, is_causal, scale):
 
 def _varlen(q, k, v, sizes, kernel_size, dilation, scale):
     rank = q.dim() - 3
+    host = sizes.detach().to("cpu", torch.int64).reshape(q.shape[0], rank)
+    clamped = bool((host >= torch.tensor([d * kk for d, kk in zip(dilation, kernel_size)])).all())
     se = sizes.to(device=q.device, dtype=torch.int32).reshape(q.shape[0], rank).contiguous()
-    spec = FusedSpec(tuple(kernel_size), (1,) * rank, tuple(dilation), (False,) * rank, scale)
+    spec = FusedSpec(tuple(kernel_size), (1,) * rank, tuple(dilation), (False,) * rank, scale,
+                     varlen_clamped=clamped)
     return na_fused_with_grad(q, k, v, spec, sample_extent=se)[0]
 
 

@@ -353,7 +353,7 @@ def na1d_varlen_gqa(query, key, value, seq_lens, kernel_size, dilation=1, scale=
         raise ValueError(f"All seq_lens must be >= dilation * kernel_size ({dil[0] * ks[0]}).")
     scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
     se = seq_lens.to(device=query.device, dtype=torch.int32).reshape(B, 1).contiguous()
-    spec = FusedSpec(tuple(ks), (1,), tuple(dil), (False,), scale_value)
+    spec = FusedSpec(tuple(ks), (1,), tuple(dil), (False,), scale_value, varlen_clamped=True)
     out, lse = na_fused_with_grad(query, key.to(query.dtype), value.to(query.dtype), spec,
                                   add_k, add_v, sample_extent=se)
     return (out, lse) if return_lse else out
