@@ -129,9 +129,10 @@ int na_mfma_selftest(int32_t dtype, float *out, void *stream);
 
 /*
  * Diagnostic with no counterpart in the reference: the kernel family that
- * na_fwd (backward = 0) or na_bwd (backward = 1) runs for these parameters,
- * one of na_kernel_path_t, or the negated na_status of invalid parameters.
- * Launches nothing and reads no device memory.
+ * na_fwd (backward = 0), na_bwd (backward = 1) or the split ops na_qk_fwd /
+ * na_av_fwd / na_qk_bwd / na_av_bwd (backward = 2) run for these
+ * parameters, one of na_kernel_path_t, or the negated na_status of invalid
+ * parameters.  Launches nothing and reads no device memory.
  */
 enum na_kernel_path_t {
   NA_PATH_GENERIC = 0, /* vector-ALU kernels: every dtype / head_dim / stride */

@@ -127,6 +127,11 @@ bool use_lean_bwd(const na_params *p, const na::Prob &P) {
          na::lean_bwd_eligible(P, p->dtype);
 }
 
+bool use_lsplit(const na_params *p, const na::Prob &P) {
+  return (p->flags & (NA_FLAG_GENERIC | NA_FLAG_NO_LEAN)) == 0 &&
+         na::lsplit_eligible(P, p->dtype);
+}
+
 bool use_msplit(const na_params *p, const na::Prob &P) {
   return (p->flags & NA_FLAG_GENERIC) == 0 && na::msplit_eligible(P, p->dtype);
 }
@@ -268,8 +273,13 @@ int na_mfma_selftest(int32_t dtype, float *out, void *stream) {
 
 int na_kernel_path(const na_params *p, int32_t backward) {
   na::Prob P;
-  const int rc = make_prob(p, &P, true);
+  const int rc = make_prob(p, &P, backward != 2);
   if (rc != NA_OK) return -rc;
+  if (backward == 2) {
+    if (use_lsplit(p, P)) return NA_PATH_LEAN;
+    if (use_msplit(p, P)) return NA_PATH_MFMA;
+    return NA_PATH_GENERIC;
+  }
   if (backward ? use_lean_bwd(p, P) : use_lean(p, P)) return NA_PATH_LEAN;
   if (use_mfma(p, P)) return NA_PATH_MFMA;
   return NA_PATH_GENERIC;
@@ -365,7 +375,10 @@ int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,
   if (P.B == 0) return NA_OK;
   if (q == nullptr || k == nullptr || logits == nullptr)
     return fail(NA_ERR_INVALID, "q/k/logits must be non-NULL");
-  if (use_msplit(p, P))
+  if (use_lsplit(p, P))
+    na::lsplit_qk(P, p->dtype, q, k, logits, P.scale, -INFINITY,
+                  as_stream(stream));
+  else if (use_msplit(p, P))
     na::msplit_qk(P, p->dtype, q, k, logits, P.scale, -INFINITY,
                   as_stream(stream));
   else
@@ -382,7 +395,9 @@ int na_av_fwd(const na_params *p, const void *attn, const void *v, void *out,
   if (P.B == 0) return NA_OK;
   if (attn == nullptr || v == nullptr || out == nullptr)
     return fail(NA_ERR_INVALID, "attn/v/out must be non-NULL");
-  if (use_msplit(p, P))
+  if (use_lsplit(p, P))
+    na::lsplit_av(P, p->dtype, attn, v, out, 1.f, as_stream(stream));
+  else if (use_msplit(p, P))
     na::msplit_av(P, p->dtype, attn, v, out, 1.f, as_stream(stream));
   else
     na::valu_av(P, p->dtype, attn, v, out, as_stream(stream));
@@ -399,7 +414,10 @@ int na_qk_bwd(const na_params *p, const void *q, const void *k,
   if (q == nullptr || k == nullptr || dlogits == nullptr || dq == nullptr ||
       dk == nullptr)
     return fail(NA_ERR_INVALID, "q/k/dlogits/dq/dk must be non-NULL");
-  if (use_msplit(p, P)) {
+  if (use_lsplit(p, P)) {
+    na::lsplit_av(P, p->dtype, dlogits, k, dq, P.scale, as_stream(stream));
+    na::lsplit_inv(P, p->dtype, dlogits, q, dk, P.scale, as_stream(stream));
+  } else if (use_msplit(p, P)) {
     na::msplit_av(P, p->dtype, dlogits, k, dq, P.scale, as_stream(stream));
     na::msplit_inv(P, p->dtype, dlogits, q, dk, P.scale, as_stream(stream));
   } else {
@@ -418,7 +436,10 @@ int na_av_bwd(const na_params *p, const void *attn, const void *v,
   if (attn == nullptr || v == nullptr || dout == nullptr || dattn == nullptr ||
       dv == nullptr)
     return fail(NA_ERR_INVALID, "attn/v/dout/dattn/dv must be non-NULL");
-  if (use_msplit(p, P)) {
+  if (use_lsplit(p, P)) {
+    na::lsplit_qk(P, p->dtype, dout, v, dattn, 1.f, 0.f, as_stream(stream));
+    na::lsplit_inv(P, p->dtype, attn, dout, dv, 1.f, as_stream(stream));
+  } else if (use_msplit(p, P)) {
     na::msplit_qk(P, p->dtype, dout, v, dattn, 1.f, 0.f, as_stream(stream));
     na::msplit_inv(P, p->dtype, attn, dout, dv, 1.f, as_stream(stream));
   } else {

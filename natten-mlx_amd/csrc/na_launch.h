@@ -84,6 +84,20 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *dout, const float *dlse, void *dq, void *dk,
               void *dv, hipStream_t st);
 
+// Lean split ops (na_lsplit.hip): the lean problem class without varlen,
+// additional tokens or dense mode, where the compact rows fit LDS.
+// lsplit_qk: out[q, slot] = scale * <x_q, y_key(slot)> (fill outside the
+// window); lsplit_av: out_q = scale * sum_slot a[q, slot] * y_key(slot);
+// lsplit_inv: z_key = scale * sum over queries q holding the key (all query
+// heads of its group) of a[q, slot(q, key)] * x_q.
+bool lsplit_eligible(const Prob &P, int dtype);
+void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
+               void *out, float scale, float fill, hipStream_t st);
+void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
+               void *out, float scale, hipStream_t st);
+void lsplit_inv(const Prob &P, int dtype, const void *a, const void *x,
+                void *z, float scale, hipStream_t st);
+
 // Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with
 // d*K <= L on every non-causal axis and at most 512 kernel slots.
 bool msplit_eligible(const Prob &P, int dtype);

@@ -1,0 +1,567 @@
+// na_lsplit.hip — lean matrix-core (gfx950) kernels for the split ops
+// (na_qk_fwd / na_av_fwd and their backward) on the lean problem class
+// (bf16/fp16, head_dim 32/64/128, stride 1, odd K with d*K <= L on every
+// non-causal axis, no varlen, no additional tokens):
+//
+//   k_lqk  : out[q, slot] = scale * <x_q, y_key(slot)>, `fill` in the slots
+//            outside the window (qk forward: x = q, y = k; av backward's
+//            dattn: x = dO, y = v)
+//   k_lav  : out_q = scale * sum over slots of a[q, slot] * y_key(slot)
+//            (av forward: a = attn, y = v; qk backward's dq: a = dlogits,
+//            y = k)
+//   k_linv : z_key = scale * sum over the query heads of the key's group and
+//            the queries q whose windows hold the key of
+//            a[q, slot(q, key)] * x_q (qk backward's dk: a = dlogits,
+//            x = q; av backward's dv: a = attn, x = dO)
+//
+// The tiling is the fused kernels' (na_lean.h): a wave owns 16 queries (or
+// keys) of one dilation phase, W waves stacked along one axis form a
+// workgroup, and the workgroup stages the box of rows its waves' windows
+// cover in LDS once, here one tensor per row (row stride D + 8 elements).
+// Each wave walks its sub-box in chunks of 16 rows through the MFMA; the
+// compact rows [kprod] of the workgroup's queries pass through LDS and move
+// to or from HBM a row at a time; k_linv gathers them from HBM instead
+// (every element is used by exactly one key).
+//
+// Slot of key j in the window of query i: per axis (sub-grid coordinates)
+// j - s(i) with s(i) = wend(i) - K, i.e. the window start on a non-causal
+// axis and i - K + 1 on a causal one; slots are row-major over the axes
+// (strides K1 K2, K2, 1), so slot = sum_a j_a st_a - sum_a s_a(i) st_a.
+#include "na_lean.h"
+
+namespace na {
+namespace {
+
+// Stage a workgroup's box of rows of one tensor into LDS: box point (e0, e1,
+// e2) at layout row ((e0 * Em1 + e1) << lgP2) + e2 (rank 1: e2), element
+// row * (D + 8); layout points past the tile's true box are clamped onto it.
+// The kSlack rows after the box are zeroed.
+template <typename T, int D, int R>
+__device__ __forceinline__ void stage_box1(const LProb &P, const LTile &t,
+                                           const T *__restrict__ x,
+                                           typename L16<T>::e *xs, int tid,
+                                           int nthr, int s0) {
+  typedef typename L16<T>::v8 v8;
+  constexpr int OCT = D / 8;  // 16-byte units per row
+  constexpr int RS = lds_y(D);
+  const int nun = P.ebox * OCT;
+  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
+    v8 xr[4];
+    int la[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = min(u0 + j * nthr + tid, nun - 1);
+      const int kk = u / OCT, o = u % OCT;
+      xr[j] = ld8(x, unit_offset<R>(P, t, kk, o, s0));
+      la[j] = kk * RS + 8 * o;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<v8 *>(xs + la[j]) = xr[j];
+  }
+  constexpr int SLU = kSlack * RS / 8;
+  for (int u = tid; u < SLU; u += nthr) {
+    v8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (typename L16<T>::e)0.f;
+    *reinterpret_cast<v8 *>(xs + P.ebox * RS + 8 * u) = z;
+  }
+}
+
+// The lane's row (query for k_lqk / k_lav, key for k_linv) of wave tile w:
+// validity, element offset of the row (`heads` heads of head_dim D), its
+// window (INV: inverse window) relative to the tile box, [wl, wl + ww) per
+// axis (ww = 0 on every axis for rows outside the tensor), and its absolute
+// sub-grid coordinates.
+template <int R, bool INV>
+__device__ __forceinline__ int lane_row(const LProb &P, const LTile &t,
+                                        const WSub &ws, int n, int head,
+                                        int heads, bool &valid, int wl[3],
+                                        int ww[3], int idx[3]) {
+  int u[3];
+  const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+  u[2] = n & (P.ax[2].T - 1);
+  u[1] = (n >> lg2) & (P.ax[1].T - 1);
+  u[0] = n >> (lg2 + lg1);
+  valid = ws.any;
+  int tok = t.b * P.Ltot;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (a < 3 - R) {
+      wl[a] = 0;
+      ww[a] = 1;
+      idx[a] = 0;
+      continue;
+    }
+    const LAx &x = P.ax[a];
+    valid = valid && u[a] < ws.nv[a];
+    // rows past the end take the tile's last row
+    const int i = min(ws.i0[a] + min(u[a], max(ws.nv[a] - 1, 0)),
+                      t.i0[a] + t.nv[a] - 1);
+    tok += (t.r[a] + x.d * i) * x.tok;
+    const int s0 = INV ? iwstart(x, i, t.Lr[a]) : wstart(x, i, t.Lr[a]);
+    const int s1 = INV ? iwend(x, i, t.Lr[a]) : wend(x, i, t.Lr[a]);
+    wl[a] = s0 - t.lo[a];
+    ww[a] = s1 - s0;
+    idx[a] = i;
+  }
+  if (!valid) ww[2] = 0;
+  return tok * heads + head;
+}
+
+// Chunk j of a group: first LDS row, row test and the coordinates the slot
+// arithmetic needs (box-relative e0, e1 and the first column).
+struct ChunkPos {
+  int kb;      // first LDS row
+  bool rok;    // real chunk whose row lies in the lane's window
+  int e0, e1;  // box coordinates of the chunk's row
+  int e01;     // e0 * kst0 + e1 * kst1
+  int col;     // box column of the chunk's first row
+};
+
+template <int R>
+__device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
+                                              Cursor &cc, bool real, int s0,
+                                              int key0, const int wl[3],
+                                              const int ww[3]) {
+  ChunkPos c;
+  c.kb = real ? (((cc.e0 - s0) * P.ax[1].Em + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
+              : key0;
+  bool ok = real;
+  if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+  if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+  c.rok = ok;
+  c.e0 = cc.e0;
+  c.e1 = cc.e1;
+  c.e01 = cc.e0 * P.kst0 + cc.e1 * P.kst1;
+  c.col = ws.ws[2] + 16 * cc.cs;
+  advance(cc, ws);
+  return c;
+}
+
+// ---------------------------------------------------------------------------
+// k_lqk.  Per chunk S^T = Y_chunk . X^T (lane l: query l % 16, keys
+// 4 (l / 16) + r), each in-window score to its slot of the query's row in
+// LDS; then the rows to HBM.  FILL: some slots lie outside every window
+// (a causal axis) and start as `fill`.
+template <typename T, int D, int R, bool CPR1>
+__global__ void __launch_bounds__(256)
+    k_lqk(LProb P, const T *__restrict__ x, const T *__restrict__ y,
+          T *__restrict__ out, float scale, float fill, int prefill) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;
+  constexpr int NB = 256 / D;  // chunks whose operands are read together
+  constexpr int RS = lds_y(D);
+  extern __shared__ __align__(16) char smem[];
+
+  LTile t;
+  const bool tile_any = decode_tile<R>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  const WSub ws = wave_sub<R>(P, t, w);
+  bool qv;
+  int wl[3], ww[3], qi[3];
+  const int qrow = lane_row<R, false>(P, t, ws, n, t.head, P.H, qv, wl, ww, qi);
+  // slot base of the lane's query (box-relative s_a = wl + ww - K)
+  const int sq = (R == 3 ? (wl[0] + ww[0] - P.ax[0].K) * P.kst0 : 0) +
+                 (R >= 2 ? (wl[1] + ww[1] - P.ax[1].K) * P.kst1 : 0) +
+                 (wl[2] + (qv ? ww[2] : P.ax[2].K) - P.ax[2].K);
+  if (!tile_any) return;  // uniform over the workgroup
+  v8 qf[NT];
+#pragma unroll
+  for (int st = 0; st < NT; ++st) qf[st] = ld8(x, qrow * D + 32 * st + 8 * gq);
+
+  E *ys = reinterpret_cast<E *>(smem);
+  E *ob = ys + align16((P.ebox + kSlack) * RS * 2) / 2;
+  const int kp = P.kp;
+  if (prefill) {
+    for (int i = tid; i < 16 * (nthr >> 6) * kp; i += nthr) ob[i] = (E)fill;
+  }
+  E *mine = ob + (16 * w + n) * kp;
+  const int ka_off = n * RS + 8 * gq;
+  const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  for (int si = 0; si < nsl; ++si) {
+    const int s0 = si * P.sl;
+    if (si > 0) __syncthreads();  // the previous slab's reads are done
+    stage_box1<T, D, R>(P, t, y, ys, tid, nthr, s0);
+    __syncthreads();
+    if (!ws.any) continue;
+    const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+    const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+    const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+    Cursor cc{a0, ws.ws[1], 0};
+    const int key0 = (((a0 - s0) * P.ax[1].Em + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    for (int c0 = 0; c0 < nch; c0 += NB) {
+      ChunkPos cp[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+      v8 ka[NB][NT];
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+          ka[j][st] = *reinterpret_cast<const v8 *>(ys + cp[j].kb * RS + ka_off + 32 * st);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        f32x4 sv = zero4();
+#pragma unroll
+        for (int st = 0; st < NT; ++st) sv = M::mma(ka[j][st], qf[st], sv);
+        const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
+          if (ok) mine[cp[j].e01 + xc + r - sq] = (E)(sv[r] * scale);
+        }
+      }
+    }
+  }
+  // the wave's 16 rows (written by this wave only) to HBM, four at a time
+  wave_lds_sync();
+  const uint64_t vb = __builtin_amdgcn_ballot_w64(qv);
+  E *oe = reinterpret_cast<E *>(out);
+  for (int p0 = 0; p0 < 16; p0 += 4) {
+    for (int s = lane; s < kp; s += 64) {
+      E vals[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vals[j] = ob[(16 * w + p0 + j) * kp + s];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = __builtin_amdgcn_readlane(qrow, p0 + j);
+        if ((vb >> (p0 + j)) & 1) oe[row * kp + s] = vals[j];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_lav.  The wave's 16 compact rows to LDS; per pair of chunks the B
+// operand (query n, keys 4 (l / 16) + r of each chunk) is gathered from them
+// by slot (zero outside the window) and O^T += Y^T . A^T with Y^T through
+// the transposing LDS read.
+template <typename T, int D, int R, bool CPR1>
+__global__ void __launch_bounds__(256)
+    k_lav(LProb P, const T *__restrict__ a, const T *__restrict__ y,
+          T *__restrict__ out, float scale) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int NB = D == 128 ? 2 : 4;  // chunks read together
+  constexpr int NDB = D / 16;
+  constexpr int RS = lds_y(D);
+  extern __shared__ __align__(16) char smem[];
+
+  LTile t;
+  const bool tile_any = decode_tile<R>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  const WSub ws = wave_sub<R>(P, t, w);
+  bool qv;
+  int wl[3], ww[3], qi[3];
+  const int qrow = lane_row<R, false>(P, t, ws, n, t.head, P.H, qv, wl, ww, qi);
+  const int sq = (R == 3 ? (wl[0] + ww[0] - P.ax[0].K) * P.kst0 : 0) +
+                 (R >= 2 ? (wl[1] + ww[1] - P.ax[1].K) * P.kst1 : 0) +
+                 (wl[2] + (qv ? ww[2] : P.ax[2].K) - P.ax[2].K);
+  if (!tile_any) return;  // uniform over the workgroup
+
+  E *ys = reinterpret_cast<E *>(smem);
+  E *ab = ys + align16((P.ebox + kSlack) * RS * 2) / 2;
+  const int kp = P.kp;
+  // the wave's 16 compact rows, all loads in flight together (issued
+  // before the box staging)
+  const uint64_t vb = __builtin_amdgcn_ballot_w64(qv);
+  const E *ae = reinterpret_cast<const E *>(a);
+  for (int s0 = 0; s0 < kp; s0 += 64) {
+    const int s = s0 + lane;
+    const bool in = s < kp;
+    E vals[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = __builtin_amdgcn_readlane(qrow, j);
+      vals[j] = in && ((vb >> j) & 1) ? ae[row * kp + s] : (E)0.f;
+    }
+    if (in) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ab[(16 * w + j) * kp + s] = vals[j];
+    }
+  }
+  const E *mine = ab + (16 * w + n) * kp;
+
+  f32x4 o[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) o[j] = zero4();
+  const int tr_off = (4 * gq + (n >> 2)) * RS + 4 * (n & 3);
+  const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  for (int si = 0; si < nsl; ++si) {
+    const int s0 = si * P.sl;
+    if (si > 0) __syncthreads();  // the previous slab's reads are done
+    stage_box1<T, D, R>(P, t, y, ys, tid, nthr, s0);
+    __syncthreads();
+    if (!ws.any) continue;
+    const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+    const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+    const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+    Cursor cc{a0, ws.ws[1], 0};
+    const int key0 = (((a0 - s0) * P.ax[1].Em + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    for (int c0 = 0; c0 < nch; c0 += NB) {
+      ChunkPos cp[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+      v8 bp[NB / 2];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
+          bp[j >> 1][4 * (j & 1) + r] = ok ? mine[cp[j].e01 + xc + r - sq] : (E)0.f;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < NB / 2; ++jj) {
+        const E *ca = ys + cp[2 * jj].kb * RS + tr_off;
+        const E *cb = ys + cp[2 * jj + 1].kb * RS + tr_off;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const v4 lo4 = M::tr(ca + 16 * db);
+          const v4 hi4 = M::tr(cb + 16 * db);
+          const v8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[db] = M::mma(av, bp[jj], o[db]);
+        }
+      }
+    }
+  }
+  if (!qv) return;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    v4 wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r] = (E)(o[db][r] * scale);
+    *reinterpret_cast<v4 *>(out + qrow * D + 16 * db + 4 * gq) = wv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_linv.  A workgroup owns a tile of keys of one key/value head; per query
+// head of the group it stages the X rows of the query box of the keys'
+// inverse windows.  Per pair of chunks of 16 queries the B operand (queries
+// 4 (l / 16) + r of each chunk, key l % 16) is a[q, J - S(q)] inside the
+// key's inverse window, gathered from HBM (J = sum_a j_a st_a of the lane's
+// key, S(q) = sum_a s_a(q) st_a), and Z^T += X^T . A with X^T through the
+// transposing LDS read.  The gathers of a group of chunk pairs are issued
+// together; every compact-row element is read by exactly one key.
+template <typename T, int D, int R, bool CPR1>
+__global__ void __launch_bounds__(256)
+    k_linv(LProb P, const T *__restrict__ a, const T *__restrict__ x,
+           T *__restrict__ z, float scale) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int NDB = D / 16;
+  constexpr int NP = 4;  // chunk pairs whose gathers are issued together
+  constexpr int RS = lds_y(D);
+  extern __shared__ __align__(16) char smem[];
+
+  // tile: (batch, key/value head, spatial tile)
+  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const uint32_t rest = fdiv((uint32_t)tile, P.fGrid);
+  const uint32_t sp = (uint32_t)tile - rest * P.fGrid.d;
+  const uint32_t bq = fdiv(rest, P.fHkv);
+  LTile t;
+  t.hk = (int)(rest - bq * P.fHkv.d);
+  t.b = (int)bq;
+  t.head = t.hk * P.rep;
+  const bool tile_any = tile_origin<R>(P, sp, t) & (t.b < P.B);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  if (!tile_any) return;  // uniform over the workgroup
+  tile_box<R, true>(P, t, t.head, P.H);
+  const WSub ws = wave_sub<R, true>(P, t, w);
+  bool kv;
+  int wl[3], ww[3], kj[3];
+  const int krow = lane_row<R, true>(P, t, ws, n, t.hk, P.Hkv, kv, wl, ww, kj);
+  const int J = (R == 3 ? kj[0] * P.kst0 : 0) + (R >= 2 ? kj[1] * P.kst1 : 0) + kj[2];
+
+  E *xs = reinterpret_cast<E *>(smem);
+  const E *ae = reinterpret_cast<const E *>(a);
+  const int kp = P.kp;
+  const LAx &x2 = P.ax[2];
+  f32x4 acc[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) acc[j] = zero4();
+  const int tr_off = (4 * gq + (n >> 2)) * RS + 4 * (n & 3);
+  const int qbase0 = t.kbase;  // X rows of query head hk * rep
+  const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  const int Em1 = P.ax[1].Em;
+  for (int hr = 0; hr < P.rep; ++hr) {
+    t.kbase = qbase0 + hr * D;
+    const int head = t.head + hr;
+    for (int si = 0; si < nsl; ++si) {
+      const int s0 = si * P.sl;
+      __syncthreads();  // the LDS reads of the previous box or slab are done
+      stage_box1<T, D, R>(P, t, x, xs, tid, nthr, s0);
+      __syncthreads();
+      if (!ws.any) continue;
+      const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
+      const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
+      const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+      Cursor cc{a0, ws.ws[1], 0};
+      const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+      for (int c0 = 0; c0 < nch; c0 += 2 * NP) {
+        ChunkPos cp[2 * NP];
+        v8 bp[NP];
+#pragma unroll
+        for (int j = 0; j < 2 * NP; ++j) {
+          cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+          // the chunk's row: slot-base and token parts of axes 0 and 1
+          int sb01 = 0, tok01 = t.b * P.Ltot + t.r[2];
+          if (R == 3) {
+            const int i0 = t.lo[0] + cp[j].e0;
+            sb01 += (wend(P.ax[0], i0, t.Lr[0]) - P.ax[0].K) * P.kst0;
+            tok01 += (t.r[0] + P.ax[0].d * i0) * P.ax[0].tok;
+          }
+          if (R >= 2) {
+            const int i1 = t.lo[1] + cp[j].e1;
+            sb01 += (wend(P.ax[1], i1, t.Lr[1]) - P.ax[1].K) * P.kst1;
+            tok01 += (t.r[1] + P.ax[1].d * i1) * P.ax[1].tok;
+          }
+          const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
+            const int i2 = t.lo[2] + xc + r;
+            const int sq = sb01 + wend(x2, i2, t.Lr[2]) - x2.K;
+            const int row = (tok01 + x2.d * i2) * P.H + head;
+            bp[j >> 1][4 * (j & 1) + r] = ok ? ae[row * kp + J - sq] : (E)0.f;
+          }
+        }
+#pragma unroll
+        for (int jj = 0; jj < NP; ++jj) {
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const v4 x0 = M::tr(xs + cp[2 * jj].kb * RS + tr_off + 16 * db);
+            const v4 x1 = M::tr(xs + cp[2 * jj + 1].kb * RS + tr_off + 16 * db);
+            const v8 xt = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[db] = M::mma(xt, bp[jj], acc[db]);
+          }
+        }
+      }
+    }
+  }
+  if (!kv) return;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    v4 wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r] = (E)(acc[db][r] * scale);
+    *reinterpret_cast<v4 *>(z + krow * D + 16 * db + 4 * gq) = wv;
+  }
+}
+
+}  // namespace
+
+bool lsplit_eligible(const Prob &P, int dtype) {
+  if (!lean_shape_ok(P, dtype)) return false;
+  if (P.dense || P.n_extra > 0 || P.sample_extent != nullptr) return false;
+  // 32-bit offsets into the compact rows
+  if ((int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L * P.H * P.kprod >=
+      (int64_t(1) << 31))
+    return false;
+  return lean_choice(P, kLQK).ok && lean_choice(P, kLInv).ok;
+}
+
+#define LS_D(D_, BODY) \
+  do {                 \
+    if ((D_) == 32) {  \
+      BODY(32);        \
+    } else if ((D_) == 64) { \
+      BODY(64);        \
+    } else {           \
+      BODY(128);       \
+    }                  \
+  } while (0)
+
+// Launch KERNEL<T, D, R, CPR1> for the problem's dtype, head_dim and rank.
+#define LS_DISPATCH(KERNEL, ARGS)                                               \
+  do {                                                                          \
+    auto go = [&](auto tt, auto dd, auto rr, auto cc) {                         \
+      typedef decltype(tt) TT;                                                  \
+      constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;         \
+      constexpr bool CC = decltype(cc)::value;                                  \
+      hipLaunchKernelGGL((KERNEL<TT, DD, RR, CC>), grid, block, lds, st, L,     \
+                         ARGS);                                                 \
+    };                                                                          \
+    auto by_r = [&](auto tt, auto dd) {                                         \
+      if (P.rank == 1)                                                          \
+        go(tt, dd, std::integral_constant<int, 1>(), std::false_type());        \
+      else if (P.rank == 2) {                                                   \
+        if (C.cpr1) go(tt, dd, std::integral_constant<int, 2>(), std::true_type()); \
+        else go(tt, dd, std::integral_constant<int, 2>(), std::false_type());   \
+      } else {                                                                  \
+        if (C.cpr1) go(tt, dd, std::integral_constant<int, 3>(), std::true_type()); \
+        else go(tt, dd, std::integral_constant<int, 3>(), std::false_type());   \
+      }                                                                         \
+    };                                                                          \
+    auto by_d = [&](auto tt) {                                                  \
+      if (P.D == 32) by_r(tt, std::integral_constant<int, 32>());               \
+      else if (P.D == 64) by_r(tt, std::integral_constant<int, 64>());          \
+      else by_r(tt, std::integral_constant<int, 128>());                        \
+    };                                                                          \
+    if (dtype == NA_BF16) by_d(bf16_t());                                       \
+    else by_d(f16_t());                                                         \
+  } while (0)
+
+void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
+               void *out, float scale, float fill, hipStream_t st) {
+  const LChoice C = lean_choice(P, kLQK);
+  const LProb L = make_lprob(P, C);
+  if (L.n_tiles == 0) return;
+  const size_t lds = lean_lds_bytes(P, kLQK, L.ebox, C.W);
+  const dim3 grid(L.n_launch), block(64 * C.W);
+  int prefill = 0;
+  for (int a = 0; a < 3; ++a) prefill |= P.ax[a].causal;
+#define LS_ARGS_QK(TT) (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill
+  LS_DISPATCH(k_lqk, LS_ARGS_QK(TT));
+#undef LS_ARGS_QK
+}
+
+void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
+               void *out, float scale, hipStream_t st) {
+  const LChoice C = lean_choice(P, kLQK);
+  const LProb L = make_lprob(P, C);
+  if (L.n_tiles == 0) return;
+  const size_t lds = lean_lds_bytes(P, kLQK, L.ebox, C.W);
+  const dim3 grid(L.n_launch), block(64 * C.W);
+#define LS_ARGS_AV(TT) (const TT *)a, (const TT *)y, (TT *)out, scale
+  LS_DISPATCH(k_lav, LS_ARGS_AV(TT));
+#undef LS_ARGS_AV
+}
+
+void lsplit_inv(const Prob &P, int dtype, const void *a, const void *x,
+                void *z, float scale, hipStream_t st) {
+  const LChoice C = lean_choice(P, kLInv);
+  LProb L = make_lprob(P, C);
+  L.n_tiles = P.B * P.Hkv * (int)L.fGrid.d;
+  L.n_launch = (L.n_tiles + 7) & ~7;
+  if (L.n_tiles == 0) return;
+  const size_t lds = lean_lds_bytes(P, kLInv, L.ebox, C.W);
+  const dim3 grid(L.n_launch), block(64 * C.W);
+#define LS_ARGS_INV(TT) (const TT *)a, (const TT *)x, (TT *)z, scale
+  LS_DISPATCH(k_linv, LS_ARGS_INV(TT));
+#undef LS_ARGS_INV
+}
+
+#undef LS_DISPATCH
+#undef LS_D
+
+}  // namespace na

@@ -128,13 +128,15 @@ KERNEL_PATHS = {0: "generic", 1: "mfma", 2: "lean"}
 
 
 def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_extra=0,
-                dense=False, sample_extent=None, backward=False, varlen_clamped=False):
-    """Name of the kernel family na_fwd (or na_bwd) runs for this problem:
-    "generic", "mfma" or "lean" (a diagnostic; launches nothing)."""
+                dense=False, sample_extent=None, backward=False, varlen_clamped=False,
+                split=False):
+    """Name of the kernel family na_fwd (or na_bwd; or with ``split`` the
+    split ops qk/av forward and backward) runs for this problem: "generic",
+    "mfma" or "lean" (a diagnostic; launches nothing)."""
     lib = _lib.load()
     p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
                 sample_extent, varlen_clamped)
-    r = int(lib.na_kernel_path(p, 1 if backward else 0))
+    r = int(lib.na_kernel_path(p, 2 if split else 1 if backward else 0))
     if r < 0:
         _lib.check(-r, "na_kernel_path")
     return KERNEL_PATHS[r]

@@ -7,6 +7,7 @@ oracle (2e-2 absolute of the dtype-rounded value, see tests/_helpers.py) and
 with the generic vector-ALU kernels on the same device.
 """
 
+import contextlib
 import sys
 
 import pytest
@@ -136,14 +137,16 @@ SPLIT_CASES = [
     ("3d_causal", 1, (6, 12, 12), 4, 4, 64, (3, 7, 7), (1, 1, 1), (True, False, False)),
     ("1d_k63_d128", 2, (300,), 2, 1, 128, (63,), (2,), (False,)),
     ("1d_causal", 2, (70,), 2, 2, 32, (9,), (3,), (True,)),
+    ("2d_wide_causal_gqa4", 1, (12, 40), 8, 2, 32, (3, 17), (1, 2), (True, False)),
 ]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
 def test_mfma_split_ops(case, dtype):
-    """Matrix-core split QK / AV forward and backward against the oracle,
-    and the generic kernels on the same inputs against the oracle too."""
+    """Split QK / AV forward and backward against the oracle on the lean
+    workgroup kernels (where they run by default), the 32-query matrix-core
+    kernels and the generic kernels, all on the same inputs."""
     import natten_amd
     from natten_amd._core import hip
 
@@ -168,9 +171,14 @@ def test_mfma_split_ops(case, dtype):
     rq, rk = O.grads(qk_masked, (q, k), (gl,))
     ra, rv = O.grads(lambda a, b: O.na_av(a, b, ks, 1, dil, caus), (attn, v), (go,))
     ref_out = O.na_av(attn, v, ks, 1, dil, caus)
-    for generic in (False, True):
-        tag = f"{name}{' generic' if generic else ''}"
-        with hip.generic_kernels(generic):
+    assert hip.kernel_path(q, k, ks, (1,) * rank, dil, caus, split=True) == "lean"
+    with hip.no_lean_kernels():
+        assert hip.kernel_path(q, k, ks, (1,) * rank, dil, caus, split=True) == "mfma"
+    modes = {"lean": contextlib.nullcontext, "mfma": hip.no_lean_kernels,
+             "generic": hip.generic_kernels}
+    for mode, ctx in modes.items():
+        tag = f"{name} {mode}"
+        with ctx():
             qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
             logits = qk(qd, kd, ks, dil, is_causal=caus, scale=0.25)
             assert torch.equal(torch.isinf(logits).cpu(), ~finite), f"{tag} mask"

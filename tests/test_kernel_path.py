@@ -69,3 +69,16 @@ def test_lean_boundaries():
     with hip.no_lean_kernels():
         assert _path(*base) == "mfma"
         assert _path(*base, backward=True) == "mfma"
+
+
+def test_split_ops_run_lean():
+    for d in ((1, 1), (4, 4)):
+        assert _path((4, 56, 56, 4, 32), 4, (7, 7), d, (False, False), split=True) == "lean"
+    assert _path((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False),
+                 split=True) == "lean"
+    assert _path((2, 300, 2, 128), 1, (63,), (2,), (False,), split=True) == "lean"
+    assert _path((2, 40, 40, 4, 32), 4, (7, 7), (1, 1), (False, False), dtype=torch.float32,
+                 split=True) == "generic"
+    with hip.no_lean_kernels():
+        assert _path((4, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False),
+                     split=True) == "mfma"
