@@ -257,24 +257,30 @@ __global__ void __launch_bounds__(256)
         const bool box = c < nchb;
         const bool ext = VX && !box && c < nch;
         bool ok = box;
-        if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+        // closed forms: one box row (rank 1) or one chunk per row (rank 2,
+        // CPR1); otherwise the cursor
+        const int e1 = R == 2 && CPR1 ? ws.ws[1] + c : cc.e1;
+        const int cs = R == 1 ? c : CPR1 ? 0 : cc.cs;
+        if (R > 1) ok = ok && (unsigned)(e1 - wl[1]) < (unsigned)ww[1];
         if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+        const int krow = R == 1 ? key0 + 16 * c
+                         : R == 2 && CPR1 ? key0 + (c << P.lgP2)
+                         : (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs;
         float cb[4];
         if (CPR1 && !VX) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
-          kb[j] = box ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] : key0;
+          kb[j] = box ? krow : key0;
         } else {
           // extra chunk c - nchb: keys 16 (c - nchb) + 4 gq + r < nx
           const int xc = 16 * (c - nchb);
-          col_bias(box ? ws.ws[2] + 16 * cc.cs + 4 * gq - wl[2] : xc + 4 * gq,
+          col_bias(box ? ws.ws[2] + 16 * cs + 4 * gq - wl[2] : xc + 4 * gq,
                    box ? ww[2] : (qv ? P.nx : 0), cb);
-          kb[j] = box ? (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
-                      : ext ? xc - nxr : key0;
+          kb[j] = box ? krow : ext ? xc - nxr : key0;
           ok = ok || ext;
         }
         sv[j] = mask_init(ok, cb);
-        advance(cc, ws);
+        if (R == 3 || (R == 2 && !CPR1)) advance(cc, ws);
       }
       fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, l, sl2, ka_off, tr_off);
     };
@@ -403,7 +409,10 @@ __device__ __forceinline__ int lane_rows(const LProb &P, const LTile &t,
 
 // Rows of chunk pair (a, b) of a wave's sub-box: first LDS row, row test
 // and column segment of each (padding chunks: row 0 of the sub-box, masked).
-template <int R>
+// Closed forms where the walk is one box row (rank 1: chunk c is columns
+// 16 c..) or one chunk per row (rank 2, CPR1: chunk c is row ws1 + c);
+// otherwise the cursor walks rows and segments.
+template <int R, bool CPR1>
 __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
                                           int nch, int s0, int Em1, int lgP2,
                                           int key0,
@@ -411,14 +420,25 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
                                           int kb[2], bool rok[2], int cs[2]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const bool real = c0 + h < nch;
-    kb[h] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
-    cs[h] = cc.cs;
-    bool ok = real;
-    if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
-    if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
-    rok[h] = ok;
-    advance(cc, ws);
+    const int c = c0 + h;
+    const bool real = c < nch;
+    if (R == 1) {
+      kb[h] = key0 + (real ? 16 * c : 0);
+      cs[h] = c;
+      rok[h] = real;
+    } else if (R == 2 && CPR1) {
+      kb[h] = key0 + (real ? c << lgP2 : 0);
+      cs[h] = 0;
+      rok[h] = real && (unsigned)(ws.ws[1] + c - wl[1]) < (unsigned)ww[1];
+    } else {
+      kb[h] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
+      cs[h] = cc.cs;
+      bool ok = real;
+      if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+      if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+      rok[h] = ok;
+      advance(cc, ws);
+    }
   }
 }
 
@@ -512,7 +532,7 @@ __global__ void __launch_bounds__(256)
       for (int c0 = 0; c0 < nch; c0 += 2) {
         int kb[2], cs[2];
         bool rok[2];
-        pair_rows<R>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        pair_rows<R, CPR1>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
         v8 kr[2][NT], vr[2][NT];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -643,7 +663,7 @@ __global__ void __launch_bounds__(256)
     for (int c0 = 0; c0 < nch; c0 += 2) {
       int kb[2], cs[2];
       bool rok[2];
-      pair_rows<R>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+      pair_rows<R, CPR1>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
       v8 qr[2][NT], orr[2][NT];
       float ls2[2][4];
 #pragma unroll
