@@ -118,23 +118,41 @@ struct ChunkPos {
   int col;     // box column of the chunk's first row
 };
 
-template <int R>
+// Chunk ci of the walk; closed forms where the walk is one box row (rank 1)
+// or one chunk per row (rank 2, CPR1), otherwise the cursor (chunks in
+// order).
+template <int R, bool CPR1>
 __device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
-                                              Cursor &cc, bool real, int s0,
-                                              int key0, const int wl[3],
+                                              Cursor &cc, int ci, int nch,
+                                              int s0, int key0, const int wl[3],
                                               const int ww[3]) {
   ChunkPos c;
-  c.kb = real ? (((cc.e0 - s0) * P.ax[1].Em + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
-              : key0;
-  bool ok = real;
-  if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
-  if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
-  c.rok = ok;
-  c.e0 = cc.e0;
-  c.e1 = cc.e1;
-  c.e01 = cc.e0 * P.kst0 + cc.e1 * P.kst1;
-  c.col = ws.ws[2] + 16 * cc.cs;
-  advance(cc, ws);
+  const bool real = ci < nch;
+  if (R == 1) {
+    c.kb = key0 + (real ? 16 * ci : 0);
+    c.rok = real;
+    c.e0 = 0;
+    c.e1 = 0;
+    c.col = ws.ws[2] + 16 * ci;
+  } else if (R == 2 && CPR1) {
+    c.kb = key0 + (real ? ci << P.lgP2 : 0);
+    c.e0 = 0;
+    c.e1 = ws.ws[1] + ci;
+    c.rok = real && (unsigned)(c.e1 - wl[1]) < (unsigned)ww[1];
+    c.col = ws.ws[2];
+  } else {
+    c.kb = real ? (((cc.e0 - s0) * P.ax[1].Em + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
+                : key0;
+    bool ok = real;
+    if (R > 1) ok = ok && (unsigned)(cc.e1 - wl[1]) < (unsigned)ww[1];
+    if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+    c.rok = ok;
+    c.e0 = cc.e0;
+    c.e1 = cc.e1;
+    c.col = ws.ws[2] + 16 * cc.cs;
+    advance(cc, ws);
+  }
+  c.e01 = c.e0 * P.kst0 + c.e1 * P.kst1;
   return c;
 }
 
@@ -198,7 +216,7 @@ __global__ void __launch_bounds__(256)
       ChunkPos cp[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+        cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
       v8 ka[NB][NT];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
@@ -313,7 +331,7 @@ __global__ void __launch_bounds__(256)
       ChunkPos cp[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+        cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
       v8 bp[NB / 2];
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
@@ -422,7 +440,7 @@ __global__ void __launch_bounds__(256)
         v8 bp[NP];
 #pragma unroll
         for (int j = 0; j < 2 * NP; ++j) {
-          cp[j] = chunk_pos<R>(P, ws, cc, c0 + j < nch, s0, key0, wl, ww);
+          cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
           // the chunk's row: slot-base and token parts of axes 0 and 1
           int sb01 = 0, tok01 = t.b * P.Ltot + t.r[2];
           if (R == 3) {
