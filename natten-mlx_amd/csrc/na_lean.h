@@ -420,7 +420,7 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
       const int g = unit_offset<R>(P, t, kk, o, s0);
       xr[j] = ld8(x, g);
       yr[j] = ld8(y, g);
-      la[j] = kk * RSE + 8 * o;
+      la[j] = __umul24(kk, RSE) + 8 * o;  // 24-bit: LDS rows
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

@@ -348,8 +348,8 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<v8 *>(qs + kk[j] * RSE + 8 * o[j]) = qr[j];
-      *reinterpret_cast<v8 *>(os + kk[j] * RSE + 8 * o[j]) = dr[j];
+      *reinterpret_cast<v8 *>(qs + __umul24(kk[j], RSE) + 8 * o[j]) = qr[j];
+      *reinterpret_cast<v8 *>(os + __umul24(kk[j], RSE) + 8 * o[j]) = dr[j];
       float part = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -363,7 +363,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
 #pragma unroll
       for (int m = 1; m < OCT; m <<= 1) part += __shfl_xor(part, m);
       if (o[j] == 0)
-        *reinterpret_cast<float2 *>(qs + kk[j] * RSE + D) =
+        *reinterpret_cast<float2 *>(qs + __umul24(kk[j], RSE) + D) =
             make_float2(lr[j] * kLog2e, dl[j] - part);
     }
   }
@@ -480,6 +480,8 @@ __global__ void __launch_bounds__(256)
   const int Em1 = P.ax[1].Em;
   const int ka_off = n * RSE + 8 * gq;
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
+  // the (lse, -delta) pad of query row 4 gq of a chunk
+  const int pad_off = 4 * gq * RSE + D;
   if (!tile_any) return;  // uniform over the workgroup
   E *xs = reinterpret_cast<E *>(smem);
   E *ys = xs + lds_y(D);
@@ -675,7 +677,7 @@ __global__ void __launch_bounds__(256)
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          ls2[h][r] = *reinterpret_cast<const float *>(xs + (kb[h] + 4 * gq + r) * RSE + D);
+          ls2[h][r] = *reinterpret_cast<const float *>(xs + kb[h] * RSE + pad_off + r * RSE);
       }
       // dO^T and Q^T operands of the dV / dK MFMAs, read now so their
       // latency overlaps the score MFMAs and exponentials
@@ -704,7 +706,7 @@ __global__ void __launch_bounds__(256)
         sc[h] = mask_init(rok[h], cb);
 #pragma unroll
         for (int r = 0; r < 4; ++r)  // -delta of the row, read into the accumulator
-          dp[h][r] = *reinterpret_cast<const float *>(xs + (kb[h] + 4 * gq + r) * RSE + D + 2);
+          dp[h][r] = *reinterpret_cast<const float *>(xs + kb[h] * RSE + pad_off + r * RSE + 2);
 #pragma unroll
         for (int st = 0; st < NT; ++st) {
           sc[h] = M::mma(qr[h][st], kf[st], sc[h]);

@@ -53,7 +53,7 @@ __device__ __forceinline__ void stage_box1(const LProb &P, const LTile &t,
       const int u = min(u0 + j * nthr + tid, nun - 1);
       const int kk = u / OCT, o = u % OCT;
       xr[j] = ld8(x, unit_offset<R>(P, t, kk, o, s0));
-      la[j] = kk * RS + 8 * o;
+      la[j] = __umul24(kk, RS) + 8 * o;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<v8 *>(xs + la[j]) = xr[j];
