@@ -40,13 +40,17 @@ namespace {
 // One group of NB (even) chunks of 16 staged keys (first LDS rows kb[j]
 // from the bases ks / vs; sv[j] holds the chunk's mask as the score
 // accumulator's initial value): scores, online softmax update of (m, l, o)
-// and O^T += V^T . P^T.
+// and O^T += V^T . P^T.  The row sums l come out of the matrix core too:
+// `ones` is an A operand whose row 0 is all ones, so lacc[0] of lane n
+// (lanes 0-15) accumulates the sum of query n's rounded probabilities (the
+// same values that weight V) and the other lanes' lacc stay zero.
 template <typename T, int D, int NB>
 __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
                                           const typename L16<T>::e *vs,
                                           const int (&kb)[NB], f32x4 (&sv)[NB],
                                           const typename L16<T>::v8 (&qf)[D / 32],
-                                          f32x4 (&o)[D / 16], float &m, float &l,
+                                          f32x4 (&o)[D / 16], float &m, f32x4 &lacc,
+                                          const typename L16<T>::v8 &ones,
                                           float sl2, int ka_off, int tr_off) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
@@ -78,7 +82,7 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
   if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
     const float mn = fmaxf(m, mx);
     const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
-    l *= alpha;
+    lacc *= alpha;
 #pragma unroll
     for (int j = 0; j < NDB; ++j) o[j] *= alpha;
     m = mn;
@@ -92,7 +96,6 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float p = __builtin_amdgcn_exp2f(fmaf(sv[2 * jj + h][r], sl2, -mu));
-        l += p;
         bp[jj][4 * h + r] = (E)p;
       }
   // ---- O^T += V^T . P^T, two chunks per MFMA ----
@@ -107,6 +110,7 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
       const v8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
       o[db] = M::mma(a, bp[jj], o[db]);
     }
+    lacc = M::mma(ones, bp[jj], lacc);
   }
 }
 
@@ -221,7 +225,11 @@ __global__ void __launch_bounds__(256)
   f32x4 o[NDB];
 #pragma unroll
   for (int j = 0; j < NDB; ++j) o[j] = zero4();
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY;
+  f32x4 lacc = zero4();
+  v8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = (E)(n == 0 ? 1.f : 0.f);
   const float sl2 = P.sl2;
   const int Em1 = P.ax[1].Em;
   // operand-read lane offsets inside a chunk: K rows (key n, 8 elements at
@@ -282,7 +290,7 @@ __global__ void __launch_bounds__(256)
         sv[j] = mask_init(ok, cb);
         if (R == 3 || (R == 2 && !CPR1)) advance(cc, ws);
       }
-      fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, l, sl2, ka_off, tr_off);
+      fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, lacc, ones, sl2, ka_off, tr_off);
     };
     if constexpr (NB >= 4) {
       int c0 = 0;
@@ -295,7 +303,7 @@ __global__ void __launch_bounds__(256)
   }
 
   // ---- epilogue: sum l over the query's 4 lanes, normalise, store ----
-  l = quad_sum(l);
+  const float l = quad_sum(lacc[0]);
   if (!(VX ? qt : qv)) return;
   const float inv = qv && l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
