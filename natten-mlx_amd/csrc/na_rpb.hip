@@ -444,16 +444,20 @@ __device__ __forceinline__ void slots_of_bias_row(int32_t r, int32_t pb,
   *hi = b > K - 1 ? K - 1 : b;
 }
 
-// Bias gradient, pass 1: one block per chunk of `chunk` queries (rows in
-// (b, i0, i1) order).  The chunk's windows are computed once into LDS; then
-// thread t owns bins t, t + 256, ... (bin = (h, r0[, r1])) and sums, in
-// query order, dlogits over the slots whose clipped bias row is the bin.
-// partial is output-major, partial[bin * n_chunks + c], so pass 2 reads
-// each bin's partials contiguously.
+// Bias gradient, pass 1: one block per chunk of `chunk` (<= kBiasChunk)
+// queries (rows in (b, i0, i1) order); partial[bin * n_chunks + c] is the
+// chunk's sum for bin = (h, r0[, r1]), output-major so pass 2 reads each
+// bin's partials contiguously.  `scatter` (the chunk's [query][head][bin]
+// sums fit 32 KB of LDS): thread (t, h) adds its row's valid slots into
+// its own LDS cells [t][h][clipped bias row] (slot order), then thread
+// `bin` sums the chunk's cells in query order.  Otherwise thread `bin` walks
+// the queries and reads the slots whose clipped bias row is the bin.
+// Either way the order of every sum is fixed.
 __global__ void __launch_bounds__(256)
     k_rpb_bias_partial(RpbProb A, const float *__restrict__ dl,
                        float *__restrict__ partial, int32_t chunk,
-                       int32_t n_chunks) {
+                       int32_t n_chunks, int scatter) {
+  extern __shared__ float sacc[];
   __shared__ RWin sw0[kBiasChunk], sw1[kBiasChunk];
   __shared__ int32_t sb[kBiasChunk], si0[kBiasChunk], si1[kBiasChunk];
   const int32_t c = blockIdx.x;
@@ -461,6 +465,8 @@ __global__ void __launch_bounds__(256)
   const int32_t q0 = c * chunk;
   const int32_t nqc = min(chunk, nq - q0);
   const int tid = threadIdx.x;
+  const int32_t per_h = A.R0 * A.R1;
+  const int32_t nb = A.H * per_h;
   if (tid < nqc) {
     const int32_t qi = q0 + tid;
     const int32_t rest = (int32_t)fdiv((uint32_t)qi, A.fL1);
@@ -473,9 +479,42 @@ __global__ void __launch_bounds__(256)
     si0[tid] = i0;
     si1[tid] = i1;
   }
+  if (scatter) {
+    for (int32_t i = tid; i < nqc * nb; i += blockDim.x) sacc[i] = 0.f;
+    __syncthreads();
+    for (int32_t th = tid; th < nqc * A.H; th += blockDim.x) {
+      const int32_t t = th / A.H;
+      const int32_t h = th - t * A.H;
+      const RWin w0 = sw0[t];
+      const RWin w1 = sw1[t];
+      const float *row = dl + rrow(A, sb[t], h, si0[t], si1[t]) * A.KK;
+      float *cell = sacc + th * per_h;
+      for (int32_t k0 = 0; k0 < A.K0; ++k0) {
+        const int32_t j0 = w0.s + k0 * A.d0;
+        if (j0 < 0 || j0 >= w0.e) continue;
+        const int32_t r0 = clampi(w0.pb + k0, 0, A.R0 - 1);
+        if (A.rank == 1) {
+          cell[r0] += row[k0];
+          continue;
+        }
+        for (int32_t k1 = 0; k1 < A.K1; ++k1) {
+          const int32_t j1 = w1.s + k1 * A.d1;
+          if (j1 < 0 || j1 >= w1.e) continue;
+          cell[r0 * A.R1 + clampi(w1.pb + k1, 0, A.R1 - 1)] += row[k0 * A.K1 + k1];
+        }
+      }
+    }
+    __syncthreads();
+    for (int32_t bin = tid; bin < nb; bin += blockDim.x) {
+      const int32_t h = bin / per_h;
+      const int32_t rb = bin - h * per_h;
+      float acc = 0.f;
+      for (int32_t t = 0; t < nqc; ++t) acc += sacc[(t * A.H + h) * per_h + rb];
+      partial[(int64_t)bin * n_chunks + c] = acc;
+    }
+    return;
+  }
   __syncthreads();
-  const int32_t per_h = A.R0 * A.R1;
-  const int32_t nb = A.H * per_h;
   for (int32_t bin = tid; bin < nb; bin += blockDim.x) {
     const int32_t h = bin / per_h;
     const int32_t rb = bin - h * per_h;
@@ -513,8 +552,18 @@ __global__ void __launch_bounds__(64)
   const int32_t o = blockIdx.x;
   const int lane = threadIdx.x;
   const float *src = partial + (int64_t)o * n_chunks;
+  // eight loads in flight per lane, summed in a fixed order
   float acc = 0.f;
-  for (int32_t c = lane; c < n_chunks; c += 64) acc += src[c];
+  for (int32_t c0 = 0; c0 < n_chunks; c0 += 8 * 64) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int32_t c = c0 + j * 64 + lane;
+      v[j] = c < n_chunks ? src[c] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += v[j];
+  }
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (lane == 0) drpb[o] = acc;
 }
@@ -688,9 +737,13 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     int32_t chunk, n_chunks;
     bias_chunking(A, &chunk, &n_chunks);
     const int32_t nb = A.H * A.R0 * A.R1;
+    // per-(query, head) bin cells in LDS when they fit 32 KB
+    const size_t sbytes = (size_t)chunk * nb * sizeof(float);
+    const int scatter = sbytes <= 32768;
     if (n_chunks > 0)
       hipLaunchKernelGGL(k_rpb_bias_partial, dim3((unsigned)n_chunks), dim3(256),
-                         0, st, A, dlogits, workspace, chunk, n_chunks);
+                         scatter ? sbytes : 0, st, A, dlogits, workspace, chunk,
+                         n_chunks, scatter);
     hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)nb), dim3(64), 0, st,
                        (const float *)workspace, n_chunks, drpb);
   }
