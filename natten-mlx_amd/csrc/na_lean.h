@@ -452,6 +452,20 @@ size_t lds_budget() {
   return b;
 }
 
+// Largest number of waves per workgroup tried: 8 on rank 1, 4 otherwise
+// (measured: eight-wave workgroups halve the workgroup count, and at
+// config 2 size the CUs holding two of them set a longer tail than the 16
+// CUs holding a fourth four-wave workgroup; on the 1-D config 4 they are
+// faster).  NATTEN_AMD_LEAN_WAVES overrides it (tuning).
+int lean_max_waves(int rank) {
+  static const int w = [] {
+    const char *e = std::getenv("NATTEN_AMD_LEAN_WAVES");
+    const int v = e != nullptr ? std::atoi(e) : 0;
+    return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
+  }();
+  return w > 0 ? w : rank == 1 ? 8 : 4;
+}
+
 struct LChoice {
   int T[3];      // wave tile (product 16 over the active axes)
   int W, sa;     // waves per workgroup and the axis they are stacked along
@@ -527,7 +541,7 @@ int box_max(const Axis &x, int t, bool inverse) {
 }
 
 // Wave tile: the power-of-two shape with the fewest (waves x chunks);
-// workgroup: up to 4 waves stacked along the axis with the smallest staged
+// workgroup: up to 8 waves stacked along the axis with the smallest staged
 // box per wave whose box fits the LDS budget.  For the backward the boxes
 // also cover the inverse windows (query boxes of key tiles) and the LDS
 // holds a (lse, delta) pair per staged row.
@@ -571,10 +585,11 @@ LChoice lean_choice(const Prob &P, LMode mode) {
       }
     }
   double best_per_wave = 1e300;
-  for (int W = 4; W >= 1; W >>= 1)
+  for (int W = lean_max_waves(R); W >= 1; W >>= 1)
     for (int sa = lead; sa < 3; ++sa) {
       const Axis &x = P.ax[sa];
-      if (W > 1 && best.T[sa] >= (x.L + x.d - 1) / x.d) continue;
+      // every wave tile of a workgroup must start inside the phase
+      if (W > 1 && best.T[sa] * (W - 1) >= (x.L + x.d - 1) / x.d) continue;
       int Em[3];
       for (int a = 0; a < 3; ++a) Em[a] = ext(a, best.T[a] * (a == sa ? W : 1));
       // rank 3 may stage the box a few layers (axis 0) at a time
@@ -583,8 +598,10 @@ LChoice lean_choice(const Prob &P, LMode mode) {
         --sl;
       const int ebox = lds_rows(R, Em) / Em[0] * sl;
       if (lean_lds_bytes(P, mode, ebox, W) > lds_budget()) continue;
-      // staged rows per wave over all slabs; fewer slabs break ties
-      const double per_wave = (double)lds_rows(R, Em) / W;
+      // staged rows per wave over all slabs, each extra slab (a restaging
+      // round trip and barrier) counted as a quarter more
+      const int nsl = (Em[0] + sl - 1) / sl;
+      const double per_wave = (double)lds_rows(R, Em) / W * (1.0 + 0.25 * (nsl - 1));
       if (per_wave < best_per_wave * 0.999 ||
           (per_wave < best_per_wave * 1.001 && sl > best.sl)) {
         best_per_wave = per_wave;

@@ -120,7 +120,7 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
 // before the box and attended after it); query rows of the tensor outside
 // their sample's extent get zero output and lse 0.
 template <typename T, int D, int R, bool CPR1, bool VX>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_wfwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, T *__restrict__ out,
@@ -458,7 +458,7 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
 // accumulates dK and dV of its 16 keys.  One workgroup per tile keeps the
 // whole launch resident at once.
 template <typename T, int D, int R, bool CPR1>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_wbwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ out,
            const float *__restrict__ lse, const T *__restrict__ dout,

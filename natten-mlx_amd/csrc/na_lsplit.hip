@@ -162,7 +162,7 @@ __device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
 // LDS; then the rows to HBM.  FILL: some slots lie outside every window
 // (a causal axis) and start as `fill`.
 template <typename T, int D, int R, bool CPR1>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_lqk(LProb P, const T *__restrict__ x, const T *__restrict__ y,
           T *__restrict__ out, float scale, float fill, int prefill) {
   typedef L16<T> M;
@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(256)
 // by slot (zero outside the window) and O^T += Y^T . A^T with Y^T through
 // the transposing LDS read.
 template <typename T, int D, int R, bool CPR1>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_lav(LProb P, const T *__restrict__ a, const T *__restrict__ y,
           T *__restrict__ out, float scale) {
   typedef L16<T> M;
@@ -376,7 +376,7 @@ __global__ void __launch_bounds__(256)
 // transposing LDS read.  The gathers of a group of chunk pairs are issued
 // together; every compact-row element is read by exactly one key.
 template <typename T, int D, int R, bool CPR1>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_linv(LProb P, const T *__restrict__ a, const T *__restrict__ x,
            T *__restrict__ z, float scale) {
   typedef L16<T> M;
