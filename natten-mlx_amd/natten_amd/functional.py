@@ -282,6 +282,7 @@ def _validate_seq_lens(seq_lens, batch_size, l_max, kernel_size):
                          f"but min(seq_lens)={min_len}.")
     if max_len > l_max:
         raise ValueError(f"All seq_lens must be <= L_max ({l_max}), but max(seq_lens)={max_len}.")
+    return min_len
 
 
 def na1d_varlen(query, key, value, seq_lens, kernel_size, dilation=1, scale=None):
@@ -347,9 +348,8 @@ def na1d_varlen_gqa(query, key, value, seq_lens, kernel_size, dilation=1, scale=
     B, L_max = query.shape[0], query.shape[1]
     ks = normalize_kernel_size(kernel_size, 1)
     dil = normalize_tuple_param(dilation, 1, "dilation")
-    _validate_seq_lens(seq_lens, B, L_max, ks[0])
-    host = seq_lens.detach().cpu()
-    if int(host.min()) < dil[0] * ks[0]:
+    min_len = _validate_seq_lens(seq_lens, B, L_max, ks[0])
+    if min_len < dil[0] * ks[0]:
         raise ValueError(f"All seq_lens must be >= dilation * kernel_size ({dil[0] * ks[0]}).")
     scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
     se = seq_lens.to(device=query.device, dtype=torch.int32).reshape(B, 1).contiguous()
