@@ -250,10 +250,10 @@ __device__ __forceinline__ int64_t stage_window(const RpbProb &A, const T *y,
   return lo;
 }
 
-// Rows of the staged window per block (bounds the LDS it needs).
-inline int64_t window_rows(const RpbProb &A, int lgG) {
+// Rows of the staged window per block of rb threads (bounds its LDS).
+inline int64_t window_rows(const RpbProb &A, int lgG, int rb) {
   const int64_t step = A.heads_first ? 1 : A.H;
-  return (256 >> lgG) + 2 * (int64_t)A.K0 * A.d0 * step;
+  return (rb >> lgG) + 2 * (int64_t)A.K0 * A.d0 * step;
 }
 
 // ---- kernels ---------------------------------------------------------------
@@ -263,7 +263,7 @@ inline int64_t window_rows(const RpbProb &A, int lgG) {
 // (x = q, y = key, fill = -inf) and the AV backward's dattn (x = dout,
 // y = value, no bias, fill = 0).
 template <typename TX, typename TY, int VEC, bool YS>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_rpb_dot(RpbProb A, const TX *__restrict__ x, const TY *__restrict__ y,
               const float *__restrict__ rpb, float *__restrict__ out,
               int scale_x, float fill, int staged, int G, int lgG) {
@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256)
     const TY *ybase = y;
     int64_t ylo = 0;
     if constexpr (YS) {
-      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (256 >> lgG) * A.KK : 0));
+      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (blockDim.x >> lgG) * A.KK : 0));
       ylo = stage_window<TY>(A, y, ys, lgG);
       ybase = ys;
     }
@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(256)
 // forward (w = attn, y = value) and the QK backward's dq (w = dlogits,
 // y = key, post = the query scale).
 template <typename TY, typename TO, int VEC, bool YS>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_rpb_gather(RpbProb A, const float *__restrict__ w,
                  const TY *__restrict__ y, TO *__restrict__ out, float post,
                  int staged, int G, int lgG) {
@@ -359,7 +359,7 @@ __global__ void __launch_bounds__(256)
     const TY *ybase = y;
     int64_t ylo = 0;
     if constexpr (YS) {
-      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (256 >> lgG) * A.KK : 0));
+      TY *ys = reinterpret_cast<TY *>(stage + (staged ? (blockDim.x >> lgG) * A.KK : 0));
       ylo = stage_window<TY>(A, y, ys, lgG);
       ybase = ys;
     }
@@ -590,9 +590,23 @@ RShape rshape(int D, int vmax) {
   return s;
 }
 
-dim3 rgrid(const RpbProb &A, int lgG) {
+dim3 rgrid(const RpbProb &A, int lgG, int rb = 256) {
   const int64_t threads = (int64_t)A.n_rows << lgG;
-  return dim3((unsigned)((threads + 255) / 256));
+  return dim3((unsigned)((threads + rb - 1) / rb));
+}
+
+// Threads per block of the forward gathers (k_rpb_dot / k_rpb_gather):
+// 512 when the window reach K0 * d0 is at least 7 (the halo then weighs
+// on a 256-row block: measured at D = 12, K in {3, 5, 7}, d in {1..8}),
+// 256 otherwise; NATTEN_AMD_RPB_BLOCK overrides it (tuning).
+int rpb_block(const RpbProb &A) {
+  static const int forced = [] {
+    const char *e = std::getenv("NATTEN_AMD_RPB_BLOCK");
+    const int v = e != nullptr ? std::atoi(e) : 0;
+    return v == 64 || v == 128 || v == 256 || v == 512 ? v : 0;
+  }();
+  if (forced > 0) return forced;
+  return A.rank == 1 && A.K0 * A.d0 >= 7 ? 512 : 256;
 }
 
 template <typename A_, typename B_>
@@ -600,10 +614,10 @@ constexpr int vmax_of() {
   return 16 / (int)(sizeof(A_) > sizeof(B_) ? sizeof(A_) : sizeof(B_));
 }
 
-// LDS for a block's slot rows (256 / G rows of KK floats), or 0 when that
+// LDS for a block's slot rows (rb / G rows of KK floats), or 0 when that
 // exceeds 32 KB and the rows go straight to memory.
-size_t stage_bytes(const RpbProb &A, int lgG) {
-  const size_t b = (size_t)(256 >> lgG) * A.KK * sizeof(float);
+size_t stage_bytes(const RpbProb &A, int lgG, int rb) {
+  const size_t b = (size_t)(rb >> lgG) * A.KK * sizeof(float);
   return b <= 32768 ? b : 0;
 }
 
@@ -611,12 +625,12 @@ size_t stage_bytes(const RpbProb &A, int lgG) {
 // rows must be whole 16-byte units, the halo at most the block's rows and
 // the window must fit with the slot staging in 64 KB.
 template <typename TY>
-size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes) {
+size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes, int rb) {
   if (A.rank != 1 || (A.D * sizeof(TY)) % 16 != 0) return 0;
   // only worth it while the halo is no larger than the block's own rows
   // (large dilations would mostly copy other phases' rows)
-  if (window_rows(A, lgG) > 2 * (int64_t)(256 >> lgG)) return 0;
-  const size_t b = (size_t)window_rows(A, lgG) * A.D * sizeof(TY);
+  if (window_rows(A, lgG, rb) > 2 * (int64_t)(rb >> lgG)) return 0;
+  const size_t b = (size_t)window_rows(A, lgG, rb) * A.D * sizeof(TY);
   return slot_bytes + b <= 65536 ? b : 0;
 }
 
@@ -626,11 +640,12 @@ void launch_dot(const RpbProb &A, const void *x, const void *y,
                 hipStream_t st) {
   constexpr int V = vmax_of<TX, TY>();
   const RShape s = rshape(A.D, V);
-  const size_t lds = stage_bytes(A, s.lgG);
+  const int rb = rpb_block(A);
+  const size_t lds = stage_bytes(A, s.lgG, rb);
   const int staged = lds > 0;
-  const size_t wb = window_bytes<TY>(A, s.lgG, lds);
+  const size_t wb = window_bytes<TY>(A, s.lgG, lds, rb);
 #define DOT_(VV, YS)                                                          \
-  hipLaunchKernelGGL((k_rpb_dot<TX, TY, VV, YS>), rgrid(A, s.lgG), dim3(256), \
+  hipLaunchKernelGGL((k_rpb_dot<TX, TY, VV, YS>), rgrid(A, s.lgG, rb), dim3(rb), \
                      lds + wb, st, A, (const TX *)x, (const TY *)y, rpb, out,  \
                      scale_x, fill, staged, s.G, s.lgG)
   if (s.vec == V) {
@@ -646,12 +661,13 @@ void launch_gather(const RpbProb &A, const float *w, const void *y, void *out,
                    float post, hipStream_t st) {
   constexpr int V = vmax_of<TY, TO>();
   const RShape s = rshape(A.D, V);
-  const size_t lds = stage_bytes(A, s.lgG);
+  const int rb = rpb_block(A);
+  const size_t lds = stage_bytes(A, s.lgG, rb);
   const int staged = lds > 0;
-  const size_t wb = window_bytes<TY>(A, s.lgG, lds);
+  const size_t wb = window_bytes<TY>(A, s.lgG, lds, rb);
 #define GAT_(VV, YS)                                                          \
-  hipLaunchKernelGGL((k_rpb_gather<TY, TO, VV, YS>), rgrid(A, s.lgG),         \
-                     dim3(256), lds + wb, st, A, w, (const TY *)y, (TO *)out,  \
+  hipLaunchKernelGGL((k_rpb_gather<TY, TO, VV, YS>), rgrid(A, s.lgG, rb),     \
+                     dim3(rb), lds + wb, st, A, w, (const TY *)y, (TO *)out,   \
                      post, staged, s.G, s.lgG)
   if (s.vec == V) {
     if (wb > 0) GAT_(V, true); else GAT_(V, false);
