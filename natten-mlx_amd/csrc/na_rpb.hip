@@ -405,6 +405,47 @@ __global__ void __launch_bounds__(256)
   for (int t = 0; t < kNT; ++t)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[t][e] = 0.f;
+  if (A.rank == 1) {
+    // candidates i0 = i + t d, |t| <= K, in batches of four: the batch's
+    // window tests first, then every load of the batch, then the FMAs
+    const int64_t step = A.heads_first ? 1 : A.H;
+    for (int32_t tb = -A.K0; tb <= A.K0; tb += 4) {
+      float wt[4];
+      float xv[4][kNT][VEC];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int32_t t0 = tb + u;
+        const int32_t i0 = p.i0 + t0 * A.d0;
+        bool ok = t0 <= A.K0 && i0 >= 0 && i0 < A.L0;
+        int32_t k0 = 0;
+        if (ok) {
+          const RWin w0 = rwin0(A, i0);
+          ok = p.i0 >= w0.s && p.i0 < w0.e;
+          k0 = (int32_t)fdiv((uint32_t)(p.i0 - w0.s), A.fd0);
+        }
+        const int64_t r = g.id + (int64_t)t0 * A.d0 * step;
+        wt[u] = ok ? w[r * A.KK + k0] : 0.f;
+        if (ok) {
+          ld_row<TX, VEC>(xv[u], x + r * A.D, g.lane, G, A.D);
+        } else {
+#pragma unroll
+          for (int t = 0; t < kNT; ++t)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) xv[u][t][e] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (scale_x) scale_round<TX, VEC>(xv[u], A.scale);
+#pragma unroll
+        for (int t = 0; t < kNT; ++t)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[t][e] = fmaf(wt[u], xv[u][t][e], acc[t][e]);
+      }
+    }
+    if (g.live) st_row<TO, VEC>(out + g.id * A.D, acc, 1.f, g.lane, G, A.D);
+    return;
+  }
   const int32_t t1max = A.rank == 2 ? A.K1 : 0;
   for (int32_t t0 = -A.K0; t0 <= A.K0; ++t0) {
     const int32_t i0 = p.i0 + t0 * A.d0;
