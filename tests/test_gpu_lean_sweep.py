@@ -1,0 +1,135 @@
+"""Seeded sweep of the lean workgroup kernels over random problems of their
+class (ranks 1-3, odd kernels with d*K <= L on every axis, causal axes,
+GQA, head_dim 32/64/128, bf16/fp16), forward + LSE + backward against the
+float64 oracle; and the lean forward with per-sample extents and additional
+tokens.  Every case asserts it ran on the lean kernels.  Runs on an MI355X.
+"""
+
+import random
+import sys
+
+import pytest
+import torch
+
+from _helpers import DEV, assert_close, randn
+from oracle import na as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _problem(rng):
+    rank = rng.choice((1, 1, 2, 2, 2, 3))
+    ks, dil, caus, sp = [], [], [], []
+    for a in range(rank):
+        causal = rng.random() < 0.25
+        K = rng.choice((3, 5, 7) if rank < 3 else (3, 5))
+        d = rng.choice((1, 1, 2, 3))
+        hi = 40 if rank == 1 else 20 if rank == 2 else 10
+        L = rng.randint(min(d * K, hi), hi)
+        if d * K > L:  # the API requires d * K <= L on every axis
+            d = 1
+        ks.append(K)
+        dil.append(d)
+        caus.append(causal)
+        sp.append(L)
+    if rank == 1:
+        sp = [rng.randint(max(ks[0] * dil[0], 20), 300)]
+    hkv = rng.choice((1, 2))
+    H = hkv * rng.choice((1, 2, 4))
+    D = rng.choice((32, 64, 128))
+    dtype = rng.choice((torch.bfloat16, torch.float16))
+    B = rng.choice((1, 2))
+    return B, tuple(sp), H, hkv, D, tuple(ks), tuple(dil), tuple(caus), dtype
+
+
+CASES = [_problem(random.Random(1000 + i)) for i in range(24)]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"p{i}" for i in range(len(CASES))])
+def test_lean_random_problem(case):
+    import natten_amd
+    from natten_amd._core import hip
+
+    B, sp, H, Hkv, D, ks, dil, caus, dtype = case
+    _say(f"[case] lean sweep {case}")
+    st = (1,) * len(sp)
+    q = randn((B, *sp, H, D), dtype, 51)
+    k = randn((B, *sp, Hkv, D), dtype, 52)
+    v = randn((B, *sp, Hkv, D), dtype, 53)
+    go = randn((B, *sp, H, D), dtype, 54)
+    gl = randn((B, *sp, H), dtype, 55)
+    if hip.kernel_path(q, k, ks, st, dil, caus) != "lean":
+        pytest.skip("outside the lean class (LDS budget)")
+    fn = {1: natten_amd.na1d, 2: natten_amd.na2d, 3: natten_amd.na3d}[len(sp)]
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    out, lse = fn(*ts, kernel_size=ks, dilation=dil, is_causal=caus, return_lse=True)
+    torch.autograd.backward((out, lse), (go.to(DEV), gl.to(DEV)))
+    ref_out, ref_lse = O.na_functional(q, k, v, ks, 1, dil, caus, return_lse=True)
+    assert_close(out, ref_out, dtype, "out")
+    assert_close(lse, ref_lse, dtype, "lse")
+    lean_bwd = hip.kernel_path(q, k, ks, st, dil, caus, backward=True) == "lean"
+    ref = O.grads(lambda a, b, c: O.na_functional(a, b, c, ks, 1, dil, caus, return_lse=True),
+                  (q, k, v), (go, gl))
+    for t, r, nm in zip(ts, ref, ("dq", "dk", "dv")):
+        assert_close(t.grad, r, dtype, f"{nm} (lean backward: {lean_bwd})")
+
+
+def _vx_problem(rng):
+    rank = rng.choice((1, 1, 2))
+    ks, dil, sp = [], [], []
+    for a in range(rank):
+        K = rng.choice((3, 5, 7, 9))
+        d = rng.choice((1, 2))
+        L = rng.randint(d * K + 4, 64 if rank == 2 else 200)
+        ks.append(K)
+        dil.append(d)
+        sp.append(L)
+    B = rng.choice((2, 3))
+    sizes = [[rng.randint(d * K, L) for K, d, L in zip(ks, dil, sp)] for _ in range(B)]
+    sizes[0] = list(sp)
+    nx = rng.choice((0, 1, 5, 16, 33))
+    hkv = rng.choice((1, 2))
+    return (B, tuple(sp), hkv * rng.choice((1, 2)), hkv, rng.choice((32, 64)), tuple(ks),
+            tuple(dil), sizes, nx, rng.choice((torch.bfloat16, torch.float16)))
+
+
+VX_CASES = [_vx_problem(random.Random(2000 + i)) for i in range(12)]
+
+
+@pytest.mark.parametrize("case", VX_CASES, ids=[f"v{i}" for i in range(len(VX_CASES))])
+def test_lean_random_varlen_extra_forward(case):
+    from natten_amd._core import hip
+
+    B, sp, H, Hkv, D, ks, dil, sizes, nx, dtype = case
+    _say(f"[case] lean vx sweep {case}")
+    rank = len(sp)
+    caus = (False,) * rank
+    st = (1,) * rank
+    q = randn((B, *sp, H, D), dtype, 61)
+    k = randn((B, *sp, Hkv, D), dtype, 62)
+    v = randn((B, *sp, Hkv, D), dtype, 63)
+    ek = randn((B, nx, Hkv, D), dtype, 64) if nx else None
+    ev = randn((B, nx, Hkv, D), dtype, 65) if nx else None
+    se = torch.tensor(sizes, dtype=torch.int32)
+    assert hip.kernel_path(q, k, ks, st, dil, caus, n_extra=nx, sample_extent=se,
+                           varlen_clamped=True) == "lean"
+    dev = [None if t is None else t.to(DEV) for t in (q, k, v, ek, ev, se)]
+    out, lse = hip.fused_forward(dev[0], dev[1], dev[2], ks, st, dil, caus, None,
+                                 extra_k=dev[3], extra_v=dev[4], sample_extent=dev[5],
+                                 varlen_clamped=True)
+    for b in range(B):
+        sl = (slice(b, b + 1),) + tuple(slice(0, e) for e in sizes[b])
+        ro, rl = O.na_functional(q[sl], k[sl], v[sl], ks, 1, dil, caus, return_lse=True,
+                                 additional_keys=None if ek is None else ek[b:b + 1],
+                                 additional_values=None if ev is None else ev[b:b + 1])
+        assert_close(out[sl], ro, dtype, f"out b{b}")
+        assert_close(lse[sl].to(dtype), rl, dtype, f"lse b{b}")
+        pad = torch.ones(sp, dtype=torch.bool)
+        pad[tuple(slice(0, e) for e in sizes[b])] = False
+        pad = pad.to(DEV)
+        assert (out[b][pad] == 0).all() and (lse[b][pad] == 0).all()
