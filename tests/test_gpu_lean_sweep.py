@@ -133,3 +133,50 @@ def test_lean_random_varlen_extra_forward(case):
         pad[tuple(slice(0, e) for e in sizes[b])] = False
         pad = pad.to(DEV)
         assert (out[b][pad] == 0).all() and (lse[b][pad] == 0).all()
+
+
+SPLIT_CASES = [_problem(random.Random(3000 + i)) for i in range(12)]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"s{i}" for i in range(len(SPLIT_CASES))])
+def test_lean_random_split_ops(case):
+    """Split QK / AV forward and all four gradients on the lean split
+    kernels (k_lqk, k_lav, k_linv) against the oracle."""
+    import natten_amd
+    from natten_amd._core import hip
+
+    B, sp, H, Hkv, D, ks, dil, caus, dtype = case
+    _say(f"[case] lean split sweep {case}")
+    rank = len(sp)
+    q = randn((B, *sp, H, D), dtype, 71)
+    k = randn((B, *sp, Hkv, D), dtype, 72)
+    v = randn((B, *sp, Hkv, D), dtype, 73)
+    if hip.kernel_path(q, k, ks, (1,) * rank, dil, caus, split=True) != "lean":
+        pytest.skip("outside the lean split class (LDS budget)")
+    qk = {1: natten_amd.na1d_qk, 2: natten_amd.na2d_qk, 3: natten_amd.na3d_qk}[rank]
+    av = {1: natten_amd.na1d_av, 2: natten_amd.na2d_av, 3: natten_amd.na3d_av}[rank]
+    ref_logits = O.na_qk(q, k, ks, 1, dil, caus, 0.3)
+    finite = torch.isfinite(ref_logits)
+    attn = torch.softmax(ref_logits, -1).to(dtype)
+    gl = randn(ref_logits.shape, dtype, 74)
+    go = randn((B, *sp, H, D), dtype, 75)
+
+    def qk_masked(a, b):
+        x = O.na_qk(a, b, ks, 1, dil, caus, 0.3)
+        return torch.where(finite, x, torch.zeros_like(x))
+
+    rq, rk = O.grads(qk_masked, (q, k), (gl,))
+    ra, rv = O.grads(lambda a, b: O.na_av(a, b, ks, 1, dil, caus), (attn, v), (go,))
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    logits = qk(qd, kd, ks, dil, is_causal=caus, scale=0.3)
+    assert torch.equal(torch.isinf(logits).cpu(), ~finite), "mask"
+    assert_close(logits, ref_logits, dtype, "logits")
+    ad = attn.to(DEV).requires_grad_(True)
+    out = av(ad, vd, ks, dil, is_causal=caus)
+    assert_close(out, O.na_av(attn, v, ks, 1, dil, caus), dtype, "av")
+    logits.backward(gl.to(DEV))
+    out.backward(go.to(DEV))
+    assert_close(qd.grad, rq, dtype, "dq")
+    assert_close(kd.grad, rk, dtype, "dk")
+    assert_close(ad.grad, ra, dtype, "dattn")
+    assert_close(vd.grad, rv, dtype, "dv")
