@@ -138,6 +138,13 @@ bool use_msplit(const na_params *p, const na::Prob &P) {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+size_t delta_bytes(const na::Prob &P);
+
+// delta, then the extra-token gradient partials
+size_t bwd_workspace_bytes(const na::Prob &P) {
+  return delta_bytes(P) + align256(na::dextra_workspace_bytes(P));
+}
+
 size_t delta_bytes(const na::Prob &P) {
   return align256(sizeof(float) * (size_t)P.B * P.ax[0].O * P.ax[1].O *
                   P.ax[2].O * P.H);
@@ -323,7 +330,7 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
 size_t na_bwd_workspace_bytes(const na_params *p) {
   na::Prob P;
   if (make_prob(p, &P, true) != NA_OK) return 0;
-  return delta_bytes(P);
+  return bwd_workspace_bytes(P);
 }
 
 int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
@@ -342,27 +349,30 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                 "q/k/v/out/lse/dout/dq/dk/dv must be non-NULL");
   if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
     return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
-  if (workspace == nullptr || workspace_bytes < delta_bytes(P))
-    return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
-                delta_bytes(P), workspace == nullptr ? (size_t)0 : workspace_bytes);
+  const size_t need = bwd_workspace_bytes(P);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
   float *delta = static_cast<float *>(workspace);
+  float *xpart = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                           delta_bytes(P));
   const hipStream_t st = as_stream(stream);
+  const bool dextra =
+      P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
   if (use_lean_bwd(p, P)) {
     na::lean_bwd(P, p->dtype, q, k, v, out, lse, dout, dlse, dq, dk, dv, st);
   } else if (use_mfma(p, P)) {
-    const bool dextra =
-        P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
     if (dextra || na::mfma_bwd_reads_delta(P))
       na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::mfma_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
                  delta, dq, dk, dv, st);
-    if (dextra)
-      na::valu_dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout,
-                      d_extra_k, d_extra_v, st);
   } else {
     na::valu_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
-                 dq, dk, dv, d_extra_k, d_extra_v, delta, st);
+                 dq, dk, dv, delta, st);
   }
+  if (dextra)
+    na::dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout, d_extra_k,
+               d_extra_v, xpart, st);
   return launch_status("na_bwd");
 }
 

@@ -14,8 +14,7 @@ void valu_fwd(const Prob &P, int dtype, const void *q, const void *k,
 void valu_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, const void *out,
               const float *lse, const void *dout, const float *dlse, void *dq,
-              void *dk, void *dv, void *dek, void *dev, float *delta,
-              hipStream_t st);
+              void *dk, void *dv, float *delta, hipStream_t st);
 void valu_qk(const Prob &P, int dtype, const void *q, const void *k,
              void *logits, hipStream_t st);
 void valu_av(const Prob &P, int dtype, const void *attn, const void *v,
@@ -124,8 +123,15 @@ void merge_bwd(int dtype, int n, int64_t rows, int D, const void *const *outs,
 // Generic pieces reused around the MFMA backward.
 void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
                 const float *dlse, float *delta, hipStream_t st);
-void valu_dextra(const Prob &P, int dtype, const void *q, const void *ek,
-                 const void *ev, const float *lse, const float *delta,
-                 const void *dout, void *dek, void *dev, hipStream_t st);
+
+// Gradients of the additional tokens (na_dextra.hip): a two-pass segment
+// reduction over every query of the sample, reading delta (rowsum(dO * O) -
+// dlse per (query, head)); `part` is a float workspace of
+// dextra_workspace_bytes(P).
+size_t dextra_workspace_bytes(const Prob &P);
+void dextra(const Prob &P, int dtype, const void *q, const void *ek,
+            const void *ev, const float *lse, const float *delta,
+            const void *dout, void *dek, void *dev, float *part,
+            hipStream_t st);
 
 }  // namespace na

@@ -268,50 +268,6 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Gradients of the additional tokens: a sum over every query of the sample.
-template <typename T, int VEC, int NT>
-__global__ void __launch_bounds__(256)
-    k_dextra(Prob P, const T *__restrict__ q, const T *__restrict__ ek,
-             const T *__restrict__ ev, const float *__restrict__ lse,
-             const float *__restrict__ delta, const T *__restrict__ dout,
-             T *__restrict__ dek, T *__restrict__ dev, int G, int lgG,
-             int64_t n_groups) {
-  const Group g = make_group(lgG, n_groups);
-  // g.id = (b * n_extra + n) * Hkv + hk  ==  row index of the token.
-  const int hk = (int)(g.id % P.Hkv);
-  const int b = (int)(g.id / ((int64_t)P.Hkv * P.n_extra));
-  int32_t L[3], O[3];
-  sample_extents(P, b, L, O);
-  const int D = P.D;
-  const float sl2 = P.scale * kLog2e;
-  Row<T, VEC, NT> kr, vr, dka, dva;
-  dka.zero();
-  dva.zero();
-  kr.load(ek + g.id * D, g.lane, G, D);
-  vr.load(ev + g.id * D, g.lane, G, D);
-  for (int32_t o0 = 0; o0 < O[0]; ++o0)
-    for (int32_t o1 = 0; o1 < O[1]; ++o1)
-      for (int32_t o2 = 0; o2 < O[2]; ++o2) {
-        const int64_t qt =
-            tok_in(P, b, o0 * P.ax[0].s, o1 * P.ax[1].s, o2 * P.ax[2].s);
-        const int64_t ot = tok_out(P, b, o0, o1, o2);
-        for (int h = hk * P.rep; h < (hk + 1) * P.rep; ++h) {
-          const T *qrow = q + (qt * P.H + h) * D;
-          const T *drow = dout + (ot * P.H + h) * D;
-          const float s = group_sum(kr.dot_mem(qrow, g.lane, G, D), G);
-          const float dp = group_sum(vr.dot_mem(drow, g.lane, G, D), G);
-          const float pr = exp2f(fmaf(s, sl2, -lse[ot * P.H + h] * kLog2e));
-          const float ds = pr * (dp - delta[ot * P.H + h]);
-          dva.scale_add_mem(1.f, pr, drow, g.lane, G, D);
-          dka.scale_add_mem(1.f, ds, qrow, g.lane, G, D);
-        }
-      }
-  dka.mul(P.scale);
-  if (g.live) {
-    dka.store(dek + g.id * D, g.lane, G, D);
-    dva.store(dev + g.id * D, g.lane, G, D);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Split operators.  Slot n of the last logits axis is row-major over
@@ -567,7 +523,7 @@ template <typename T>
 void bwd_t(const Prob &P, const void *q, const void *k, const void *v,
            const void *ek, const void *ev, const void *out, const float *lse,
            const void *dout, const float *dlse, void *dq, void *dk, void *dv,
-           void *dek, void *dev, float *delta, hipStream_t st) {
+           float *delta, hipStream_t st) {
   const Shape s = pick_shape<T>(P.D);
   const int64_t n_out = (int64_t)P.B * P.ax[0].O * P.ax[1].O * P.ax[2].O * P.H;
   const int64_t n_in_q = (int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L * P.H;
@@ -586,13 +542,6 @@ void bwd_t(const Prob &P, const void *q, const void *k, const void *v,
                        dim3(256), 0, st, P, (const TT *)q, (const TT *)k,     \
                        (const TT *)v, lse, delta, (const TT *)dout,           \
                        (TT *)dk, (TT *)dv, s.G, s.lgG, n_in_kv);              \
-    if (P.n_extra > 0 && dek != nullptr && dev != nullptr) {                  \
-      const int64_t n_ex = (int64_t)P.B * P.n_extra * P.Hkv;                  \
-      hipLaunchKernelGGL((k_dextra<TT, V, N>), grid_for(n_ex, s.lgG),         \
-                         dim3(256), 0, st, P, (const TT *)q, (const TT *)ek,  \
-                         (const TT *)ev, lse, delta, (const TT *)dout,        \
-                         (TT *)dek, (TT *)dev, s.G, s.lgG, n_ex);             \
-    }                                                                         \
   } while (0)
   NA_VALU_DISPATCH(T, s, L_);
 #undef L_
@@ -607,21 +556,6 @@ void delta_t(const Prob &P, const void *out, const void *dout, const float *dlse
   hipLaunchKernelGGL((k_delta<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
                      st, P, (const TT *)out, (const TT *)dout, dlse, delta,  \
                      s.G, s.lgG, n)
-  NA_VALU_DISPATCH(T, s, L_);
-#undef L_
-}
-
-template <typename T>
-void dextra_t(const Prob &P, const void *q, const void *ek, const void *ev,
-              const float *lse, const float *delta, const void *dout, void *dek,
-              void *dev, hipStream_t st) {
-  const Shape s = pick_shape<T>(P.D);
-  const int64_t n = (int64_t)P.B * P.n_extra * P.Hkv;
-#define L_(TT, V, N)                                                          \
-  hipLaunchKernelGGL((k_dextra<TT, V, N>), grid_for(n, s.lgG), dim3(256), 0, \
-                     st, P, (const TT *)q, (const TT *)ek, (const TT *)ev,    \
-                     lse, delta, (const TT *)dout, (TT *)dek, (TT *)dev, s.G, \
-                     s.lgG, n)
   NA_VALU_DISPATCH(T, s, L_);
 #undef L_
 }
@@ -703,21 +637,14 @@ void valu_fwd(const Prob &P, int dtype, const void *q, const void *k,
 void valu_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, const void *out,
               const float *lse, const void *dout, const float *dlse, void *dq,
-              void *dk, void *dv, void *dek, void *dev, float *delta,
-              hipStream_t st) {
+              void *dk, void *dv, float *delta, hipStream_t st) {
   NA_BY_DTYPE(dtype, bwd_t, P, q, k, v, ek, ev, out, lse, dout, dlse, dq, dk,
-              dv, dek, dev, delta, st);
+              dv, delta, st);
 }
 
 void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
                 const float *dlse, float *delta, hipStream_t st) {
   NA_BY_DTYPE(dtype, delta_t, P, out, dout, dlse, delta, st);
-}
-
-void valu_dextra(const Prob &P, int dtype, const void *q, const void *ek,
-                 const void *ev, const float *lse, const float *delta,
-                 const void *dout, void *dek, void *dev, hipStream_t st) {
-  NA_BY_DTYPE(dtype, dextra_t, P, q, ek, ev, lse, delta, dout, dek, dev, st);
 }
 
 void valu_qk(const Prob &P, int dtype, const void *q, const void *k,

@@ -250,3 +250,61 @@ def test_backward_is_deterministic():
         grads.append([t.grad.clone() for t in ts])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_varlen_gqa_extra_gradients(dtype):
+    """Gradients of q, k, v and of the additional tokens under varlen + GQA
+    (4 query heads per key/value head, 21 tokens: two token tiles), against
+    the oracle summed over per-sample calls; the extra-token gradients
+    reduce over every query of a sample."""
+    import natten_amd
+
+    _say(f"[case] varlen gqa extra gradients {dtype}")
+    B, L, H, Hkv, D, nx = 3, 150, 8, 2, 32, 21
+    q, k, v = _inputs(B, (L,), H, Hkv, D, dtype, 81)
+    ek, ev = randn((B, nx, Hkv, D), dtype, 84), randn((B, nx, Hkv, D), dtype, 85)
+    lens = torch.tensor([150, 97, 40], dtype=torch.int32)
+    go = randn((B, L, H, D), dtype, 86)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, ek, ev)]
+    out = natten_amd.na1d_varlen_gqa(ts[0], ts[1], ts[2], lens.to(DEV), 7, 2,
+                                     additional_keys=ts[3], additional_values=ts[4])
+    out.backward(go.to(DEV))
+    ref = [torch.zeros(t.shape, dtype=torch.float64) for t in (q, k, v, ek, ev)]
+    for b in range(B):
+        Lb = int(lens[b])
+        sl = (slice(b, b + 1), slice(0, Lb))
+        g = O.grads(lambda a, c, d, e, f: O.na_functional(a, c, d, 7, 1, 2, False,
+                                                          additional_keys=e,
+                                                          additional_values=f),
+                    (q[sl], k[sl], v[sl], ek[b:b + 1], ev[b:b + 1]), (go[sl],))
+        for r, gg, s in zip(ref, g, (sl, sl, sl, slice(b, b + 1), slice(b, b + 1))):
+            r[s] = gg.to(torch.float64)
+    for t, r, nm in zip(ts, ref, ("dq", "dk", "dv", "dek", "dev")):
+        assert_close(t.grad, r, dtype, nm)
+
+
+@pytest.mark.parametrize("D", [6, 264, 520, 1024])
+def test_extra_gradients_head_dims(D):
+    """Extra-token gradients at head_dims that change the reduction's tiling:
+    not a multiple of 4 (zero-padded rows), and above 256 (eight, then four
+    tokens per tile), with GQA and a stride, against the oracle."""
+    import natten_amd
+
+    dtype = torch.float16
+    _say(f"[case] extra gradients head_dim {D}")
+    B, L, H, Hkv, nx = 2, 30, 4, 2, 11
+    q, k, v = _inputs(B, (L,), H, Hkv, D, dtype, 91)
+    ek, ev = randn((B, nx, Hkv, D), dtype, 94), randn((B, nx, Hkv, D), dtype, 95)
+    go = randn((B, 15, H, D), dtype, 96)
+
+    def f(a, c, d, e, g):
+        return O.na_functional(a, c, d, 5, 2, 1, False, additional_keys=e, additional_values=g)
+
+    ref = O.grads(f, (q, k, v, ek, ev), (go,))
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, ek, ev)]
+    out = natten_amd.na1d(ts[0], ts[1], ts[2], 5, stride=2, additional_keys=ts[3],
+                          additional_values=ts[4])
+    out.backward(go.to(DEV))
+    for t, r, nm in zip(ts, ref, ("dq", "dk", "dv", "dek", "dev")):
+        assert_close(t.grad, r, dtype, nm)
