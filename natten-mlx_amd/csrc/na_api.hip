@@ -372,7 +372,7 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
   }
   if (dextra)
     na::dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout, d_extra_k,
-               d_extra_v, xpart, st);
+               d_extra_v, xpart, (p->flags & NA_FLAG_GENERIC) == 0, st);
   return launch_status("na_bwd");
 }
 

@@ -21,6 +21,7 @@
 
 #include "na_common.h"
 #include "na_launch.h"
+#include "na_lean.h"
 
 namespace na {
 namespace {
@@ -126,6 +127,8 @@ __global__ void __launch_bounds__(kXThreads)
   const int br = 2 * (tid / TP), be = 2 * (tid % TP);
 
   const int O12 = P.ax[1].O * P.ax[2].O;
+  // rows past the sample's extent on the first axis are all outside it
+  nrows = min(nrows, (int64_t)O[0] * O12 * P.rep);
   for (int ci = 0; ci < nper; ++ci) {
     const int64_t r0 = ((int64_t)sg * nper + ci) * rw;
     if (r0 >= nrows) break;  // uniform
@@ -280,18 +283,222 @@ __global__ void __launch_bounds__(kXThreads)
   dev[i] = from_f32<T>(v);
 }
 
+// Matrix-core variant (bf16 / fp16, head_dim 32, 64 or 128; 16 tokens per
+// tile).  Each wave takes 32 rows at a time: it gathers their q and dO rows
+// into its own LDS slice ([32][D + 8]), computes S = q ek^T and dP = dO ev^T
+// for two 16-row blocks on mfma_f32_16x16x32 (ek / ev of the tile live in
+// registers as the B operand), forms P and dS in the accumulator layout
+// (lane: token l % 16, rows 4 (l / 16) + r) and packs them, rounded to the
+// input type, as the B operand of dek^T += q^T dS and dev^T += dO^T P, whose
+// A operand is read from the staged rows with the transposing LDS read.  The
+// four waves' sums are added in LDS in wave order at the end.
+constexpr int kXMRows = 128;  // rows per workgroup step (4 waves x 32)
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+    k_xmfma(Prob P, const T *__restrict__ q, const T *__restrict__ ek,
+            const T *__restrict__ ev, const float *__restrict__ lse,
+            const float *__restrict__ delta, const T *__restrict__ dout,
+            float *__restrict__ part, int ntt, int nsg, int nper, int64_t nrows) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int RS = D + 8, NKB = D / 32, NDB = D / 16, UPL = D / 16, C8 = D / 8;
+  extern __shared__ __align__(16) char xsm[];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  E *sq = reinterpret_cast<E *>(xsm) + w * 2 * 32 * RS;
+  E *sd = sq + 32 * RS;
+
+  int wg = blockIdx.x;
+  const int sg = wg % nsg;
+  wg /= nsg;
+  const int tt = wg % ntt;
+  wg /= ntt;
+  const int hk = wg % P.Hkv;
+  const int b = wg / P.Hkv;
+  int32_t L[3], O[3];
+  sample_extents(P, b, L, O);
+  const int O12 = P.ax[1].O * P.ax[2].O;
+  nrows = min(nrows, (int64_t)O[0] * O12 * P.rep);
+  const int e0 = tt * 16;
+  const int ne = min(16, P.n_extra - e0);
+  const float sl2 = P.scale * kLog2e;
+  v8 zero;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zero[i] = (E)0.f;
+  // the tile's ek / ev as the B operand: token n, columns 32 kb + 8 g + i
+  v8 bk[NKB], bv[NKB];
+  {
+    const int64_t row = (((int64_t)b * P.n_extra + e0 + n) * P.Hkv + hk) * D + 8 * g;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      bk[kb] = n < ne ? *reinterpret_cast<const v8 *>(ek + row + 32 * kb) : zero;
+      bv[kb] = n < ne ? *reinterpret_cast<const v8 *>(ev + row + 32 * kb) : zero;
+    }
+  }
+  f32x4 adk[NDB], adv[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) {
+    adk[j] = zero4();
+    adv[j] = zero4();
+  }
+  const int tr_off = (4 * g + (n >> 2)) * RS + 4 * (n & 3);
+
+  for (int ci = 0; ci < nper; ++ci) {
+    const int64_t r0 = ((int64_t)sg * nper + ci) * kXMRows + 32 * w;
+    if (r0 >= nrows) break;  // wave-uniform; no workgroup barrier in the loop
+    // lanes 0..31 decode the wave's rows: q / dO offsets, lse * log2(e)
+    // (+inf outside the sample: P = 0), delta
+    int64_t qo = -1, dof = -1;
+    float l2 = INFINITY, dl = 0.f;
+    if (lane < 32) {
+      const int64_t ri = r0 + lane;
+      bool ok = ri < nrows;
+      const int64_t of = ok ? ri / P.rep : 0;
+      const int hr = (int)(ri - of * P.rep);
+      const int o0 = (int)(of / O12);
+      const int rem = (int)(of - (int64_t)o0 * O12);
+      const int o1 = rem / P.ax[2].O;
+      const int o2 = rem - o1 * P.ax[2].O;
+      ok = ok && o0 < O[0] && o1 < O[1] && o2 < O[2];
+      const int h = hk * P.rep + hr;
+      if (ok) {
+        const int64_t qt = tok_in(P, b, o0 * P.ax[0].s, o1 * P.ax[1].s, o2 * P.ax[2].s);
+        const int64_t ot = tok_out(P, b, o0, o1, o2);
+        qo = (qt * P.H + h) * D;
+        dof = (ot * P.H + h) * D;
+        l2 = lse[ot * P.H + h] * kLog2e;
+        dl = delta[ot * P.H + h];
+      }
+    }
+    // gather the 32 q and dO rows: 16-byte units u = lane + 64 j
+    v8 xq[UPL], xd[UPL];
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
+      const int64_t a = __shfl(qo, row), c = __shfl(dof, row);
+      xq[j] = a >= 0 ? *reinterpret_cast<const v8 *>(q + a + 8 * c8) : zero;
+      xd[j] = c >= 0 ? *reinterpret_cast<const v8 *>(dout + c + 8 * c8) : zero;
+    }
+    wave_lds_sync();  // the previous step's reads of the slice are done
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
+      *reinterpret_cast<v8 *>(sq + row * RS + 8 * c8) = xq[j];
+      *reinterpret_cast<v8 *>(sd + row * RS + 8 * c8) = xd[j];
+    }
+    wave_lds_sync();
+    v8 bp, bds;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      f32x4 s = zero4(), dp = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int off = (16 * h + n) * RS + 32 * kb + 8 * g;
+        s = M::mma(*reinterpret_cast<const v8 *>(sq + off), bk[kb], s);
+        dp = M::mma(*reinterpret_cast<const v8 *>(sd + off), bv[kb], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * h + 4 * g + r;
+        const float l2r = __shfl(l2, row), dlr = __shfl(dl, row);
+        const float p = n < ne ? exp2f(fmaf(s[r], sl2, -l2r)) : 0.f;
+        bp[4 * h + r] = (E)p;
+        bds[4 * h + r] = (E)(p * (dp[r] - dlr));
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const v4 q0 = M::tr(sq + tr_off + 16 * db), q1 = M::tr(sq + 16 * RS + tr_off + 16 * db);
+      const v4 o0 = M::tr(sd + tr_off + 16 * db), o1 = M::tr(sd + 16 * RS + tr_off + 16 * db);
+      adk[db] = M::mma(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), bds, adk[db]);
+      adv[db] = M::mma(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), bp, adv[db]);
+    }
+  }
+  // the four waves' sums, added in wave order: red[w][2][16][D]
+  __syncthreads();
+  float *red = reinterpret_cast<float *>(xsm);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = 16 * db + 4 * g + r;
+      red[(w * 2 * 16 + n) * D + c] = adk[db][r];
+      red[(w * 2 * 16 + 16 + n) * D + c] = adv[db][r];
+    }
+  __syncthreads();
+  float *dst = part + (((int64_t)(b * P.Hkv + hk) * ntt + tt) * nsg + sg) * 2 * 16 * D;
+  for (int i = threadIdx.x; i < 2 * 16 * D; i += 256) {
+    float acc = red[i];
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) acc += red[ww * 2 * 16 * D + i];
+    dst[i] = acc;
+  }
+}
+
+bool xmfma_ok(const Prob &P, int dtype) {
+  return dtype != NA_F32 && (P.D == 32 || P.D == 64 || P.D == 128);
+}
+
+XPlan xplan_mfma(const Prob &P) {
+  XPlan x;
+  x.xt = 16;
+  x.rw = kXMRows;
+  x.ntt = (P.n_extra + 15) / 16;
+  x.nrows = (int64_t)P.ax[0].O * P.ax[1].O * P.ax[2].O * P.rep;
+  const int64_t nchunk = (x.nrows + kXMRows - 1) / kXMRows;
+  const int64_t base = (int64_t)P.B * P.Hkv * x.ntt;
+  int64_t nsg = base > 0 ? (1024 + base - 1) / base : 1;
+  nsg = std::max<int64_t>(1, std::min<int64_t>(nsg, nchunk));
+  x.nper = (int)((nchunk + nsg - 1) / nsg);
+  x.nsg = (int)((nchunk + x.nper - 1) / x.nper);
+  x.part_floats = (size_t)base * x.nsg * 2 * 16 * P.D;
+  return x;
+}
+
 }  // namespace
 
 size_t dextra_workspace_bytes(const Prob &P) {
   if (P.n_extra <= 0) return 0;
-  return xplan(P).part_floats * sizeof(float);
+  // either variant (the choice depends on the dtype)
+  return std::max(xplan(P).part_floats, xplan_mfma(P).part_floats) * sizeof(float);
 }
 
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, void *dek, void *dev, float *part,
+            const void *dout, void *dek, void *dev, float *part, bool matrix,
             hipStream_t st) {
   if (P.n_extra <= 0 || P.B == 0) return;
+  if (matrix && xmfma_ok(P, dtype)) {
+    const XPlan x = xplan_mfma(P);
+    const size_t lds = (size_t)4 * 2 * 32 * (P.D + 8) * 2;
+    const unsigned g1 = (unsigned)((int64_t)P.B * P.Hkv * x.ntt * x.nsg);
+    const int64_t n2 = (int64_t)P.B * P.n_extra * P.Hkv * P.D;
+    const unsigned g2 = (unsigned)((n2 + kXThreads - 1) / kXThreads);
+#define XM_(TT, DD)                                                              \
+  hipLaunchKernelGGL((k_xmfma<TT, DD>), dim3(g1), dim3(256), lds, st, P,         \
+                     (const TT *)q, (const TT *)ek, (const TT *)ev, lse, delta,  \
+                     (const TT *)dout, part, x.ntt, x.nsg, x.nper, x.nrows)
+#define XMD_(TT)          \
+  do {                    \
+    if (P.D == 32)        \
+      XM_(TT, 32);        \
+    else if (P.D == 64)   \
+      XM_(TT, 64);        \
+    else                  \
+      XM_(TT, 128);       \
+    hipLaunchKernelGGL((k_xreduce<TT, 16>), dim3(g2), dim3(kXThreads), 0, st, P, \
+                       (const float *)part, (TT *)dek, (TT *)dev, x.ntt, x.nsg); \
+  } while (0)
+    if (dtype == NA_F16)
+      XMD_(f16_t);
+    else
+      XMD_(bf16_t);
+#undef XMD_
+#undef XM_
+    return;
+  }
   const XPlan x = xplan(P);
   const int DR = (P.D + 3) & ~3;
   const size_t lds = sizeof(float) * ((size_t)2 * x.rw * DR + (size_t)2 * x.xt * (DR + 4) +

@@ -127,11 +127,12 @@ void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
 // Gradients of the additional tokens (na_dextra.hip): a two-pass segment
 // reduction over every query of the sample, reading delta (rowsum(dO * O) -
 // dlse per (query, head)); `part` is a float workspace of
-// dextra_workspace_bytes(P).
+// dextra_workspace_bytes(P); `matrix` allows the matrix-core variant
+// (bf16 / fp16, head_dim 32 / 64 / 128).
 size_t dextra_workspace_bytes(const Prob &P);
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, void *dek, void *dev, float *part,
+            const void *dout, void *dek, void *dev, float *part, bool matrix,
             hipStream_t st);
 
 }  // namespace na

@@ -253,23 +253,29 @@ def test_backward_is_deterministic():
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
-def test_varlen_gqa_extra_gradients(dtype):
+@pytest.mark.parametrize("generic", [False, True], ids=["matrix", "generic"])
+def test_varlen_gqa_extra_gradients(dtype, generic):
     """Gradients of q, k, v and of the additional tokens under varlen + GQA
     (4 query heads per key/value head, 21 tokens: two token tiles), against
     the oracle summed over per-sample calls; the extra-token gradients
-    reduce over every query of a sample."""
-    import natten_amd
+    reduce over every query of a sample (matrix-core reduction for bf16 /
+    fp16, the vector-ALU one for fp32 and under generic_kernels())."""
+    import contextlib
 
-    _say(f"[case] varlen gqa extra gradients {dtype}")
+    import natten_amd
+    from natten_amd._core import hip
+
+    _say(f"[case] varlen gqa extra gradients {dtype} generic={generic}")
     B, L, H, Hkv, D, nx = 3, 150, 8, 2, 32, 21
     q, k, v = _inputs(B, (L,), H, Hkv, D, dtype, 81)
     ek, ev = randn((B, nx, Hkv, D), dtype, 84), randn((B, nx, Hkv, D), dtype, 85)
     lens = torch.tensor([150, 97, 40], dtype=torch.int32)
     go = randn((B, L, H, D), dtype, 86)
     ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, ek, ev)]
-    out = natten_amd.na1d_varlen_gqa(ts[0], ts[1], ts[2], lens.to(DEV), 7, 2,
-                                     additional_keys=ts[3], additional_values=ts[4])
-    out.backward(go.to(DEV))
+    with hip.generic_kernels() if generic else contextlib.nullcontext():
+        out = natten_amd.na1d_varlen_gqa(ts[0], ts[1], ts[2], lens.to(DEV), 7, 2,
+                                         additional_keys=ts[3], additional_values=ts[4])
+        out.backward(go.to(DEV))
     ref = [torch.zeros(t.shape, dtype=torch.float64) for t in (q, k, v, ek, ev)]
     for b in range(B):
         Lb = int(lens[b])
