@@ -383,6 +383,16 @@ def wl_cfg4(args):
                                                 extra_k=ak, extra_v=av, sample_extent=se,
                                                 varlen_clamped=True),
                       args.steps)
+    # the backward (dq, dk, dv and the additional tokens' gradients), timed
+    # alongside; not part of `value`
+    out, lse = hip.fused_forward(q, k, v, (63,), (1,), (2,), (False,), None, extra_k=ak,
+                                 extra_v=av, sample_extent=se, varlen_clamped=True)
+    do = _gen(out.shape, torch.float16, 6)
+    b_ms = time_calls(lambda: hip.fused_backward(q, k, v, out, lse, do, None, (63,), (1,),
+                                                 (2,), (False,), None, extra_k=ak,
+                                                 extra_v=av, sample_extent=se,
+                                                 varlen_clamped=True),
+                      args.steps)
     tokens = int(lens.sum())
     flops = tokens * H * 4 * Dc * (63 + nx)
     nbytes = tokens * (H * Dc * 2 + 2 * Hkv * Dc * 2 + H * Dc * 2) + 2 * Bc * nx * Hkv * Dc * 2
@@ -394,7 +404,8 @@ def wl_cfg4(args):
     return _line("na1d varlen gqa+extra fp16 fwd TFLOP/s, 1 MI355X",
                  flops / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "fp16", cfg, rf,
                  {"timing": {"fwd_call_ms": round(f_ms, 5),
-                             "call_tflops": round(flops / (f_ms * 1e-3) / 1e12, 3)}})
+                             "call_tflops": round(flops / (f_ms * 1e-3) / 1e12, 3),
+                             "bwd_call_ms": round(b_ms, 5)}})
 
 
 def wl_cfg5(args):

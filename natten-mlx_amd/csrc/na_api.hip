@@ -360,7 +360,9 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
   const bool dextra =
       P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
   if (use_lean_bwd(p, P)) {
-    na::lean_bwd(P, p->dtype, q, k, v, out, lse, dout, dlse, dq, dk, dv, st);
+    if (dextra) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+    na::lean_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
+                 dq, dk, dv, st);
   } else if (use_mfma(p, P)) {
     if (dextra || na::mfma_bwd_reads_delta(P))
       na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);

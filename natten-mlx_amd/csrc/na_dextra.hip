@@ -288,8 +288,9 @@ __global__ void __launch_bounds__(kXThreads)
 // into its own LDS slice ([32][D + 8]), computes S = q ek^T and dP = dO ev^T
 // for two 16-row blocks on mfma_f32_16x16x32 (ek / ev of the tile live in
 // registers as the B operand), forms P and dS in the accumulator layout
-// (lane: token l % 16, rows 4 (l / 16) + r) and packs them, rounded to the
-// input type, as the B operand of dek^T += q^T dS and dev^T += dO^T P, whose
+// (lane: token l % 16, rows 4 (l / 16) + r) and packs them, as a rounded
+// part plus the rounded remainder in the input type, as the B operands of
+// dek^T += q^T dS and dev^T += dO^T P, whose
 // A operand is read from the staged rows with the transposing LDS read.  The
 // four waves' sums are added in LDS in wave order at the end.
 constexpr int kXMRows = 128;  // rows per workgroup step (4 waves x 32)
@@ -389,7 +390,10 @@ __global__ void __launch_bounds__(256)
       *reinterpret_cast<v8 *>(sd + row * RS + 8 * c8) = xd[j];
     }
     wave_lds_sync();
-    v8 bp, bds;
+    // P and dS as B operands, each split into a rounded part and the
+    // rounded remainder (two products: the sums keep float accuracy over
+    // the thousands of rows a token's gradient adds)
+    v8 bp, bds, bpl, bdsl;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       f32x4 s = zero4(), dp = zero4();
@@ -404,16 +408,22 @@ __global__ void __launch_bounds__(256)
         const int row = 16 * h + 4 * g + r;
         const float l2r = __shfl(l2, row), dlr = __shfl(dl, row);
         const float p = n < ne ? exp2f(fmaf(s[r], sl2, -l2r)) : 0.f;
-        bp[4 * h + r] = (E)p;
-        bds[4 * h + r] = (E)(p * (dp[r] - dlr));
+        const float ds = p * (dp[r] - dlr);
+        const E ph = (E)p, dh = (E)ds;
+        bp[4 * h + r] = ph;
+        bpl[4 * h + r] = (E)(p - (float)ph);
+        bds[4 * h + r] = dh;
+        bdsl[4 * h + r] = (E)(ds - (float)dh);
       }
     }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const v4 q0 = M::tr(sq + tr_off + 16 * db), q1 = M::tr(sq + 16 * RS + tr_off + 16 * db);
       const v4 o0 = M::tr(sd + tr_off + 16 * db), o1 = M::tr(sd + 16 * RS + tr_off + 16 * db);
-      adk[db] = M::mma(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), bds, adk[db]);
-      adv[db] = M::mma(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), bp, adv[db]);
+      const v8 aq = __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+      const v8 ao = __builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7);
+      adk[db] = M::mma(aq, bdsl, M::mma(aq, bds, adk[db]));
+      adv[db] = M::mma(ao, bpl, M::mma(ao, bp, adv[db]));
     }
   }
   // the four waves' sums, added in wave order: red[w][2][16][D]

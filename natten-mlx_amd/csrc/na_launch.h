@@ -76,10 +76,13 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,
               float *lse, hipStream_t st);
 // Lean fused backward: one launch, no workspace (delta is computed in the
-// kernel); dlse may be null.  No additional tokens, one extent per sample.
+// kernel); dlse may be null.  Per-sample extents and additional tokens as
+// in lean_fwd (ek / ev: their contribution to dq; their own gradients come
+// from dextra).
 bool lean_bwd_eligible(const Prob &P, int dtype);
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
-              const void *v, const void *out, const float *lse,
+              const void *v, const void *ek, const void *ev,
+              const void *out, const float *lse,
               const void *dout, const float *dlse, void *dq, void *dk,
               void *dv, hipStream_t st);
 

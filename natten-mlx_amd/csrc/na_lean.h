@@ -500,8 +500,8 @@ size_t lean_lds_bytes(const Prob &P, LMode mode, int ebox, int W) {
   switch (mode) {
     case kLFwd:
       return (size_t)(lean_nxr(P) + ebox + kSlack) * lds_row(D) * 2;
-    case kLBwd:
-      return (size_t)(ebox + kSlack) * lds_row(D) * 2;
+    case kLBwd:  // the dQ pass stages the additional tokens before its box
+      return (size_t)(lean_nxr(P) + ebox + kSlack) * lds_row(D) * 2;
     case kLQK:
       return (size_t)align16((ebox + kSlack) * lds_y(D) * 2) + (size_t)16 * W * kp * 2;
     default:
@@ -555,8 +555,12 @@ LChoice lean_choice(const Prob &P, LMode mode) {
     const Axis &x = P.ax[a];
     if (P.sample_extent != nullptr) {
       // any sample: a box spans at most t + K - 1 points of a phase no
-      // longer than the tensor's
-      return std::min((x.L + x.d - 1) / x.d, t + x.K - 1);
+      // longer than the tensor's; an inverse box on a non-causal axis up to
+      // t + 2 (K - 1) (keys within K of an end of the sample are in the
+      // windows of every query up to that end, and a short sample puts both
+      // ends in one tile's reach)
+      const bool inv = (mode == kLBwd || mode == kLInv) && !x.causal;
+      return std::min((x.L + x.d - 1) / x.d, t + (inv ? 2 : 1) * (x.K - 1));
     }
     if (mode == kLInv) return box_max(x, t, true);
     const int f = box_max(x, t, false);

@@ -457,10 +457,11 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
 // box of the tile's keys (Q, dO, lse, delta) is staged and each wave
 // accumulates dK and dV of its 16 keys.  One workgroup per tile keeps the
 // whole launch resident at once.
-template <typename T, int D, int R, bool CPR1>
+template <typename T, int D, int R, bool CPR1, bool VX>
 __global__ void __launch_bounds__(512)
     k_wbwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
-           const T *__restrict__ v, const T *__restrict__ out,
+           const T *__restrict__ v, const T *__restrict__ ek,
+           const T *__restrict__ ev, const T *__restrict__ out,
            const float *__restrict__ lse, const T *__restrict__ dout,
            const float *__restrict__ dlse, T *__restrict__ dq,
            T *__restrict__ dk, T *__restrict__ dv) {
@@ -480,7 +481,7 @@ __global__ void __launch_bounds__(512)
   LTile t;
   t.hk = (int)(rest - bq * P.fHkv.d);
   t.b = (int)bq;
-  const bool tile_any = tile_origin<R>(P, sp, t) & (t.b < P.B);
+  const bool tile_any = tile_origin<R, VX>(P, sp, t) & (t.b < P.B);
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, gq = lane >> 4;
@@ -490,6 +491,42 @@ __global__ void __launch_bounds__(512)
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
   // the (lse, -delta) pad of query row 4 gq of a chunk
   const int pad_off = 4 * gq * RSE + D;
+  if (VX && t.b < P.B) {
+    // the lane's row of the tensor (wave tile w, position n): rows of the
+    // tensor outside the sample get zero dq (every head of the group), dk
+    // and dv here; the passes below write the sample's rows only
+    int u[3];
+    const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+    u[2] = n & (P.ax[2].T - 1);
+    u[1] = (n >> lg2) & (P.ax[1].T - 1);
+    u[0] = n >> (lg2 + lg1);
+    bool rin = true, rsm = true;
+    int rtok = t.b * P.Ltot;
+#pragma unroll
+    for (int a = 3 - R; a < 3; ++a) {
+      const LAx &x = P.ax[a];
+      const int rel = (a == P.sa ? w * x.T : 0) + u[a];
+      rin = rin && rel < t.nvt[a];
+      rsm = rsm && rel < t.nv[a];
+      rtok += (t.r[a] + x.d * (t.i0[a] + min(rel, max(t.nvt[a] - 1, 0)))) * x.tok;
+    }
+    if (rin && !rsm) {
+      v4 z;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = (E)0.f;
+      const int ko = (rtok * P.Hkv + t.hk) * D + 4 * gq;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        *reinterpret_cast<v4 *>(dk + ko + 16 * db) = z;
+        *reinterpret_cast<v4 *>(dv + ko + 16 * db) = z;
+      }
+      for (int hr = 0; hr < P.rep; ++hr) {
+        const int qo = (rtok * P.H + t.hk * P.rep + hr) * D + 4 * gq;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) *reinterpret_cast<v4 *>(dq + qo + 16 * db) = z;
+      }
+    }
+  }
   if (!tile_any) return;  // uniform over the workgroup
   E *xs = reinterpret_cast<E *>(smem);
   E *ys = xs + lds_y(D);
@@ -498,6 +535,23 @@ __global__ void __launch_bounds__(512)
   {
     tile_box<R, false>(P, t, t.hk, P.Hkv);
     const WSub ws = wave_sub<R, false>(P, t, w);
+    // VX: the additional tokens in LDS rows [0, nxr) (rows past nx repeat
+    // the last token: finite, masked), the K / V box after them; their
+    // chunks run after the last slab's box chunks
+    const int nxr = VX ? P.nxr : 0;
+    const int nxc = nxr >> 4;
+    E *ks = xs + nxr * RSE;
+    E *vs = ys + nxr * RSE;
+    if (VX && nxr > 0) {
+      constexpr int OCT = D / 8;
+      const int xrow0 = (t.b * P.nx * P.Hkv + t.hk) * D;
+      for (int uu = tid; uu < nxr * OCT; uu += nthr) {
+        const int e = uu / OCT, oo = uu % OCT;
+        const int g = xrow0 + min(e, P.nx - 1) * P.Hkv * D + 8 * oo;
+        *reinterpret_cast<v8 *>(xs + e * RSE + 8 * oo) = ld8(ek, g);
+        *reinterpret_cast<v8 *>(ys + e * RSE + 8 * oo) = ld8(ev, g);
+      }
+    }
     // the K / V box in slabs of P.sl layers along axis 0 (rank 3); a single
     // slab is staged once for every query head of the group
     const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
@@ -529,35 +583,48 @@ __global__ void __launch_bounds__(512)
       const int s0 = si * P.sl;
       if (nsl > 1 || hr == 0) {
         if (hr > 0 || si > 0) __syncthreads();  // the previous slab's reads are done
-        stage_box<T, D, R>(P, t, k, v, xs, ys, tid, nthr, s0);
+        stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
         __syncthreads();
       }
       if (!ws.any) continue;
       if (si == 0) delta = quad_sum(dsum) - dl;
       const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
       const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
-      const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+      const int nchb = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
+      const int nch = nchb + (si == nsl - 1 ? nxc : 0);
       const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
       Cursor cc{a0, ws.ws[1], 0};
       for (int c0 = 0; c0 < nch; c0 += 2) {
         int kb[2], cs[2];
         bool rok[2];
-        pair_rows<R, CPR1>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        pair_rows<R, CPR1>(ws, cc, c0, nchb, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        bool ext[2] = {false, false};
+        if (VX) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int c = c0 + h;
+            ext[h] = c >= nchb && c < nch;
+            if (ext[h]) {
+              kb[h] = 16 * (c - nchb) - nxr;
+              rok[h] = true;
+            }
+          }
+        }
         v8 kr[2][NT], vr[2][NT];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int st = 0; st < NT; ++st) {
-            kr[h][st] = *reinterpret_cast<const v8 *>(xs + kb[h] * RSE + ka_off + 32 * st);
-            vr[h][st] = *reinterpret_cast<const v8 *>(ys + kb[h] * RSE + ka_off + 32 * st);
+            kr[h][st] = *reinterpret_cast<const v8 *>(ks + kb[h] * RSE + ka_off + 32 * st);
+            vr[h][st] = *reinterpret_cast<const v8 *>(vs + kb[h] * RSE + ka_off + 32 * st);
           }
         // K^T operands of dQ^T += K^T . dS^T, read now so their latency
         // overlaps the score MFMAs and exponentials
         v8 kt[NDB];
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const v4 lo4 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
-          const v4 hi4 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+          const v4 lo4 = M::tr(ks + kb[0] * RSE + tr_off + 16 * db);
+          const v4 hi4 = M::tr(ks + kb[1] * RSE + tr_off + 16 * db);
           kt[db] = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
         }
         __builtin_amdgcn_sched_barrier(0);  // keep every read of the pair ahead
@@ -566,7 +633,9 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float cb[4];
-          if (CPR1) {
+          if (VX && ext[h]) {  // keys 16 (c - nchb) + 4 gq + r < nx
+            col_bias(16 * (c0 + h - nchb) + 4 * gq, qv ? P.nx : 0, cb);
+          } else if (CPR1) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) cb[r] = cb0[r];
           } else {
@@ -767,9 +836,7 @@ bool lean_eligible(const Prob &P, int dtype) {
 }
 
 bool lean_bwd_eligible(const Prob &P, int dtype) {
-  // additional tokens and per-sample extents: forward only
-  return P.n_extra == 0 && P.sample_extent == nullptr && lean_eligible(P, dtype) &&
-         lean_choice(P, kLBwd).ok;
+  return lean_eligible(P, dtype) && lean_choice(P, kLBwd).ok;
 }
 
 #define LEAN_D(D_, BODY) \
@@ -823,7 +890,8 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
 }
 
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
-              const void *v, const void *out, const float *lse,
+              const void *v, const void *ek, const void *ev,
+              const void *out, const float *lse,
               const void *dout, const float *dlse, void *dq, void *dk,
               void *dv, hipStream_t st) {
   const LChoice C = lean_choice(P, kLBwd);
@@ -834,11 +902,17 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
   if (L.n_tiles == 0) return;
   const size_t lds = lean_lds_bytes(P, kLBwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
-#define LB_LAUNCH(TT, DD, RR, CC)                                              \
-  hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC>), grid, block, lds, st, L,        \
+  const bool vx = P.sample_extent != nullptr || P.n_extra > 0;
+#define LB_LAUNCH1(TT, DD, RR, CC, VV)                                          \
+  hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV>), grid, block, lds, st, L,    \
                      (const TT *)q, (const TT *)k, (const TT *)v,              \
-                     (const TT *)out, lse, (const TT *)dout, dlse, (TT *)dq,   \
-                     (TT *)dk, (TT *)dv)
+                     (const TT *)ek, (const TT *)ev, (const TT *)out, lse,     \
+                     (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv)
+#define LB_LAUNCH(TT, DD, RR, CC)                                             \
+  do {                                                                        \
+    if (vx) LB_LAUNCH1(TT, DD, RR, CC, true);                                 \
+    else LB_LAUNCH1(TT, DD, RR, CC, false);                                   \
+  } while (0)
 #define LB_R(TT, DD)                                                          \
   do {                                                                        \
     if (P.rank == 1) LB_LAUNCH(TT, DD, 1, false);                             \
@@ -857,6 +931,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef LB_D
 #undef LB_R
 #undef LB_LAUNCH
+#undef LB_LAUNCH1
 }
 
 }  // namespace na

@@ -144,8 +144,9 @@ def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_ex
 
 def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, dilation,
                    is_causal, scale, extra_k=None, extra_v=None, sample_extent=None,
-                   dense=False):
-    """Returns ``(dq, dk, dv, d_extra_k, d_extra_v)``."""
+                   dense=False, varlen_clamped=False):
+    """Returns ``(dq, dk, dv, d_extra_k, d_extra_v)``; ``varlen_clamped`` as
+    in ``fused_forward``."""
     _require_device(q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v)
     q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v = map(
         _c, (q, k, v, out, lse, grad_out, grad_lse, extra_k, extra_v))
@@ -156,7 +157,7 @@ def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, d
     lib = _lib.load()
     n_extra = 0 if extra_k is None else extra_k.shape[1]
     p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
-                sample_extent)
+                sample_extent, varlen_clamped)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)

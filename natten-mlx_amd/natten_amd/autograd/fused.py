@@ -50,7 +50,8 @@ class _FusedNA(torch.autograd.Function):
         be = ops.backend_module()
         dq, dk, dv, dek, dev = be.fused_backward(
             q, k, v, out, lse, grad_out, grad_lse, spec.kernel_size, spec.stride, spec.dilation,
-            spec.is_causal, spec.scale, extra_k, extra_v, sample_extent, spec.dense)
+            spec.is_causal, spec.scale, extra_k, extra_v, sample_extent, spec.dense,
+            varlen_clamped=spec.varlen_clamped)
         return dq, dk, dv, dek, dev, None, None
 
 

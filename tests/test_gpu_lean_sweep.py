@@ -180,3 +180,60 @@ def test_lean_random_split_ops(case):
     assert_close(kd.grad, rk, dtype, "dk")
     assert_close(ad.grad, ra, dtype, "dattn")
     assert_close(vd.grad, rv, dtype, "dv")
+
+
+VXB_CASES = [_vx_problem(random.Random(4000 + i)) for i in range(12)]
+
+
+@pytest.mark.parametrize("case", VXB_CASES, ids=[f"b{i}" for i in range(len(VXB_CASES))])
+def test_lean_random_varlen_extra_backward(case):
+    """The lean backward with per-sample extents and additional tokens: dq,
+    dk, dv (zero outside each sample) and the additional tokens' gradients,
+    against the oracle run per sample, with upstream gradients on out and
+    lse."""
+    from natten_amd._core import hip
+
+    B, sp, H, Hkv, D, ks, dil, sizes, nx, dtype = case
+    _say(f"[case] lean vx backward sweep {case}")
+    rank = len(sp)
+    caus = (False,) * rank
+    st = (1,) * rank
+    q = randn((B, *sp, H, D), dtype, 161)
+    k = randn((B, *sp, Hkv, D), dtype, 162)
+    v = randn((B, *sp, Hkv, D), dtype, 163)
+    ek = randn((B, nx, Hkv, D), dtype, 164) if nx else None
+    ev = randn((B, nx, Hkv, D), dtype, 165) if nx else None
+    go = randn((B, *sp, H, D), dtype, 166)
+    gl = randn((B, *sp, H), torch.float32, 167)
+    se = torch.tensor(sizes, dtype=torch.int32)
+    assert hip.kernel_path(q, k, ks, st, dil, caus, n_extra=nx, sample_extent=se,
+                           varlen_clamped=True, backward=True) == "lean"
+    dev = [None if t is None else t.to(DEV) for t in (q, k, v, ek, ev, se)]
+    out, lse = hip.fused_forward(dev[0], dev[1], dev[2], ks, st, dil, caus, None,
+                                 extra_k=dev[3], extra_v=dev[4], sample_extent=dev[5],
+                                 varlen_clamped=True)
+    dq, dk, dv, dek, dvx = hip.fused_backward(
+        dev[0], dev[1], dev[2], out, lse, go.to(DEV), gl.to(DEV), ks, st, dil, caus, None,
+        extra_k=dev[3], extra_v=dev[4], sample_extent=dev[5], varlen_clamped=True)
+    ref = [torch.zeros(t.shape, dtype=torch.float64) for t in (q, k, v)]
+    rx = [torch.zeros((B, nx, Hkv, D), dtype=torch.float64) for _ in range(2)]
+    for b in range(B):
+        sl = (slice(b, b + 1),) + tuple(slice(0, e) for e in sizes[b])
+        ins = (q[sl], k[sl], v[sl]) + ((ek[b:b + 1], ev[b:b + 1]) if nx else ())
+
+        def f(a, c, d, *x):
+            return O.na_functional(a, c, d, ks, 1, dil, caus, return_lse=True,
+                                   additional_keys=x[0] if x else None,
+                                   additional_values=x[1] if x else None)
+
+        g = O.grads(f, ins, (go[sl], gl[sl]))
+        for r, gg in zip(ref, g[:3]):
+            r[sl] = gg.to(torch.float64)
+        if nx:
+            rx[0][b:b + 1] = g[3].to(torch.float64)
+            rx[1][b:b + 1] = g[4].to(torch.float64)
+    for t, r, nm in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert_close(t, r, dtype, nm)
+    if nx:
+        assert_close(dek, rx[0], dtype, "dek")
+        assert_close(dvx, rx[1], dtype, "dev")

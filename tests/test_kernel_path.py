@@ -1,11 +1,11 @@
 """Kernel selection (na_kernel_path, no GPU needed): which family each
 BASELINE configuration and each eligibility boundary dispatches to.  The
 lean workgroup kernels take the common problems (rank 3 staging its box a
-few layers at a time when it is too large for LDS), and the forward of
-varlen problems (when the caller has checked d * K <= L_b) and of
-additional tokens; their backward, unchecked varlen and over-budget
-rank-1/2 boxes stay on the 32-query matrix-core kernels; fp32, even kernels
-and strides on the generic kernels."""
+few layers at a time when it is too large for LDS), varlen problems (when
+the caller has checked d * K <= L_b) and additional tokens, forward and
+backward; unchecked varlen and over-budget rank-1/2 boxes stay on the
+32-query matrix-core kernels; fp32, even kernels and strides on the generic
+kernels."""
 
 import torch
 
@@ -37,14 +37,16 @@ def test_rank2_box_beyond_lds_budget_stays_on_mfma():
     assert _path((1, 64, 64, 2, 128), 2, (31, 31), (1, 1), (False, False)) == "mfma"
 
 
-def test_config4_forward_runs_lean():
+def test_config4_runs_lean_both_ways():
     # 1-D varlen GQA, k 63 d 2, 16 additional tokens (the functional entry
     # point checks d * K <= L_b on the host and says so)
     ext = torch.tensor([[4096], [1024]], dtype=torch.int32)
     kw = dict(n_extra=16, sample_extent=ext, dtype=torch.float16)
-    assert _path((2, 4096, 16, 64), 4, (63,), (2,), (False,), varlen_clamped=True,
-                 **kw) == "lean"
-    assert _path((2, 4096, 16, 64), 4, (63,), (2,), (False,), **kw) == "mfma"
+    for bwd in (False, True):
+        assert _path((2, 4096, 16, 64), 4, (63,), (2,), (False,), varlen_clamped=True,
+                     backward=bwd, **kw) == "lean"
+        assert _path((2, 4096, 16, 64), 4, (63,), (2,), (False,), backward=bwd,
+                     **kw) == "mfma"
 
 
 def test_lean_boundaries():
@@ -55,7 +57,7 @@ def test_lean_boundaries():
     assert _path((2, 40, 40, 4, 32), 4, (6, 7), (1, 1), (False, False)) == "generic"  # even K
     assert _path((2, 40, 40, 4, 48), 4, (7, 7), (1, 1), (False, False)) == "generic"  # head_dim 48
     ext = torch.tensor([[40, 40], [20, 30]], dtype=torch.int32)
-    for bwd, want in ((False, "lean"), (True, "mfma")):
+    for bwd, want in ((False, "lean"), (True, "lean")):
         assert _path(*base, n_extra=3, backward=bwd) == want     # additional tokens
         assert _path(*base, sample_extent=ext, varlen_clamped=True,
                      backward=bwd) == want                       # checked varlen
