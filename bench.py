@@ -226,6 +226,24 @@ def profile_calls(n: int, workload: str = "cfg2") -> None:
         torch.cuda.synchronize()
         print(f"profile-calls: {n} x allin1 K=7 d=1 forward and backward done", flush=True)
         return
+    if workload == "cfg4":
+        Bc, L, H, Hkv, Dc, nx = 8, 4096, 16, 4, 64, 16
+        qc = _gen((Bc, L, H, Dc), torch.float16, 0)
+        kc, vc = (_gen((Bc, L, Hkv, Dc), torch.float16, s) for s in (1, 2))
+        ak, av = (_gen((Bc, nx, Hkv, Dc), torch.float16, s) for s in (3, 4))
+        g = torch.Generator().manual_seed(5)
+        se = torch.randint(1024, 4097, (Bc, 1), generator=g, dtype=torch.int32).to("cuda:0")
+        a = ((63,), (1,), (2,), (False,), None)
+        kw = dict(extra_k=ak, extra_v=av, sample_extent=se, varlen_clamped=True)
+        out, lse = hip.fused_forward(qc, kc, vc, *a, **kw)
+        doc = _gen(out.shape, torch.float16, 6)
+        for _ in range(n):
+            hip.fused_forward(qc, kc, vc, *a, **kw)
+            hip.fused_backward(qc, kc, vc, out, lse, doc, None, *a, **kw)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x config-4 forward and backward (with extras) done",
+              flush=True)
+        return
     if workload == "merge":
         shape = (1, 16, 32, 32, 8, 64)
         outs = [_gen(shape, torch.bfloat16, s) for s in range(2)]

@@ -274,10 +274,26 @@ __global__ void __launch_bounds__(kXThreads)
   const int tt = e / kXT, el = e - tt * kXT;
   const float *src = part + (((int64_t)(b * P.Hkv + hk) * ntt + tt) * nsg) * 2 * kXT * D +
                      el * D + dd;
+  // in segment order, eight segments' loads in flight at a time
+  const int64_t sst = (int64_t)2 * kXT * D;
   float a = 0.f, v = 0.f;
-  for (int sg = 0; sg < nsg; ++sg) {
-    a += src[(int64_t)sg * 2 * kXT * D];
-    v += src[(int64_t)sg * 2 * kXT * D + kXT * D];
+  int sg = 0;
+  for (; sg + 8 <= nsg; sg += 8) {
+    float ta[8], tv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ta[j] = src[(sg + j) * sst];
+      tv[j] = src[(sg + j) * sst + kXT * D];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a += ta[j];
+      v += tv[j];
+    }
+  }
+  for (; sg < nsg; ++sg) {
+    a += src[sg * sst];
+    v += src[sg * sst + kXT * D];
   }
   dek[i] = from_f32<T>(a * P.scale);
   dev[i] = from_f32<T>(v);
