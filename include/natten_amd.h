@@ -57,9 +57,9 @@ enum na_flags {
   NA_FLAG_NO_LEAN = 4,
   /* With sample_extent: the caller has checked that every sample extent
    * satisfies dilation * kernel_size <= extent on each non-causal axis.
-   * Lets na_fwd run such problems on the lean kernels; a sample that breaks
-   * the promise gets wrong values in its rows (every memory access stays
-   * inside the tensors). */
+   * Lets na_fwd and na_bwd run such problems on the lean kernels; a sample
+   * that breaks the promise gets wrong values in its rows (every memory
+   * access stays inside the tensors). */
   NA_FLAG_VARLEN_CLAMPED = 8
 };
 
