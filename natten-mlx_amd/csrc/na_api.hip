@@ -359,8 +359,13 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
   const hipStream_t st = as_stream(stream);
   const bool dextra =
       P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
+  const bool matrix = (p->flags & NA_FLAG_GENERIC) == 0;
+  // the lean backward computes delta inside; the matrix-core extra-token
+  // reduction can too (from O and dO), else it reads a delta pass
+  bool xdelta = false;
   if (use_lean_bwd(p, P)) {
-    if (dextra) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+    xdelta = dextra && na::dextra_fuses_delta(P, p->dtype, matrix);
+    if (dextra && !xdelta) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::lean_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
                  dq, dk, dv, st);
   } else if (use_mfma(p, P)) {
@@ -373,8 +378,8 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                  dq, dk, dv, delta, st);
   }
   if (dextra)
-    na::dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout, d_extra_k,
-               d_extra_v, xpart, (p->flags & NA_FLAG_GENERIC) == 0, st);
+    na::dextra(P, p->dtype, q, extra_k, extra_v, lse, xdelta ? nullptr : delta,
+               dout, out, dlse, d_extra_k, d_extra_v, xpart, matrix, st);
   return launch_status("na_bwd");
 }
 

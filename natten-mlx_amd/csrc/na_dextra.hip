@@ -311,11 +311,14 @@ __global__ void __launch_bounds__(kXThreads)
 // four waves' sums are added in LDS in wave order at the end.
 constexpr int kXMRows = 128;  // rows per workgroup step (4 waves x 32)
 
+// delta == nullptr: delta of each row is computed here, rowsum(dO * O) -
+// dlse, from the O row loaded beside the dO row.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     k_xmfma(Prob P, const T *__restrict__ q, const T *__restrict__ ek,
             const T *__restrict__ ev, const float *__restrict__ lse,
             const float *__restrict__ delta, const T *__restrict__ dout,
+            const T *__restrict__ out, const float *__restrict__ dlse,
             float *__restrict__ part, int ntt, int nsg, int nper, int64_t nrows) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
@@ -386,7 +389,8 @@ __global__ void __launch_bounds__(256)
         qo = (qt * P.H + h) * D;
         dof = (ot * P.H + h) * D;
         l2 = lse[ot * P.H + h] * kLog2e;
-        dl = delta[ot * P.H + h];
+        dl = delta != nullptr ? delta[ot * P.H + h]
+                              : (dlse != nullptr ? -dlse[ot * P.H + h] : 0.f);
       }
     }
     // gather the 32 q and dO rows: 16-byte units u = lane + 64 j
@@ -397,6 +401,30 @@ __global__ void __launch_bounds__(256)
       const int64_t a = __shfl(qo, row), c = __shfl(dof, row);
       xq[j] = a >= 0 ? *reinterpret_cast<const v8 *>(q + a + 8 * c8) : zero;
       xd[j] = c >= 0 ? *reinterpret_cast<const v8 *>(dout + c + 8 * c8) : zero;
+    }
+    if (delta == nullptr) {  // uniform
+      // rowsum(dO * O): unit j's partial dot, summed over the C8 lanes that
+      // hold its row; lane L < 32 then takes row L's sum (unit L C8 / 64,
+      // lane L C8 % 64)
+      float rs[UPL];
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) {
+        const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
+        const int64_t c = __shfl(dof, row);
+        const v8 xo = c >= 0 ? *reinterpret_cast<const v8 *>(out + c + 8 * c8) : zero;
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)xd[j][e], (float)xo[e], acc);
+        rs[j] = group_sum(acc, C8);
+      }
+      const int src = lane * C8;
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < UPL; ++j) {
+        const float x = __shfl(rs[j], src & 63);
+        if ((src >> 6) == j) sum = x;
+      }
+      dl += sum;  // rows outside the sample: dO = 0, sum 0, dl stays 0
     }
     wave_lds_sync();  // the previous step's reads of the slice are done
 #pragma unroll
@@ -467,6 +495,14 @@ bool xmfma_ok(const Prob &P, int dtype) {
   return dtype != NA_F32 && (P.D == 32 || P.D == 64 || P.D == 128);
 }
 
+}  // namespace
+
+bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix) {
+  return matrix && xmfma_ok(P, dtype);
+}
+
+namespace {
+
 XPlan xplan_mfma(const Prob &P) {
   XPlan x;
   x.xt = 16;
@@ -493,8 +529,8 @@ size_t dextra_workspace_bytes(const Prob &P) {
 
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, void *dek, void *dev, float *part, bool matrix,
-            hipStream_t st) {
+            const void *dout, const void *out, const float *dlse, void *dek,
+            void *dev, float *part, bool matrix, hipStream_t st) {
   if (P.n_extra <= 0 || P.B == 0) return;
   if (matrix && xmfma_ok(P, dtype)) {
     const XPlan x = xplan_mfma(P);
@@ -505,7 +541,8 @@ void dextra(const Prob &P, int dtype, const void *q, const void *ek,
 #define XM_(TT, DD)                                                              \
   hipLaunchKernelGGL((k_xmfma<TT, DD>), dim3(g1), dim3(256), lds, st, P,         \
                      (const TT *)q, (const TT *)ek, (const TT *)ev, lse, delta,  \
-                     (const TT *)dout, part, x.ntt, x.nsg, x.nper, x.nrows)
+                     (const TT *)dout, (const TT *)out, dlse, part, x.ntt,       \
+                     x.nsg, x.nper, x.nrows)
 #define XMD_(TT)          \
   do {                    \
     if (P.D == 32)        \

@@ -132,10 +132,13 @@ void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
 // dlse per (query, head)); `part` is a float workspace of
 // dextra_workspace_bytes(P); `matrix` allows the matrix-core variant
 // (bf16 / fp16, head_dim 32 / 64 / 128).
+// With delta == nullptr (only where dextra_fuses_delta) the matrix-core
+// variant computes delta from out, dout and dlse (nullable) itself.
 size_t dextra_workspace_bytes(const Prob &P);
+bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix);
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, void *dek, void *dev, float *part, bool matrix,
-            hipStream_t st);
+            const void *dout, const void *out, const float *dlse, void *dek,
+            void *dev, float *part, bool matrix, hipStream_t st);
 
 }  // namespace na
