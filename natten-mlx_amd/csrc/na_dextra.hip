@@ -365,13 +365,24 @@ __global__ void __launch_bounds__(256)
   }
   const int tr_off = (4 * g + (n >> 2)) * RS + 4 * (n & 3);
 
-  for (int ci = 0; ci < nper; ++ci) {
+  // One step's rows: lanes 0..31 decode the wave's 32 rows (q / dO
+  // offsets, lse * log2(e): +inf outside the sample, P = 0; delta or -dlse
+  // when it is computed here), then the 16-byte units u = lane + 64 j of
+  // the q, dO (and O) rows are loaded.  Steps are software-pipelined: the
+  // next step's loads are issued before this step's matrix work.
+  const bool fuse = delta == nullptr;
+  struct Step {
+    int64_t qo, dof;
+    float l2, dl;
+    v8 xq[UPL], xd[UPL], xo[UPL];
+  };
+  auto fetch = [&](int ci, Step &st) -> bool {
     const int64_t r0 = ((int64_t)sg * nper + ci) * kXMRows + 32 * w;
-    if (r0 >= nrows) break;  // wave-uniform; no workgroup barrier in the loop
-    // lanes 0..31 decode the wave's rows: q / dO offsets, lse * log2(e)
-    // (+inf outside the sample: P = 0), delta
-    int64_t qo = -1, dof = -1;
-    float l2 = INFINITY, dl = 0.f;
+    if (ci >= nper || r0 >= nrows) return false;  // wave-uniform
+    st.qo = -1;
+    st.dof = -1;
+    st.l2 = INFINITY;
+    st.dl = 0.f;
     if (lane < 32) {
       const int64_t ri = r0 + lane;
       bool ok = ri < nrows;
@@ -386,35 +397,37 @@ __global__ void __launch_bounds__(256)
       if (ok) {
         const int64_t qt = tok_in(P, b, o0 * P.ax[0].s, o1 * P.ax[1].s, o2 * P.ax[2].s);
         const int64_t ot = tok_out(P, b, o0, o1, o2);
-        qo = (qt * P.H + h) * D;
-        dof = (ot * P.H + h) * D;
-        l2 = lse[ot * P.H + h] * kLog2e;
-        dl = delta != nullptr ? delta[ot * P.H + h]
-                              : (dlse != nullptr ? -dlse[ot * P.H + h] : 0.f);
+        st.qo = (qt * P.H + h) * D;
+        st.dof = (ot * P.H + h) * D;
+        st.l2 = lse[ot * P.H + h] * kLog2e;
+        st.dl = !fuse ? delta[ot * P.H + h] : (dlse != nullptr ? -dlse[ot * P.H + h] : 0.f);
       }
     }
-    // gather the 32 q and dO rows: 16-byte units u = lane + 64 j
-    v8 xq[UPL], xd[UPL];
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
       const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
-      const int64_t a = __shfl(qo, row), c = __shfl(dof, row);
-      xq[j] = a >= 0 ? *reinterpret_cast<const v8 *>(q + a + 8 * c8) : zero;
-      xd[j] = c >= 0 ? *reinterpret_cast<const v8 *>(dout + c + 8 * c8) : zero;
+      const int64_t a = __shfl(st.qo, row), c = __shfl(st.dof, row);
+      st.xq[j] = a >= 0 ? *reinterpret_cast<const v8 *>(q + a + 8 * c8) : zero;
+      st.xd[j] = c >= 0 ? *reinterpret_cast<const v8 *>(dout + c + 8 * c8) : zero;
+      if (fuse) st.xo[j] = c >= 0 ? *reinterpret_cast<const v8 *>(out + c + 8 * c8) : zero;
     }
-    if (delta == nullptr) {  // uniform
+    return true;
+  };
+
+  Step cur;
+  bool have = fetch(0, cur);
+  for (int ci = 0; have; ++ci) {
+    float dl = cur.dl;
+    if (fuse) {
       // rowsum(dO * O): unit j's partial dot, summed over the C8 lanes that
       // hold its row; lane L < 32 then takes row L's sum (unit L C8 / 64,
-      // lane L C8 % 64)
+      // lane L C8 % 64).  Rows outside the sample: dO = 0, sum 0, dl 0.
       float rs[UPL];
 #pragma unroll
       for (int j = 0; j < UPL; ++j) {
-        const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
-        const int64_t c = __shfl(dof, row);
-        const v8 xo = c >= 0 ? *reinterpret_cast<const v8 *>(out + c + 8 * c8) : zero;
         float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf((float)xd[j][e], (float)xo[e], acc);
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)cur.xd[j][e], (float)cur.xo[j][e], acc);
         rs[j] = group_sum(acc, C8);
       }
       const int src = lane * C8;
@@ -424,15 +437,18 @@ __global__ void __launch_bounds__(256)
         const float x = __shfl(rs[j], src & 63);
         if ((src >> 6) == j) sum = x;
       }
-      dl += sum;  // rows outside the sample: dO = 0, sum 0, dl stays 0
+      dl += sum;
     }
+    const float l2 = cur.l2;
     wave_lds_sync();  // the previous step's reads of the slice are done
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
       const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
-      *reinterpret_cast<v8 *>(sq + row * RS + 8 * c8) = xq[j];
-      *reinterpret_cast<v8 *>(sd + row * RS + 8 * c8) = xd[j];
+      *reinterpret_cast<v8 *>(sq + row * RS + 8 * c8) = cur.xq[j];
+      *reinterpret_cast<v8 *>(sd + row * RS + 8 * c8) = cur.xd[j];
     }
+    Step nxt;
+    const bool hn = fetch(ci + 1, nxt);
     wave_lds_sync();
     // P and dS as B operands, each split into a rounded part and the
     // rounded remainder (two products: the sums keep float accuracy over
@@ -469,6 +485,8 @@ __global__ void __launch_bounds__(256)
       adk[db] = M::mma(aq, bdsl, M::mma(aq, bds, adk[db]));
       adv[db] = M::mma(ao, bpl, M::mma(ao, bp, adv[db]));
     }
+    if (hn) cur = nxt;
+    have = hn;
   }
   // the four waves' sums, added in wave order: red[w][2][16][D]
   __syncthreads();
