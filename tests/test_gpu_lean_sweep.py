@@ -182,7 +182,28 @@ def test_lean_random_split_ops(case):
     assert_close(vd.grad, rv, dtype, "dv")
 
 
-VXB_CASES = [_vx_problem(random.Random(4000 + i)) for i in range(12)]
+def _vx3_problem(rng):
+    # rank 3 (boxes staged in slabs along the first axis), per-sample extents
+    ks, dil, sp = [], [], []
+    for a in range(3):
+        K = rng.choice((3, 5))
+        d = rng.choice((1, 1, 2))
+        L = rng.randint(d * K + 2, 14)
+        ks.append(K)
+        dil.append(d)
+        sp.append(L)
+    B = 2
+    sizes = [list(sp), [rng.randint(d * K, L) for K, d, L in zip(ks, dil, sp)]]
+    hkv = rng.choice((1, 2))
+    return (B, tuple(sp), hkv * rng.choice((1, 2)), hkv, rng.choice((32, 64)), tuple(ks),
+            tuple(dil), sizes, rng.choice((0, 3, 17)), rng.choice((torch.bfloat16, torch.float16)))
+
+
+VXB_CASES = ([_vx_problem(random.Random(4000 + i)) for i in range(12)]
+             + [_vx3_problem(random.Random(4100 + i)) for i in range(4)]
+             # a rank-3 box beyond the LDS budget: staged in slabs
+             + [(2, (8, 24, 24), 4, 2, 64, (3, 7, 7), (1, 1, 1), [[8, 24, 24], [6, 20, 17]], 0,
+                 torch.bfloat16)])
 
 
 @pytest.mark.parametrize("case", VXB_CASES, ids=[f"b{i}" for i in range(len(VXB_CASES))])
