@@ -580,7 +580,7 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(batch/head sharding needs no communication; see DESIGN.md). "
+              "(batch and heads would shard over GPUs with no communication). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
