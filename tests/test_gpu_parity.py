@@ -290,11 +290,12 @@ def test_varlen_gqa_extra_gradients(dtype, generic):
         assert_close(t.grad, r, dtype, nm)
 
 
-@pytest.mark.parametrize("D", [6, 264, 520, 1024])
+@pytest.mark.parametrize("D", [6, 64, 128, 264, 520, 1024])
 def test_extra_gradients_head_dims(D):
     """Extra-token gradients at head_dims that change the reduction's tiling:
-    not a multiple of 4 (zero-padded rows), and above 256 (eight, then four
-    tokens per tile), with GQA and a stride, against the oracle."""
+    64 and 128 on the matrix-core reduction, not a multiple of 4
+    (zero-padded rows) and above 256 (eight, then four tokens per tile) on
+    the vector-ALU one, with GQA and a stride, against the oracle."""
     import natten_amd
 
     dtype = torch.float16
