@@ -372,7 +372,7 @@ __global__ void __launch_bounds__(256)
   // next step's loads are issued before this step's matrix work.
   const bool fuse = delta == nullptr;
   struct Step {
-    int64_t qo, dof;
+    int32_t qo, dof;  // element offsets (tensors below 2^31 elements)
     float l2, dl;
     v8 xq[UPL], xd[UPL], xo[UPL];
   };
@@ -397,8 +397,8 @@ __global__ void __launch_bounds__(256)
       if (ok) {
         const int64_t qt = tok_in(P, b, o0 * P.ax[0].s, o1 * P.ax[1].s, o2 * P.ax[2].s);
         const int64_t ot = tok_out(P, b, o0, o1, o2);
-        st.qo = (qt * P.H + h) * D;
-        st.dof = (ot * P.H + h) * D;
+        st.qo = (int32_t)((qt * P.H + h) * D);
+        st.dof = (int32_t)((ot * P.H + h) * D);
         st.l2 = lse[ot * P.H + h] * kLog2e;
         st.dl = !fuse ? delta[ot * P.H + h] : (dlse != nullptr ? -dlse[ot * P.H + h] : 0.f);
       }
@@ -406,10 +406,10 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
       const int u = lane + 64 * j, row = u / C8, c8 = u - row * C8;
-      const int64_t a = __shfl(st.qo, row), c = __shfl(st.dof, row);
-      st.xq[j] = a >= 0 ? *reinterpret_cast<const v8 *>(q + a + 8 * c8) : zero;
-      st.xd[j] = c >= 0 ? *reinterpret_cast<const v8 *>(dout + c + 8 * c8) : zero;
-      if (fuse) st.xo[j] = c >= 0 ? *reinterpret_cast<const v8 *>(out + c + 8 * c8) : zero;
+      const int32_t a = __shfl(st.qo, row), c = __shfl(st.dof, row);
+      st.xq[j] = a >= 0 ? ld8(q, a + 8 * c8) : zero;
+      st.xd[j] = c >= 0 ? ld8(dout, c + 8 * c8) : zero;
+      if (fuse) st.xo[j] = c >= 0 ? ld8(out, c + 8 * c8) : zero;
     }
     return true;
   };
@@ -510,7 +510,11 @@ __global__ void __launch_bounds__(256)
 }
 
 bool xmfma_ok(const Prob &P, int dtype) {
-  return dtype != NA_F32 && (P.D == 32 || P.D == 64 || P.D == 128);
+  // 32-bit element offsets into q, out and dout
+  const int64_t rows_in = (int64_t)P.B * P.ax[0].L * P.ax[1].L * P.ax[2].L * P.H;
+  const int64_t rows_out = (int64_t)P.B * P.ax[0].O * P.ax[1].O * P.ax[2].O * P.H;
+  return dtype != NA_F32 && (P.D == 32 || P.D == 64 || P.D == 128) &&
+         std::max(rows_in, rows_out) * P.D < (int64_t(1) << 31);
 }
 
 }  // namespace
