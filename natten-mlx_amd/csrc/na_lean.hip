@@ -138,7 +138,16 @@ __global__ void __launch_bounds__(512)
   // setup is straight-line arithmetic on kernel arguments (so their loads
   // issue together); the exit test comes after it
   LTile t;
-  const bool tile_any = decode_tile<R, VX>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  bool hl = false;  // VX: every query head of the group over one box
+  bool tile_any;
+  if constexpr (VX) {
+    hl = P.hl != 0;
+    const int tile_id = xcd_tile(blockIdx.x, P.n_launch);
+    tile_any = hl ? decode_tile_group<R>(P, tile_id, t) : decode_tile<R, VX>(P, tile_id, t);
+  } else {
+    tile_any = decode_tile<R, VX>(P, xcd_tile(blockIdx.x, P.n_launch), t);
+  }
+  const int nhl = hl ? P.rep : 1;
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, gq = lane >> 4;
@@ -179,22 +188,26 @@ __global__ void __launch_bounds__(512)
     ww[a] = wend(x, i, t.Lr[a]) - s;
   }
   if (!qv) ww[2] = 0;
-  const int qoff = (qtok * P.H + t.head) * D;
   if (!tile_any) {  // uniform over the workgroup
     if (VX && qt) {  // rows of the tensor outside the sample: zeros
       v4 z;
 #pragma unroll
       for (int r = 0; r < 4; ++r) z[r] = (E)0.f;
+      for (int hr = 0; hr < nhl; ++hr) {
+        const int zo = (qtok * P.H + t.head + hr) * D;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
-        *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = z;
-      if (lse != nullptr && gq == 0) lse[qoff / D] = 0.f;
+        for (int db = 0; db < NDB; ++db)
+          *reinterpret_cast<v4 *>(out + zo + 16 * db + 4 * gq) = z;
+        if (lse != nullptr && gq == 0) lse[zo / D] = 0.f;
+      }
     }
     return;
   }
+  // the first head's query rows, issued before the staging
   v8 qf[NT];
 #pragma unroll
-  for (int st = 0; st < NT; ++st) qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
+  for (int st = 0; st < NT; ++st)
+    qf[st] = ld8(q, (qtok * P.H + t.head) * D + 32 * st + 8 * gq);
 
   // ---- LDS: additional tokens (VX) in rows [0, nxr), then the K / V box,
   // staged in slabs of P.sl layers along axis 0 for rank 3 (one slab
@@ -222,6 +235,12 @@ __global__ void __launch_bounds__(512)
   float cb0[4];
   col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
 
+  for (int hr = 0; hr < nhl; ++hr) {  // query heads over the staged box (hl)
+  const int qoff = (qtok * P.H + t.head + hr) * D;
+  if (hr > 0) {
+#pragma unroll
+    for (int st = 0; st < NT; ++st) qf[st] = ld8(q, qoff + 32 * st + 8 * gq);
+  }
   f32x4 o[NDB];
 #pragma unroll
   for (int j = 0; j < NDB; ++j) o[j] = zero4();
@@ -243,9 +262,11 @@ __global__ void __launch_bounds__(512)
   const int nxc = VX ? nxr >> 4 : 0;
   for (int si = 0; si < nsl; ++si) {
     const int s0 = si * P.sl;
-    if (si > 0) __syncthreads();  // the previous slab's reads are done
-    stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
-    __syncthreads();
+    if (hr == 0) {  // with hl the whole box is one slab, staged once
+      if (si > 0) __syncthreads();  // the previous slab's reads are done
+      stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+      __syncthreads();
+    }
     if (!ws.any) continue;
     // the wave's box rows inside this slab
     const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
@@ -304,17 +325,19 @@ __global__ void __launch_bounds__(512)
 
   // ---- epilogue: sum l over the query's 4 lanes, normalise, store ----
   const float l = quad_sum(lacc[0]);
-  if (!(VX ? qt : qv)) return;
-  const float inv = qv && l > 0.f ? 1.f / l : 0.f;
+  if (VX ? qt : qv) {
+    const float inv = qv && l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    v4 wv;
+    for (int db = 0; db < NDB; ++db) {
+      v4 wv;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wv[r] = (E)(o[db][r] * inv);
-    *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = wv;
+      for (int r = 0; r < 4; ++r) wv[r] = (E)(o[db][r] * inv);
+      *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = wv;
+    }
+    if (lse != nullptr && gq == 0)
+      lse[qoff / D] = !qv ? 0.f : l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
   }
-  if (lse != nullptr && gq == 0)
-    lse[qoff / D] = !qv ? 0.f : l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+  }  // query heads
 }
 
 // ---------------------------------------------------------------------------
@@ -854,9 +877,20 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,
               float *lse, hipStream_t st) {
   const LChoice C = lean_choice(P, kLFwd);
-  const LProb L = make_lprob(P, C);
+  LProb L = make_lprob(P, C);
   if (L.n_tiles == 0) return;
   const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
+  // grouped query heads (one staged box for the group) where the box is one
+  // slab and the grouped launch still gives at least 4 workgroups per CU;
+  // NATTEN_AMD_HL=0 / 1 turns the grouping off / on wherever it applies
+  const char *hl_env = std::getenv("NATTEN_AMD_HL");
+  const bool hl_auto = L.n_tiles / P.rep >= 1024;
+  const bool hl_want = hl_env != nullptr ? hl_env[0] == '1' : hl_auto;
+  if (vx && P.rep > 1 && (P.rank < 3 || L.sl >= L.ax[0].Em) && hl_want) {
+    L.hl = 1;
+    L.n_tiles /= P.rep;
+    L.n_launch = (L.n_tiles + 7) & ~7;
+  }
   const size_t lds = lean_lds_bytes(P, kLFwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
 #define LF_LAUNCH1(TT, DD, RR, CC, VV)                                          \

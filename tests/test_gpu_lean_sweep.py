@@ -258,3 +258,29 @@ def test_lean_random_varlen_extra_backward(case):
     if nx:
         assert_close(dek, rx[0], dtype, "dek")
         assert_close(dvx, rx[1], dtype, "dev")
+
+
+@pytest.mark.parametrize("case", [c for c in VX_CASES if c[2] > c[3]],
+                         ids=lambda c: f"rep{c[2] // c[3]}")
+def test_lean_grouped_heads_forward(case, monkeypatch):
+    """The varlen / extra-token forward with every query head of a group run
+    over one staged box (NATTEN_AMD_HL=1; chosen automatically for large
+    launches) equals the per-head launch bit for bit."""
+    from natten_amd._core import hip
+
+    B, sp, H, Hkv, D, ks, dil, sizes, nx, dtype = case
+    _say(f"[case] lean grouped heads {case}")
+    rank = len(sp)
+    q = randn((B, *sp, H, D), dtype, 61).to(DEV)
+    k = randn((B, *sp, Hkv, D), dtype, 62).to(DEV)
+    v = randn((B, *sp, Hkv, D), dtype, 63).to(DEV)
+    ek = randn((B, nx, Hkv, D), dtype, 64).to(DEV) if nx else None
+    ev = randn((B, nx, Hkv, D), dtype, 65).to(DEV) if nx else None
+    se = torch.tensor(sizes, dtype=torch.int32).to(DEV)
+    res = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("NATTEN_AMD_HL", flag)
+        res.append(hip.fused_forward(q, k, v, ks, (1,) * rank, dil, (False,) * rank, None,
+                                     extra_k=ek, extra_v=ev, sample_extent=se,
+                                     varlen_clamped=True))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
