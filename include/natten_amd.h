@@ -141,6 +141,28 @@ enum na_kernel_path_t {
 };
 int na_kernel_path(const na_params *p, int32_t backward);
 
+/*
+ * Diagnostic with no counterpart in the reference: how na_fwd (backward =
+ * 0) or na_bwd (backward = 1) launches for these parameters.  Fields past
+ * `path` describe the lean kernels and are 0 on the other paths.  Launches
+ * nothing and reads no device memory; returns NA_OK or an NA_ERR_* code.
+ */
+typedef struct na_plan {
+  int32_t path;            /* na_kernel_path_t */
+  int32_t tile[3];         /* queries per wave along the three axes */
+  int32_t waves;           /* waves per workgroup */
+  int32_t box[3];          /* largest staged key box (backward: also the
+                              query box of a key tile) */
+  int32_t slabs;           /* pieces along axis 0 the box is staged in */
+  int32_t grouped_heads;   /* forward: a workgroup runs every query head of
+                              its key/value head over one staged box */
+  int32_t workgroups;      /* workgroups launched */
+  int32_t lds_bytes;       /* LDS per workgroup */
+  int32_t extra_reduction; /* backward with additional tokens: their
+                              gradients on 1 = vector ALU, 2 = matrix cores */
+} na_plan;
+int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan);
+
 /* ---- fused neighborhood attention --------------------------------------- */
 /*
  * out = softmax(scale * q k_nbr^T masked) v_nbr over each query's window

@@ -292,6 +292,37 @@ int na_kernel_path(const na_params *p, int32_t backward) {
   return NA_PATH_GENERIC;
 }
 
+int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan) {
+  if (plan == nullptr) return fail(NA_ERR_INVALID, "plan is NULL");
+  if (backward != 0 && backward != 1)
+    return fail(NA_ERR_INVALID, "backward must be 0 or 1, got %d", backward);
+  na::Prob P;
+  const int rc = make_prob(p, &P, true);
+  if (rc != NA_OK) return rc;
+  *plan = na_plan{};
+  const bool lean = backward ? use_lean_bwd(p, P) : use_lean(p, P);
+  plan->path = lean ? NA_PATH_LEAN : use_mfma(p, P) ? NA_PATH_MFMA : NA_PATH_GENERIC;
+  if (lean) {
+    na::LeanPlanInfo L{};
+    if (na::lean_plan(P, p->dtype, backward != 0, &L)) {
+      for (int a = 0; a < 3; ++a) {
+        plan->tile[a] = L.T[a];
+        plan->box[a] = L.Em[a];
+      }
+      plan->waves = L.W;
+      plan->slabs = L.slabs;
+      plan->grouped_heads = L.hl;
+      plan->workgroups = L.workgroups;
+      plan->lds_bytes = L.lds;
+    }
+  }
+  if (backward && P.n_extra > 0)
+    plan->extra_reduction =
+        na::dextra_uses_matrix(P, p->dtype, (p->flags & NA_FLAG_GENERIC) == 0) ? 2 : 1;
+  g_error.clear();
+  return NA_OK;
+}
+
 int na_neighbor_table(const na_params *p, int32_t *index, uint8_t *valid,
                       void *stream) {
   na::Prob P;
@@ -513,12 +544,12 @@ int na_rpb_qk_bwd(const na_rpb_params *p, const void *q, const void *key,
   if (A.n_rows == 0) {  // empty batch: drpb (if requested) is all zero
     if (drpb != nullptr)
       na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, nullptr, nullptr, drpb,
-                     (float *)workspace, as_stream(stream));
+                     workspace, as_stream(stream));
     return launch_status("na_rpb_qk_bwd");
   }
   if (q == nullptr || key == nullptr || dlogits == nullptr)
     return fail(NA_ERR_INVALID, "q/key/dlogits must be non-NULL");
-  na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, dq, dk, drpb, (float *)workspace,
+  na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, dq, dk, drpb, workspace,
                  as_stream(stream));
   return launch_status("na_rpb_qk_bwd");
 }

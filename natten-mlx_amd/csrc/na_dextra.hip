@@ -523,6 +523,10 @@ bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix) {
   return matrix && xmfma_ok(P, dtype);
 }
 
+bool dextra_uses_matrix(const Prob &P, int dtype, bool matrix) {
+  return matrix && xmfma_ok(P, dtype);
+}
+
 namespace {
 
 XPlan xplan_mfma(const Prob &P) {

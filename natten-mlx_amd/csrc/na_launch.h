@@ -47,7 +47,7 @@ void rpb_av_fwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
 size_t rpb_bias_workspace_bytes(const RpbProb &A);
 void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
                 const float *dlogits, void *dq, void *dk, float *drpb,
-                float *workspace, hipStream_t st);
+                void *workspace, hipStream_t st);
 void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
                 const void *value, const void *dout, float *dattn, void *dvalue,
                 hipStream_t st);
@@ -75,6 +75,14 @@ bool lean_eligible(const Prob &P, int dtype);
 void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,
               float *lse, hipStream_t st);
+// Launch plan of the lean fused kernels (a diagnostic): wave tile T, waves
+// per workgroup W, staged box Em, number of axis-0 slabs the box is staged
+// in, grouped query heads (forward), workgroups launched and LDS bytes.
+// False when the problem does not run on them.
+struct LeanPlanInfo {
+  int T[3], W, Em[3], slabs, hl, workgroups, lds;
+};
+bool lean_plan(const Prob &P, int dtype, bool backward, LeanPlanInfo *o);
 // Lean fused backward: one launch, no workspace (delta is computed in the
 // kernel); dlse may be null.  Per-sample extents and additional tokens as
 // in lean_fwd (ek / ev: their contribution to dq; their own gradients come
@@ -136,6 +144,8 @@ void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
 // variant computes delta from out, dout and dlse (nullable) itself.
 size_t dextra_workspace_bytes(const Prob &P);
 bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix);
+// Whether dextra runs the matrix-core reduction (else the vector-ALU one).
+bool dextra_uses_matrix(const Prob &P, int dtype, bool matrix);
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
             const void *dout, const void *out, const float *dlse, void *dek,

@@ -873,16 +873,13 @@ bool lean_bwd_eligible(const Prob &P, int dtype) {
     }                    \
   } while (0)
 
-void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
-              const void *v, const void *ek, const void *ev, void *out,
-              float *lse, hipStream_t st) {
-  const LChoice C = lean_choice(P, kLFwd);
+// The forward's launch: grouped query heads (one staged box for the group)
+// for varlen / additional-token problems where the box is one slab and the
+// grouped launch still gives at least 4 workgroups per CU;
+// NATTEN_AMD_HL=0 / 1 turns the grouping off / on wherever it applies.
+LProb lean_fwd_lprob(const Prob &P, const LChoice &C) {
   LProb L = make_lprob(P, C);
-  if (L.n_tiles == 0) return;
   const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
-  // grouped query heads (one staged box for the group) where the box is one
-  // slab and the grouped launch still gives at least 4 workgroups per CU;
-  // NATTEN_AMD_HL=0 / 1 turns the grouping off / on wherever it applies
   const char *hl_env = std::getenv("NATTEN_AMD_HL");
   const bool hl_auto = L.n_tiles / P.rep >= 1024;
   const bool hl_want = hl_env != nullptr ? hl_env[0] == '1' : hl_auto;
@@ -891,6 +888,41 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
     L.n_tiles /= P.rep;
     L.n_launch = (L.n_tiles + 7) & ~7;
   }
+  return L;
+}
+
+// The backward's launch: one workgroup per (sample, key/value head, tile).
+LProb lean_bwd_lprob(const Prob &P, const LChoice &C) {
+  LProb L = make_lprob(P, C);
+  L.n_tiles = P.B * P.Hkv * (int)L.fGrid.d;
+  L.n_launch = (L.n_tiles + 7) & ~7;
+  return L;
+}
+
+bool lean_plan(const Prob &P, int dtype, bool backward, LeanPlanInfo *o) {
+  if (!(backward ? lean_bwd_eligible(P, dtype) : lean_eligible(P, dtype))) return false;
+  const LMode mode = backward ? kLBwd : kLFwd;
+  const LChoice C = lean_choice(P, mode);
+  const LProb L = backward ? lean_bwd_lprob(P, C) : lean_fwd_lprob(P, C);
+  for (int a = 0; a < 3; ++a) {
+    o->T[a] = C.T[a];
+    o->Em[a] = C.Em[a];
+  }
+  o->W = C.W;
+  o->slabs = (C.Em[0] + C.sl - 1) / C.sl;
+  o->hl = L.hl;
+  o->workgroups = L.n_tiles;
+  o->lds = (int)lean_lds_bytes(P, mode, L.ebox, C.W);
+  return true;
+}
+
+void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
+              const void *v, const void *ek, const void *ev, void *out,
+              float *lse, hipStream_t st) {
+  const LChoice C = lean_choice(P, kLFwd);
+  const LProb L = lean_fwd_lprob(P, C);
+  if (L.n_tiles == 0) return;
+  const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
   const size_t lds = lean_lds_bytes(P, kLFwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
 #define LF_LAUNCH1(TT, DD, RR, CC, VV)                                          \
@@ -929,10 +961,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *dout, const float *dlse, void *dq, void *dk,
               void *dv, hipStream_t st) {
   const LChoice C = lean_choice(P, kLBwd);
-  LProb L = make_lprob(P, C);
-  const int grid_sp = (int)L.fGrid.d;
-  L.n_tiles = P.B * P.Hkv * grid_sp;
-  L.n_launch = (L.n_tiles + 7) & ~7;
+  const LProb L = lean_bwd_lprob(P, C);
   if (L.n_tiles == 0) return;
   const size_t lds = lean_lds_bytes(P, kLBwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);

@@ -487,7 +487,7 @@ __device__ __forceinline__ void slots_of_bias_row(int32_t r, int32_t pb,
 
 // Bias gradient, pass 1: one block per chunk of `chunk` (<= kBiasChunk)
 // queries (rows in (b, i0, i1) order); partial[bin * n_chunks + c] is the
-// chunk's sum for bin = (h, r0[, r1]), output-major so pass 2 reads each
+// chunk's float64 sum for bin = (h, r0[, r1]), output-major so pass 2 reads each
 // bin's partials contiguously.  `scatter` (the chunk's [query][head][bin]
 // sums fit 32 KB of LDS): thread (t, h) adds its row's valid slots into
 // its own LDS cells [t][h][clipped bias row] (slot order), then thread
@@ -496,7 +496,7 @@ __device__ __forceinline__ void slots_of_bias_row(int32_t r, int32_t pb,
 // Either way the order of every sum is fixed.
 __global__ void __launch_bounds__(256)
     k_rpb_bias_partial(RpbProb A, const float *__restrict__ dl,
-                       float *__restrict__ partial, int32_t chunk,
+                       double *__restrict__ partial, int32_t chunk,
                        int32_t n_chunks, int scatter) {
   extern __shared__ float sacc[];
   __shared__ RWin sw0[kBiasChunk], sw1[kBiasChunk];
@@ -549,8 +549,8 @@ __global__ void __launch_bounds__(256)
     for (int32_t bin = tid; bin < nb; bin += blockDim.x) {
       const int32_t h = bin / per_h;
       const int32_t rb = bin - h * per_h;
-      float acc = 0.f;
-      for (int32_t t = 0; t < nqc; ++t) acc += sacc[(t * A.H + h) * per_h + rb];
+      double acc = 0.0;
+      for (int32_t t = 0; t < nqc; ++t) acc += (double)sacc[(t * A.H + h) * per_h + rb];
       partial[(int64_t)bin * n_chunks + c] = acc;
     }
     return;
@@ -561,7 +561,7 @@ __global__ void __launch_bounds__(256)
     const int32_t rb = bin - h * per_h;
     const int32_t r0 = rb / A.R1;
     const int32_t r1 = rb - r0 * A.R1;
-    float acc = 0.f;
+    double acc = 0.0;
     for (int32_t t = 0; t < nqc; ++t) {
       const RWin w0 = sw0[t];
       int32_t a0, b0;
@@ -577,7 +577,7 @@ __global__ void __launch_bounds__(256)
         for (int32_t k1 = a1; k1 <= b1; ++k1) {
           const int32_t j1 = w1.s + k1 * A.d1;
           if (j1 < 0 || j1 >= w1.e) continue;
-          acc += row[k0 * A.K1 + k1];
+          acc += (double)row[k0 * A.K1 + k1];
         }
       }
     }
@@ -586,27 +586,30 @@ __global__ void __launch_bounds__(256)
 }
 
 // Bias gradient, pass 2: one wavefront per bin sums its chunk partials,
-// lane l taking chunks l, l+64, ... and a fixed xor tree after.
+// lane l taking chunks l, l+64, ... and a fixed xor tree after.  Both
+// passes accumulate in float64 (a bin adds one float32 term per query of
+// the whole problem, and such sums can cancel to far below their terms), so
+// the only float32 rounding is that of the result.
 __global__ void __launch_bounds__(64)
-    k_rpb_bias_reduce(const float *__restrict__ partial, int32_t n_chunks,
+    k_rpb_bias_reduce(const double *__restrict__ partial, int32_t n_chunks,
                       float *__restrict__ drpb) {
   const int32_t o = blockIdx.x;
   const int lane = threadIdx.x;
-  const float *src = partial + (int64_t)o * n_chunks;
+  const double *src = partial + (int64_t)o * n_chunks;
   // eight loads in flight per lane, summed in a fixed order
-  float acc = 0.f;
+  double acc = 0.0;
   for (int32_t c0 = 0; c0 < n_chunks; c0 += 8 * 64) {
-    float v[8];
+    double v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int32_t c = c0 + j * 64 + lane;
-      v[j] = c < n_chunks ? src[c] : 0.f;
+      v[j] = c < n_chunks ? src[c] : 0.0;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc += v[j];
   }
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (lane == 0) drpb[o] = acc;
+  if (lane == 0) drpb[o] = (float)acc;
 }
 
 // ---- host launchers --------------------------------------------------------
@@ -776,12 +779,12 @@ size_t rpb_bias_workspace_bytes(const RpbProb &A) {
   int32_t chunk, n_chunks;
   bias_chunking(A, &chunk, &n_chunks);
   const size_t nb = (size_t)A.H * A.R0 * A.R1;
-  return (size_t)n_chunks * nb * sizeof(float);
+  return (size_t)n_chunks * nb * sizeof(double);
 }
 
 void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
                 const float *dlogits, void *dq, void *dk, float *drpb,
-                float *workspace, hipStream_t st) {
+                void *workspace, hipStream_t st) {
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     if (A.n_rows == 0) return;
@@ -799,10 +802,10 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     const int scatter = sbytes <= 32768;
     if (n_chunks > 0)
       hipLaunchKernelGGL(k_rpb_bias_partial, dim3((unsigned)n_chunks), dim3(256),
-                         scatter ? sbytes : 0, st, A, dlogits, workspace, chunk,
+                         scatter ? sbytes : 0, st, A, dlogits, (double *)workspace, chunk,
                          n_chunks, scatter);
     hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)nb), dim3(64), 0, st,
-                       (const float *)workspace, n_chunks, drpb);
+                       (const double *)workspace, n_chunks, drpb);
   }
 }
 

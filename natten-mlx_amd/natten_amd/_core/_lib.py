@@ -71,6 +71,22 @@ class NaRpbParams(ctypes.Structure):
     ]
 
 
+class NaPlan(ctypes.Structure):
+    """Mirror of ``na_plan`` (include/natten_amd.h)."""
+
+    _fields_ = [
+        ("path", ctypes.c_int32),
+        ("tile", _I32x3),
+        ("waves", ctypes.c_int32),
+        ("box", _I32x3),
+        ("slabs", ctypes.c_int32),
+        ("grouped_heads", ctypes.c_int32),
+        ("workgroups", ctypes.c_int32),
+        ("lds_bytes", ctypes.c_int32),
+        ("extra_reduction", ctypes.c_int32),
+    ]
+
+
 class NaMergeParams(ctypes.Structure):
     """Mirror of ``na_merge_params`` (include/natten_amd.h)."""
 
@@ -102,6 +118,7 @@ SIGNATURES = {
     "na_neighbor_table": (ctypes.c_int, [_P, _V, _V, _V]),
     "na_mfma_selftest": (ctypes.c_int, [_I, _V, _V]),
     "na_kernel_path": (ctypes.c_int, [_P, _I]),
+    "na_kernel_plan": (ctypes.c_int, [_P, _I, ctypes.POINTER(NaPlan)]),
     "na_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V, _V, _V]),
     "na_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
     "na_bwd": (ctypes.c_int, [_P] + [_V] * 15 + [ctypes.c_size_t, _V]),

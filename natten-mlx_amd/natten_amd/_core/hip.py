@@ -142,6 +142,25 @@ def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_ex
     return KERNEL_PATHS[r]
 
 
+def kernel_plan(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_extra=0,
+                dense=False, sample_extent=None, backward=False, varlen_clamped=False):
+    """How na_fwd (or na_bwd) launches for this problem (a diagnostic;
+    launches nothing): a dict with the kernel family and, on the lean
+    kernels, the wave tile, waves per workgroup, staged box, axis-0 slabs,
+    grouped query heads, workgroups, LDS bytes; with additional tokens in
+    the backward, which unit reduces their gradients."""
+    lib = _lib.load()
+    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                sample_extent, varlen_clamped)
+    plan = _lib.NaPlan()
+    _lib.check(lib.na_kernel_plan(p, 1 if backward else 0, plan), "na_kernel_plan")
+    return {"path": KERNEL_PATHS[plan.path], "tile": tuple(plan.tile), "waves": plan.waves,
+            "box": tuple(plan.box), "slabs": plan.slabs,
+            "grouped_heads": bool(plan.grouped_heads), "workgroups": plan.workgroups,
+            "lds_bytes": plan.lds_bytes,
+            "extra_reduction": {0: None, 1: "valu", 2: "matrix"}[plan.extra_reduction]}
+
+
 def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, dilation,
                    is_causal, scale, extra_k=None, extra_v=None, sample_extent=None,
                    dense=False, varlen_clamped=False):
@@ -311,12 +330,19 @@ na2d_av_backward = na1d_av_backward
 na3d_av_backward = na1d_av_backward
 
 
-def na1d_fused_backward(q, k, v, grad_out, out, lse, kernel_size, stride, dilation, is_causal,
-                        scale, grad_lse=None):
-    """Backward from a saved forward (the role of the reference's
-    ``fast_metal.na{n}d_fused_simd_backward(q, k, v, dO, out, ...)``)."""
-    dq, dk, dv, _, _ = fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride,
-                                      dilation, is_causal, scale)
+def na1d_fused_backward(q, k, v, grad_out, fwd_out, kernel_size, stride, dilation, is_causal,
+                        scale, lse=None, grad_lse=None):
+    """Backward from a saved forward, with the positional signature of the
+    reference's ``fast_metal.na{n}d_fused_simd_backward(q, k, v, grad_out,
+    fwd_out, kernel_size, stride, dilation, is_causal, scale)``
+    (``fast_metal.py:2390-2521``), which the VJPs call with the forward output
+    only (``autograd/na2d.py:39-46``).  ``lse`` (float32 ``[B, *O, H]``) is
+    the forward's log-sum-exp when the caller kept it; when None it is
+    recomputed by one forward launch."""
+    if lse is None:
+        _, lse = fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale)
+    dq, dk, dv, _, _ = fused_backward(q, k, v, fwd_out, lse, grad_out, grad_lse, kernel_size,
+                                      stride, dilation, is_causal, scale)
     return dq, dk, dv
 
 

@@ -53,7 +53,7 @@ def _check_qk_av(q, k, v, rpb, K, d, scale, dtype, tag):
     assert_close(ts[0].grad, refg[0], tol_dt, f"{tag} dq")
     assert_close(ts[1].grad, refg[1], tol_dt, f"{tag} dk")
     if rpb is not None:
-        assert_close(rp.grad, refg[2], torch.float32, f"{tag} drpb", scale_tol=4.0)
+        assert_close(rp.grad, refg[2], torch.float32, f"{tag} drpb")
 
     attn = torch.softmax(randn(logits.shape, torch.float32, 41), -1)
     a_d = attn.to(DEV).requires_grad_(True)
@@ -68,7 +68,7 @@ def _check_qk_av(q, k, v, rpb, K, d, scale, dtype, tag):
     assert_close(v_d.grad, rv, tol_dt, f"{tag} dv")
 
 
-CASES_1D = [(3, 1), (5, 2), (7, 4), (5, 8), (7, 8), (4, 3), (6, 1)]
+CASES_1D = [(3, 1), (5, 2), (7, 4), (5, 8), (7, 8), (4, 3), (6, 1), (7, 1)]
 
 
 @pytest.mark.parametrize("K,d", CASES_1D)
@@ -145,7 +145,7 @@ def test_allin1_heads_first_functions():
         rq, rk, rr = O.grads(lambda a, b, c: O.qk_rpb(a, b, c, K, d), (q, k, rpb), (g,))
         assert_close(_sf(dq), rq, torch.float32, f"hf{rank} dq")
         assert_close(_sf(dk), rk, torch.float32, f"hf{rank} dk")
-        assert_close(drpb, rr, torch.float32, f"hf{rank} drpb", scale_tol=4.0)
+        assert_close(drpb, rr, torch.float32, f"hf{rank} drpb")
         go = randn(v.shape, torch.float32, 35)
         da, dv = av_b(_hf(go).to(DEV), _hf(attn).to(DEV), _hf(v).to(DEV), K, d)
         ra, rv = O.grads(lambda a, b: O.av_rpb(a, b, K, d), (attn, v), (go,))

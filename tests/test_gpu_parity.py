@@ -315,3 +315,26 @@ def test_extra_gradients_head_dims(D):
     out.backward(go.to(DEV))
     for t, r, nm in zip(ts, ref, ("dq", "dk", "dv", "dek", "dev")):
         assert_close(t.grad, r, dtype, nm)
+
+
+def test_fused_backward_hook_reference_signature():
+    """hip.na2d_fused_backward takes the reference VJP's positional
+    arguments (q, k, v, grad_out, fwd_out, kernel_size, stride, dilation,
+    is_causal, scale; fast_metal.py:2430) and recomputes the LSE when none is
+    passed: same gradients as with the forward's LSE, and as the oracle."""
+    from natten_amd._core import hip
+
+    _say("[case] fused backward hook signature")
+    dt = torch.bfloat16
+    q, k, v = _inputs(2, (20, 18), 4, 4, 32, dt, 61)
+    go = randn(q.shape, dt, 62)
+    qd, kd, vd, god = (t.to(DEV) for t in (q, k, v, go))
+    a = ((7, 5), (1, 1), (2, 1), (False, False), None)
+    out, lse = hip.fused_forward(qd, kd, vd, *a)
+    g_none = hip.na2d_fused_backward(qd, kd, vd, god, out, *a)
+    g_lse = hip.na2d_fused_backward(qd, kd, vd, god, out, *a, lse=lse)
+    for x, y in zip(g_none, g_lse):
+        assert torch.equal(x, y)
+    ref = O.grads(lambda x, y, z: O.na_forward(x, y, z, (7, 5), 1, (2, 1)), (q, k, v), (go,))
+    for g, r, n in zip(g_none, ref, "qkv"):
+        assert_close(g, r, dt, f"hook d{n}")

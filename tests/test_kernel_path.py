@@ -84,3 +84,34 @@ def test_split_ops_run_lean():
     with hip.no_lean_kernels():
         assert _path((4, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False),
                      split=True) == "mfma"
+
+
+def _plan(shape_q, hkv, ks, dil, caus, dtype=torch.bfloat16, backward=False, **kw):
+    q = torch.empty(shape_q, dtype=dtype)
+    k = torch.empty((*shape_q[:-2], hkv, shape_q[-1]), dtype=dtype)
+    return hip.kernel_plan(q, k, ks, (1,) * len(ks), dil, caus, backward=backward, **kw)
+
+
+def test_plans_of_the_benchmarked_configs():
+    """The launch shapes the benchmark lines time: config 3 stages its key
+    box in several depth slabs both ways; config 4 at its full size groups
+    the four query heads of a key/value head in the forward and reduces the
+    additional tokens' gradients on matrix cores; config 2 stages its box
+    whole."""
+    for bwd in (False, True):
+        p3 = _plan((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False),
+                   backward=bwd)
+        assert p3["path"] == "lean" and p3["slabs"] > 1, p3
+        assert p3["lds_bytes"] <= 160 * 1024
+        p2 = _plan((4, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False), backward=bwd)
+        assert p2["path"] == "lean" and p2["slabs"] == 1 and not p2["grouped_heads"], p2
+    ext = torch.full((8, 1), 1024, dtype=torch.int32)
+    kw = dict(n_extra=16, sample_extent=ext, dtype=torch.float16, varlen_clamped=True)
+    f4 = _plan((8, 4096, 16, 64), 4, (63,), (2,), (False,), **kw)
+    assert f4["path"] == "lean" and f4["grouped_heads"], f4
+    b4 = _plan((8, 4096, 16, 64), 4, (63,), (2,), (False,), backward=True, **kw)
+    assert b4["path"] == "lean" and b4["extra_reduction"] == "matrix", b4
+    # a small varlen launch keeps one query head per workgroup
+    small = _plan((3, 300, 8, 64), 2, (63,), (2,), (False,),
+                  **dict(kw, sample_extent=torch.full((3, 1), 300, dtype=torch.int32)))
+    assert small["path"] == "lean" and not small["grouped_heads"], small
