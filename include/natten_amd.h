@@ -195,6 +195,24 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
            void *dk, void *dv, void *d_extra_k, void *d_extra_v,
            void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * na_bwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The workspace
+ * is a fixed device array inside the library, one per GPU, of
+ * na_bwd_noalloc_max_workspace() bytes (32 MiB); problems whose
+ * na_bwd_workspace_bytes exceeds it are rejected with NA_ERR_UNSUPPORTED.
+ * Allocates nothing (no hipMalloc / hipFree).  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (on different streams or
+ * threads) race and must be serialised by the caller.
+ */
+size_t na_bwd_noalloc_max_workspace(void);
+int na_bwd_noalloc(const na_params *p, const void *q, const void *k,
+                   const void *v, const void *extra_k, const void *extra_v,
+                   const void *out, const float *lse, const void *dout,
+                   const float *dlse, void *dq, void *dk, void *dv,
+                   void *d_extra_k, void *d_extra_v, void *stream);
+
 /* ---- split operators ----------------------------------------------------- */
 /* logits = scale * <q, k_nbr>, -inf for invalid slots; ops.py:61-80,
  * pure.py:258-283,320-359,404-449.  logits in p->dtype. */

@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "na_common.h"
@@ -238,6 +239,41 @@ int check_merge(const na_merge_params *p, const void *const *outs,
   return NA_OK;
 }
 
+// ---- fixed scratch for na_bwd_noalloc -----------------------------------
+// The backward's workspace (delta rows and the additional tokens' gradient
+// partials) for callers that cannot allocate: a file-scope device array,
+// one copy per GPU the library runs on, held until the process ends.  Host
+// code never passes `scratch` itself (its host-side name is not a device
+// address): the device address comes from hipGetSymbolAddress, once per
+// device, with that device current, and is kept per device.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(NA_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(NA_ERR_UNSUPPORTED, "device %d is beyond the %d devices na_bwd_noalloc serves",
+                dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(NA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -412,6 +448,32 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
     na::dextra(P, p->dtype, q, extra_k, extra_v, lse, xdelta ? nullptr : delta,
                dout, out, dlse, d_extra_k, d_extra_v, xpart, matrix, st);
   return launch_status("na_bwd");
+}
+
+size_t na_bwd_noalloc_max_workspace(void) { return kScratchBytes; }
+
+int na_bwd_noalloc(const na_params *p, const void *q, const void *k,
+                   const void *v, const void *extra_k, const void *extra_v,
+                   const void *out, const float *lse, const void *dout,
+                   const float *dlse, void *dq, void *dk, void *dv,
+                   void *d_extra_k, void *d_extra_v, void *stream) {
+  na::Prob P;
+  const int rc = make_prob(p, &P, true);
+  if (rc != NA_OK) return rc;
+  const size_t need = bwd_workspace_bytes(P);
+  if (need > kScratchBytes)
+    return fail(NA_ERR_UNSUPPORTED,
+                "na_bwd_noalloc: this problem needs %zu bytes of scratch, above its "
+                "fixed maximum of %zu; use na_bwd with a caller workspace",
+                need, kScratchBytes);
+  void *ws = nullptr;
+  const int src = scratch_of_current_device(&ws);
+  if (src != NA_OK) return src;
+  // every byte the kernels read from the workspace is written earlier in
+  // the same call (delta rows; one partial per reduction segment), so the
+  // previous call's contents need no clearing
+  return na_bwd(p, q, k, v, extra_k, extra_v, out, lse, dout, dlse, dq, dk, dv,
+                d_extra_k, d_extra_v, ws, kScratchBytes, stream);
 }
 
 int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,

@@ -122,6 +122,8 @@ SIGNATURES = {
     "na_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V, _V, _V]),
     "na_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
     "na_bwd": (ctypes.c_int, [_P] + [_V] * 15 + [ctypes.c_size_t, _V]),
+    "na_bwd_noalloc_max_workspace": (ctypes.c_size_t, []),
+    "na_bwd_noalloc": (ctypes.c_int, [_P] + [_V] * 15),
     "na_qk_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V]),
     "na_av_fwd": (ctypes.c_int, [_P, _V, _V, _V, _V]),
     "na_qk_bwd": (ctypes.c_int, [_P, _V, _V, _V, _V, _V, _V]),
