@@ -139,16 +139,42 @@ bool use_msplit(const na_params *p, const na::Prob &P) {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-size_t delta_bytes(const na::Prob &P);
-
-// delta, then the extra-token gradient partials
-size_t bwd_workspace_bytes(const na::Prob &P) {
-  return delta_bytes(P) + align256(na::dextra_workspace_bytes(P));
-}
-
 size_t delta_bytes(const na::Prob &P) {
   return align256(sizeof(float) * (size_t)P.B * P.ax[0].O * P.ax[1].O *
                   P.ax[2].O * P.H);
+}
+
+// The backward's kernels and the workspace they read: delta rows
+// (rowsum(dO * O) - dlse per query and head) where a kernel reads them, then
+// the additional tokens' gradient partials.  Sized as if the extra-token
+// gradients are requested (the workspace query sees no pointers).
+enum BwdPath { kBwdLean, kBwdMfma, kBwdGeneric };
+struct BwdPlan {
+  BwdPath path;
+  bool matrix;       // the extra-token reduction may use matrix cores
+  bool xdelta;       // that reduction forms delta itself (lean path)
+  bool need_delta;   // a delta pass runs and its rows live in the workspace
+  size_t delta, total;  // bytes: delta rows, whole workspace
+};
+
+BwdPlan bwd_plan(const na_params *p, const na::Prob &P) {
+  BwdPlan b{};
+  b.matrix = (p->flags & NA_FLAG_GENERIC) == 0;
+  const bool extra = P.n_extra > 0;
+  if (use_lean_bwd(p, P)) {
+    b.path = kBwdLean;
+    b.xdelta = extra && na::dextra_fuses_delta(P, p->dtype, b.matrix);
+    b.need_delta = extra && !b.xdelta;
+  } else if (use_mfma(p, P)) {
+    b.path = kBwdMfma;
+    b.need_delta = extra || na::mfma_bwd_reads_delta(P);
+  } else {
+    b.path = kBwdGeneric;
+    b.need_delta = true;
+  }
+  b.delta = b.need_delta ? delta_bytes(P) : 0;
+  b.total = b.delta + (extra ? align256(na::dextra_workspace_bytes(P)) : 0);
+  return b;
 }
 
 // Validate the all-in-one parameters and build the device problem.
@@ -397,7 +423,7 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
 size_t na_bwd_workspace_bytes(const na_params *p) {
   na::Prob P;
   if (make_prob(p, &P, true) != NA_OK) return 0;
-  return bwd_workspace_bytes(P);
+  return bwd_plan(p, P).total;
 }
 
 int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
@@ -416,26 +442,24 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                 "q/k/v/out/lse/dout/dq/dk/dv must be non-NULL");
   if (P.n_extra > 0 && (extra_k == nullptr || extra_v == nullptr))
     return fail(NA_ERR_INVALID, "n_extra > 0 needs extra_k and extra_v");
-  const size_t need = bwd_workspace_bytes(P);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need,
+  const BwdPlan plan = bwd_plan(p, P);
+  if (plan.total > 0 && (workspace == nullptr || workspace_bytes < plan.total))
+    return fail(NA_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", plan.total,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);
   float *delta = static_cast<float *>(workspace);
-  float *xpart = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                           delta_bytes(P));
+  float *xpart = plan.total > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                                            plan.delta)
+                                : nullptr;
   const hipStream_t st = as_stream(stream);
   const bool dextra =
       P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
-  const bool matrix = (p->flags & NA_FLAG_GENERIC) == 0;
   // the lean backward computes delta inside; the matrix-core extra-token
   // reduction can too (from O and dO), else it reads a delta pass
-  bool xdelta = false;
-  if (use_lean_bwd(p, P)) {
-    xdelta = dextra && na::dextra_fuses_delta(P, p->dtype, matrix);
-    if (dextra && !xdelta) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+  if (plan.path == kBwdLean) {
+    if (dextra && !plan.xdelta) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::lean_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
                  dq, dk, dv, st);
-  } else if (use_mfma(p, P)) {
+  } else if (plan.path == kBwdMfma) {
     if (dextra || na::mfma_bwd_reads_delta(P))
       na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::mfma_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
@@ -445,8 +469,9 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                  dq, dk, dv, delta, st);
   }
   if (dextra)
-    na::dextra(P, p->dtype, q, extra_k, extra_v, lse, xdelta ? nullptr : delta,
-               dout, out, dlse, d_extra_k, d_extra_v, xpart, matrix, st);
+    na::dextra(P, p->dtype, q, extra_k, extra_v, lse,
+               plan.path == kBwdLean && plan.xdelta ? nullptr : delta, dout, out, dlse,
+               d_extra_k, d_extra_v, xpart, plan.matrix, st);
   return launch_status("na_bwd");
 }
 
@@ -460,7 +485,7 @@ int na_bwd_noalloc(const na_params *p, const void *q, const void *k,
   na::Prob P;
   const int rc = make_prob(p, &P, true);
   if (rc != NA_OK) return rc;
-  const size_t need = bwd_workspace_bytes(P);
+  const size_t need = bwd_plan(p, P).total;
   if (need > kScratchBytes)
     return fail(NA_ERR_UNSUPPORTED,
                 "na_bwd_noalloc: this problem needs %zu bytes of scratch, above its "

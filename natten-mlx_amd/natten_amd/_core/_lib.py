@@ -190,7 +190,9 @@ def dtype_code(dt: torch.dtype) -> int:
 
 
 def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device address of a tensor as a Python int (None for NULL); the
+    c_void_p argtypes take ints directly."""
+    return None if t is None else t.data_ptr()
 
 
 def ptr_array(tensors):
@@ -201,8 +203,15 @@ def ptr_array(tensors):
     return arr
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """torch's current HIP stream on the tensor's device (the handle the
+    library launches on), as an int."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def make_params(rank: int, batch: int, heads: int, kv_heads: int, head_dim: int, dtype: int,

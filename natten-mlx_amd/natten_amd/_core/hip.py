@@ -80,19 +80,46 @@ def _scale(scale, head_dim: int) -> float:
     return head_dim ** -0.5 if scale is None else float(scale)
 
 
+# Built parameter blocks (and their backward workspace sizes) by problem:
+# a training loop calls with the same few shapes every step, and building the
+# ctypes struct costs more than the launch itself.  Entries are never
+# mutated; the cache is cleared when it grows past _PARAMS_MAX.
+_params_cache: dict = {}
+_PARAMS_MAX = 256
+
+
+def _params_entry(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_causal,
+                  scale, n_extra: int = 0, dense: bool = False,
+                  sample_extent: Optional[torch.Tensor] = None, varlen_clamped: bool = False):
+    flags = ((_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0)
+             | (_lib.NA_FLAG_NO_LEAN if _no_lean else 0)
+             | (_lib.NA_FLAG_VARLEN_CLAMPED if varlen_clamped and sample_extent is not None
+                else 0))
+    se_ptr = None if sample_extent is None else sample_extent.data_ptr()
+    key = (tuple(q.shape), k.shape[-2], q.dtype, tuple(kernel_size), tuple(stride),
+           tuple(dilation), tuple(is_causal), scale, n_extra, flags, se_ptr)
+    hit = _params_cache.get(key)
+    if hit is not None:
+        return hit
+    rank = q.dim() - 3
+    p = _lib.make_params(
+        rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
+        tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
+        tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra, flags,
+        sample_extent)
+    entry = [p, None]  # [params, backward workspace bytes (filled on first use)]
+    if len(_params_cache) >= _PARAMS_MAX:
+        _params_cache.clear()
+    _params_cache[key] = entry
+    return entry
+
+
 def _params(q: torch.Tensor, k: torch.Tensor, kernel_size, stride, dilation, is_causal, scale,
             n_extra: int = 0, dense: bool = False,
             sample_extent: Optional[torch.Tensor] = None,
             varlen_clamped: bool = False) -> _lib.NaParams:
-    rank = q.dim() - 3
-    return _lib.make_params(
-        rank, q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1], _lib.dtype_code(q.dtype),
-        tuple(q.shape[1:-2]), tuple(kernel_size), tuple(dilation), tuple(stride),
-        tuple(int(bool(c)) for c in is_causal), _scale(scale, q.shape[-1]), n_extra,
-        (_lib.NA_FLAG_DENSE if dense else 0) | (_lib.NA_FLAG_GENERIC if _force_generic else 0)
-        | (_lib.NA_FLAG_NO_LEAN if _no_lean else 0)
-        | (_lib.NA_FLAG_VARLEN_CLAMPED if varlen_clamped and sample_extent is not None else 0),
-        sample_extent)
+    return _params_entry(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                         sample_extent, varlen_clamped)[0]
 
 
 def _out_spatial(spatial: Sequence[int], stride: Sequence[int]) -> tuple[int, ...]:
@@ -175,15 +202,19 @@ def fused_backward(q, k, v, out, lse, grad_out, grad_lse, kernel_size, stride, d
         grad_lse = grad_lse.float()
     lib = _lib.load()
     n_extra = 0 if extra_k is None else extra_k.shape[1]
-    p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
-                sample_extent, varlen_clamped)
+    entry = _params_entry(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
+                          sample_extent, varlen_clamped)
+    p = entry[0]
+    if entry[1] is None:
+        entry[1] = int(lib.na_bwd_workspace_bytes(p))
+    ws_bytes = entry[1]
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     dek = torch.empty_like(extra_k) if n_extra else None
     dev = torch.empty_like(extra_v) if n_extra else None
-    ws_bytes = int(lib.na_bwd_workspace_bytes(p))
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    # the lean backward without additional tokens needs no workspace
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     _lib.check(lib.na_bwd(p, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(extra_k),
                           _lib.ptr(extra_v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(grad_out),
                           _lib.ptr(grad_lse), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),

@@ -89,7 +89,11 @@ def test_invalid_params_rejected_without_device():
     assert b"exceeds" in lib.na_last_error()
     p = _lib.make_params(1, 0, 4, 4, 32, _lib.NA_BF16, (8,), (3,), (1,), (1,), (0,), 1.0)
     assert lib.na_fwd(p, None, None, None, None, None, None, None, None) == 0  # empty batch
+    # the workspace is what the chosen kernels read: none for the lean
+    # backward, one float of delta per (query, head) on the generic kernels
     p = _lib.make_params(1, 1, 4, 4, 32, _lib.NA_BF16, (8,), (3,), (1,), (1,), (0,), 1.0)
+    assert lib.na_bwd_workspace_bytes(p) == 0
+    p = _lib.make_params(1, 1, 4, 4, 32, _lib.NA_F32, (8,), (3,), (1,), (1,), (0,), 1.0)
     assert lib.na_bwd_workspace_bytes(p) >= 4 * 8 * 4
     rc = lib.na_bwd(p, *([None] * 15), 0, None)
     assert rc == 1
