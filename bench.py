@@ -8,6 +8,14 @@ under "dilation4".  One step = forward (out + LSE) and backward
 steps and replayed, so the K timed steps keep the GPU busy (eager timing is
 reported too).
 
+Timing follows the reference's protocol (benchmarks/final_perf_table.py:
+33-58; README.md:232-234): 5 warmup runs, 20 trials, the first 2 dropped,
+the median of the other 18.  A trial is one HIP-event-timed graph replay
+(device time) or, for the eager figures, one host-clocked synchronised call
+as in the reference.  Beside every warm figure (inputs resident in the
+256 MB Infinity Cache across trials) a "mall_flushed" figure repeats the
+trial right after writing a 512 MB buffer, so inputs come from HBM.
+
 Printed JSON line (rank 0): metric/value/unit per the driver contract, with
  * roofline: the dominant library call timed with HIP events on the stream
    it runs on, algorithmic bytes / duration against 8 TB/s HBM;
@@ -16,7 +24,8 @@ Printed JSON line (rank 0): metric/value/unit per the driver contract, with
    autograd) on a bounded sample, timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
-       python bench.py --workload {split,cfg3,cfg4,cfg5}   (other configurations)
+       python bench.py --workload {cfg1,split,cfg3,cfg4,cfg5,merge}
+       (the other BASELINE.json configurations, one JSON line each)
 """
 
 from __future__ import annotations
@@ -24,6 +33,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -36,8 +46,11 @@ import torch  # noqa: E402
 
 B, HH, WW, HEADS, D, K = 4, 56, 56, 4, 32, 7
 HBM_PEAK_GBS = 8000.0
-COPY_BYTES = 1 << 30   # calibration copy for --profile-calls (1 GiB each way)
 BF16_PEAK_TFLOPS = 2516.6
+FP32_PEAK_TFLOPS = 157.3
+COPY_BYTES = 1 << 30      # calibration copy for --profile-calls (1 GiB each way)
+FLUSH_BYTES = 512 << 20   # written before a "mall_flushed" trial (> the 256 MB MALL)
+WARMUP, TRIALS, DROP = 5, 20, 2   # final_perf_table.py:33-58
 
 
 def algorithmic(n_valid: int):
@@ -58,6 +71,217 @@ def make_inputs(device):
     return [torch.randn(shape, generator=g).to(torch.bfloat16).to(device) for _ in range(4)]
 
 
+# ---------------------------------------------------------------------------
+# timing
+
+_flush_buf = None
+
+
+def mall_flush():
+    """Read FLUSH_BYTES on the current stream (a reduction over a buffer
+    twice the Infinity Cache's 256 MB): evicts the inputs of the next kernel
+    from the MALL and the L2s without leaving dirty lines to write back, so
+    that kernel reads its inputs from HBM."""
+    global _flush_buf
+    if _flush_buf is None:
+        _flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    _flush_buf.sum()
+
+
+def capture(fn, reps: int):
+    """(graph, outputs of the last captured call) for a HIP graph of ``reps``
+    back-to-back calls of ``fn``; (None, None) if capture fails (the caller
+    then runs eagerly)."""
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        out = None
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                out = fn()
+        return graph, out
+    except Exception as exc:
+        print(f"[bench] graph capture unavailable: {exc}", file=sys.stderr, flush=True)
+        return None, None
+
+
+def protocol_ms(run, flush: bool = False) -> dict:
+    """Reference protocol over device time: WARMUP untimed runs, TRIALS
+    event-timed runs of ``run`` on the current stream, the first DROP
+    dropped, median of the rest.  Each trial is preceded on the stream by a
+    MALL flush (``flush``) or a ~50 us device spin, so the host has queued
+    the trial before the GPU reaches it and the interval holds no host
+    submission latency."""
+    for _ in range(WARMUP):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(TRIALS):
+        if flush:
+            mall_flush()
+        else:
+            torch.cuda._sleep(120000)
+        start.record()
+        run()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    kept = times[DROP:]
+    return {"median": statistics.median(kept), "min": min(kept), "max": max(kept)}
+
+
+def call_timing(fn, reps: int = 20) -> dict:
+    """Device time (ms) of one call of ``fn``: warm = median trial of a graph
+    replay of ``reps`` back-to-back calls, divided by ``reps``; single = one
+    call per trial (launch ramp and drain not hidden by a neighbour);
+    mall_flushed = one call per trial right after a MALL flush."""
+    fn()
+    torch.cuda.synchronize()
+    g_many, _ = capture(fn, reps)
+    g_one, _ = capture(fn, 1)
+    many = (lambda: g_many.replay()) if g_many is not None else (
+        lambda: [fn() for _ in range(reps)])
+    one = (lambda: g_one.replay()) if g_one is not None else fn
+    warm = protocol_ms(many)
+    single = protocol_ms(one)
+    cold = protocol_ms(one, flush=True)
+    return {"warm_ms": warm["median"] / reps, "single_ms": single["median"],
+            "flushed_ms": cold["median"]}
+
+
+def _as_list(x):
+    return list(x) if isinstance(x, (tuple, list)) else [x]
+
+
+def step_timing(step, steps: int, warmup: int) -> dict:
+    """A training step through the public API (autograd included): eager
+    host-clocked figures (the K-step loop and the reference's per-call
+    protocol) and graph-replayed device figures (the K-step loop, the
+    protocol median, and one step after a MALL flush)."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+    eager_trials = []
+    for _ in range(TRIALS):
+        t1 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        eager_trials.append((time.perf_counter() - t1) * 1e3)
+    res = {"eager_ms": eager_ms, "eager_protocol_ms": statistics.median(eager_trials[DROP:]),
+           "graph_ms": None, "graph_ok": None, "protocol_ms": None, "single_ms": None,
+           "flushed_ms": None}
+    eager_ref = [g.clone() for g in _as_list(step())]
+    spg = max(d for d in range(1, 11) if steps % d == 0)
+    graph, static_out = capture(step, spg)
+    if graph is None:
+        return res
+    # replays must reproduce the eager result (the backward is deterministic)
+    ok = True
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        ok = ok and all(torch.equal(a, b) for a, b in zip(_as_list(static_out), eager_ref))
+    one, _ = capture(step, 1)
+    for _ in range(max(1, warmup // spg)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps // spg):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    res["graph_ms"] = start.elapsed_time(end) / steps
+    res["graph_ok"] = ok
+    res["protocol_ms"] = protocol_ms(lambda: graph.replay())["median"] / spg
+    if one is not None:
+        res["single_ms"] = protocol_ms(lambda: one.replay())["median"]
+        res["flushed_ms"] = protocol_ms(lambda: one.replay(), flush=True)["median"]
+    return res
+
+
+def _roof(call, nbytes, flops, timing, flop_peak, traffic=None):
+    ms = timing["warm_ms"]
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cold = nbytes / (timing["flushed_ms"] * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic, "call": call,
+            "call_ms": round(ms, 5), "algorithmic_bytes": nbytes, "flops": flops,
+            "flop_frac": round(flops / (ms * 1e-3) / 1e12 / flop_peak, 6),
+            "single_call_ms": round(timing["single_ms"], 5),
+            "mall_flushed": {"call_ms": round(timing["flushed_ms"], 5),
+                             "achieved": round(cold, 2),
+                             "frac": round(cold / HBM_PEAK_GBS, 5)}}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (the oracle: a restatement of the reference's pure backend,
+# computing in the input dtype as pure does)
+
+def _cpu_threads() -> int:
+    aff = len(os.sched_getaffinity(0))
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(aff, env) if env > 0 else aff
+
+
+def cpu_median(fn, budget_s: float = 10.0, min_runs: int = 3, max_runs: int = 5000):
+    """(median seconds, runs, wall seconds, threads) of ``fn`` on the host:
+    one warmup, then runs until ``budget_s`` has passed (at least
+    ``min_runs``, at most ``max_runs``)."""
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (len(times) < max_runs
+                                    and time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times), time.perf_counter() - t_start, threads
+
+
+def _cpu_line(value, unit, threads, sample, runs, wall, per_step_s):
+    return {"value": round(value, 6), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample}; median of {runs} runs in {wall:.1f} s of CPU time",
+            "ms_per_step": round(per_step_s * 1e3, 3)}
+
+
+def cpu_cfg2(total_flops):
+    """Fused fwd+bwd in bf16 on 1 of the 4 images, scaled x4."""
+    from oracle import na as O
+
+    g = torch.Generator().manual_seed(0)
+    shape = (1, HH, WW, HEADS, D)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def once():
+        out = O.na_forward(q, k, v, K, 1, 1, False, None, compute_dtype=torch.bfloat16)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    med, runs, wall, thr = cpu_median(once, 12.0)
+    per_step = med * B
+    return _cpu_line(total_flops / per_step / 1e12, "TFLOP/s", thr,
+                     "oracle fwd+bwd (pure-backend restatement) in bf16 on 1 of the 4 images, "
+                     "scaled x4 to the full step", runs, wall, per_step)
+
+
+# ---------------------------------------------------------------------------
+# config 2 (the driver's bench line)
+
 def run_gpu(args):
     import natten_amd
     from natten_amd._core import _lib, hip
@@ -69,206 +293,137 @@ def run_gpu(args):
     k.requires_grad_(True)
     v.requires_grad_(True)
 
-    def step(dil):
-        out = natten_amd.na2d(q, k, v, K, dilation=dil)
-        return torch.autograd.grad(out, (q, k, v), do)
-
     results = {}
     for dil in (1, 4):
-        for _ in range(args.warmup):
-            step(dil)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step(dil)
-        torch.cuda.synchronize()
-        eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        def raw_step(dil=dil):
+            out = natten_amd.na2d(q, k, v, K, dilation=dil)
+            return torch.autograd.grad(out, (q, k, v), do)
 
-        graph_ms = None
-        graph_ok = None
-        if not args.no_graph:
-            try:
-                eager_ref = [g.clone() for g in step(dil)]
-                s = torch.cuda.Stream()
-                s.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(s):
-                    for _ in range(3):
-                        step(dil)
-                torch.cuda.current_stream().wait_stream(s)
-                # S steps per graph (S divides K), so replays keep the GPU
-                # busy and the timed region measures the device, not the
-                # host's replay launches; K steps = K / S replays
-                spg = max(d for d in range(1, 11) if args.steps % d == 0)
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    for _ in range(spg):
-                        static_grads = step(dil)
-                graph_ok = True
-                for i in range(3):
-                    graph.replay()
-                    torch.cuda.synchronize()
-                    for a, b in zip(static_grads, eager_ref):
-                        graph_ok = graph_ok and torch.equal(a, b)
-                for _ in range(max(1, args.warmup // spg)):
-                    graph.replay()
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                for _ in range(args.steps // spg):
-                    graph.replay()
-                torch.cuda.synchronize()
-                graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-                del graph
-            except Exception as exc:  # report, keep the eager number
-                print(f"[bench] graph capture unavailable: {exc}", file=sys.stderr, flush=True)
-                graph_ms, graph_ok = None, None
-
-        # per-call kernel durations: HIP events around `reps` back-to-back
-        # calls of one library entry point on torch's current stream (the
-        # stream the library launches on), replayed from a HIP graph so host
-        # overhead does not leave the GPU idle between launches
+        step = raw_step
+        if args.no_graph:
+            st = step_timing_eager(step, args.steps, args.warmup)
+        else:
+            st = step_timing(step, args.steps, args.warmup)
+        # per-call device durations: HIP events on torch's current stream
+        # (the stream the library launches on) around graph replays
         qd, kd, vd = q.detach(), k.detach(), v.detach()
-        ks, st, dl, ca = (K, K), (1, 1), (dil, dil), (False, False)
-        out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
-        fwd_ms = time_calls(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None),
-                            args.steps)
-        bwd_ms = time_calls(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st,
-                                                       dl, ca, None), args.steps)
-        results[dil] = dict(eager_ms=eager_ms, graph_ms=graph_ms, graph_ok=graph_ok,
-                            fwd_ms=fwd_ms, bwd_ms=bwd_ms)
+        ks, stt, dl, ca = (K, K), (1, 1), (dil, dil), (False, False)
+        out, lse = hip.fused_forward(qd, kd, vd, ks, stt, dl, ca, None)
+        fwd = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, stt, dl, ca, None))
+        bwd = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, stt,
+                                                     dl, ca, None))
+        results[dil] = dict(st, fwd=fwd, bwd=bwd)
     return results
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_hbm_traffic.md")
+def step_timing_eager(step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"eager_ms": ms, "eager_protocol_ms": None, "graph_ms": None, "graph_ok": None,
+            "protocol_ms": None, "single_ms": None, "flushed_ms": None}
+
+
+PROFILE_SUMMARIES = {
+    "cfg2": [os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_hbm_traffic.md"),
+             os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_lean_fwd_bwd.md")],
+    "cfg3": [os.path.join(ROOT, "profiles", "na3d_16x32x32_k377_causal_bf16_lean_fwd_bwd.md")],
+}
 CALL_KERNEL = {"na_fwd": "k_wfwd", "na_bwd": "k_wbwd"}
 
 
-def measured_traffic(call: str):
-    """HBM bytes per launch of the call's kernel from the committed counter
-    summary (FETCH_SIZE / WRITE_SIZE runs, copy-calibrated), or None."""
-    try:
-        text = open(TRAFFIC_PROFILE).read()
-    except OSError:
-        return None
-    for line in text.splitlines():
-        parts = line.split()
-        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and \
-                parts[1] == CALL_KERNEL.get(call):
-            return int(parts[2])
+def _profile_figure(key: str, call: str, workload: str, kind):
+    """A per-kernel figure (``<key> <kernel> <value>`` lines) from the
+    committed rocprofv3 counter summaries of the workload, or None."""
+    for path in PROFILE_SUMMARIES.get(workload, []):
+        try:
+            text = open(path).read()
+        except OSError:
+            continue
+        for line in text.splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == key and parts[1] == CALL_KERNEL.get(call):
+                return kind(parts[2])
     return None
 
 
-def time_calls(fn, steps: int, reps: int = 20) -> float:
-    """Average device time (ms) of one call of ``fn``: events bracket a
-    graph replay of ``reps`` back-to-back calls (eager loop if capture
-    fails), repeated ``steps`` times."""
-    for _ in range(3):
-        fn()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    graph = None
-    try:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            fn()
-        torch.cuda.current_stream().wait_stream(s)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                fn()
-    except Exception as exc:
-        print(f"[bench] call-timing capture unavailable: {exc}", file=sys.stderr, flush=True)
-        graph = None
-    total = 0.0
-    n = max(steps // 4, 5)
-    for _ in range(n):
-        start.record()
-        if graph is not None:
-            graph.replay()
-        else:
-            for _ in range(reps):
-                fn()
-        end.record()
-        torch.cuda.synchronize()
-        total += start.elapsed_time(end)
-    return total / (n * reps)
+def measured_traffic(call: str, workload: str = "cfg2"):
+    """HBM bytes per launch of the call's kernel (FETCH_SIZE / WRITE_SIZE
+    counter runs, copy-calibrated), or None."""
+    return _profile_figure("traffic_bytes_per_launch", call, workload, int)
 
 
-def profile_calls(n: int, workload: str = "cfg2") -> None:
-    """Run n calls of each library entry point of a workload (for rocprofv3
-    counter passes); cfg2 also runs a calibration copy of COPY_BYTES."""
-    from natten_amd._core import hip
+def measured_mfma_busy(call: str, workload: str = "cfg2"):
+    """Matrix-core busy fraction of the call's kernel (SQ_VALU_MFMA_BUSY_CYCLES
+    over 1024 SIMDs x launch duration x 2.4 GHz), or None."""
+    return _profile_figure("mfma_busy_frac", call, workload, float)
 
-    q, k, v, do = make_inputs(torch.device("cuda:0"))
-    if workload == "split":
-        a = ((K, K), (1, 1), (1, 1), (False, False))
-        logits = hip.qk_forward(q, k, *a, None)
-        attn = torch.softmax(logits, -1)
-        for _ in range(n):
-            hip.qk_forward(q, k, *a, None)
-            hip.av_forward(attn, v, *a)
-            hip.qk_backward(q, k, attn, *a, None)
-            hip.av_backward(attn, v, do, *a)
-        torch.cuda.synchronize()
-        print(f"profile-calls: {n} x split qk/av forward and backward done", flush=True)
-        return
-    if workload == "cfg5":
-        Bc, L, H, Dc = 8, 2048, 12, 12
-        qa, ka, va = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
-        rpb = _gen((H, 13), torch.float32, 17, std=0.02)
-        logits = hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
-        attn = torch.softmax(logits, -1)
-        for _ in range(n):
-            hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
-            hip.rpb_av_forward(attn, va, 7, 1)
-            hip.rpb_qk_backward(qa, ka, attn, 7, 1, 0.288)
-            hip.rpb_av_backward(attn, va, va, 7, 1)
-        torch.cuda.synchronize()
-        print(f"profile-calls: {n} x allin1 K=7 d=1 forward and backward done", flush=True)
-        return
-    if workload == "cfg4":
-        Bc, L, H, Hkv, Dc, nx = 8, 4096, 16, 4, 64, 16
-        qc = _gen((Bc, L, H, Dc), torch.float16, 0)
-        kc, vc = (_gen((Bc, L, Hkv, Dc), torch.float16, s) for s in (1, 2))
-        ak, av = (_gen((Bc, nx, Hkv, Dc), torch.float16, s) for s in (3, 4))
-        g = torch.Generator().manual_seed(5)
-        se = torch.randint(1024, 4097, (Bc, 1), generator=g, dtype=torch.int32).to("cuda:0")
-        a = ((63,), (1,), (2,), (False,), None)
-        kw = dict(extra_k=ak, extra_v=av, sample_extent=se, varlen_clamped=True)
-        out, lse = hip.fused_forward(qc, kc, vc, *a, **kw)
-        doc = _gen(out.shape, torch.float16, 6)
-        for _ in range(n):
-            hip.fused_forward(qc, kc, vc, *a, **kw)
-            hip.fused_backward(qc, kc, vc, out, lse, doc, None, *a, **kw)
-        torch.cuda.synchronize()
-        print(f"profile-calls: {n} x config-4 forward and backward (with extras) done",
-              flush=True)
-        return
-    if workload == "merge":
-        shape = (1, 16, 32, 32, 8, 64)
-        outs = [_gen(shape, torch.bfloat16, s) for s in range(2)]
-        lses = [_gen(shape[:-1], torch.float32, 20 + s) for s in range(2)]
-        dout, dlse = _gen(shape, torch.bfloat16, 40), _gen(shape[:-1], torch.float32, 41)
-        for _ in range(n):
-            hip.merge_forward(outs, lses)
-            hip.merge_backward(outs, lses, dout, dlse, [True] * 2, [True] * 2)
-        torch.cuda.synchronize()
-        print(f"profile-calls: {n} x merge forward and backward (2 parts, config-3 size) done",
-              flush=True)
-        return
-    a = ((K, K), (1, 1), (1, 1), (False, False), None)
-    out, lse = hip.fused_forward(q, k, v, *a)
-    # calibration for the HBM byte counters: a plain device copy of a known
-    # size (COPY_BYTES read + COPY_BYTES written), far larger than the caches
-    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=q.device).uniform_()
-    dst = torch.empty_like(src)
-    for _ in range(n):
-        dst.copy_(src)
-        hip.fused_forward(q, k, v, *a)
-        hip.fused_backward(q, k, v, out, lse, do, None, *a)
-    torch.cuda.synchronize()
-    print(f"profile-calls: {n} copies of {COPY_BYTES} B, {n} forward + {n} backward calls done",
-          flush=True)
+
+def main_line(args):
+    res = run_gpu(args)
+    fwd_f, bwd_f, fwd_b, bwd_b = algorithmic(K * K)
+    r1 = res[1]
+    graph_good = r1["graph_ms"] is not None and r1["graph_ok"]
+    step_ms = r1["graph_ms"] if graph_good else r1["eager_ms"]
+    total_flops = fwd_f + bwd_f
+    value = total_flops / (step_ms * 1e-3) / 1e12
+
+    # dominant call: the one with the larger event-timed duration
+    if r1["bwd"]["warm_ms"] >= r1["fwd"]["warm_ms"]:
+        dom, timing, dom_bytes, dom_flops = "na_bwd", r1["bwd"], bwd_b, bwd_f
+    else:
+        dom, timing, dom_bytes, dom_flops = "na_fwd", r1["fwd"], fwd_b, fwd_f
+    roofline = _roof(dom, dom_bytes, dom_flops, timing, BF16_PEAK_TFLOPS,
+                     measured_traffic(dom))
+    roofline["mfma_frac"] = roofline.pop("flop_frac")
+    roofline["mfma_busy"] = measured_mfma_busy(dom)
+
+    cpu = None if args.no_cpu else cpu_cfg2(total_flops)
+
+    def rnd(x):
+        return None if x is None else round(x, 5)
+
+    def timing_of(r):
+        return {"graph_ms": rnd(r["graph_ms"]), "graph_replays_match_eager": r["graph_ok"],
+                "protocol_median_ms": rnd(r["protocol_ms"]),
+                "single_step_ms": rnd(r["single_ms"]),
+                "mall_flushed_step_ms": rnd(r["flushed_ms"]),
+                "eager_ms": rnd(r["eager_ms"]), "eager_protocol_median_ms":
+                    rnd(r["eager_protocol_ms"]),
+                "fwd_call_ms": rnd(r["fwd"]["warm_ms"]), "bwd_call_ms": rnd(r["bwd"]["warm_ms"]),
+                "fwd_call_single_ms": rnd(r["fwd"]["single_ms"]),
+                "bwd_call_single_ms": rnd(r["bwd"]["single_ms"]),
+                "fwd_call_flushed_ms": rnd(r["fwd"]["flushed_ms"]),
+                "bwd_call_flushed_ms": rnd(r["bwd"]["flushed_ms"])}
+
+    return {
+        "metric": "na2d 56x56 k7 bf16 fwd+bwd ms & TFLOP/s; % MFMA/HBM roofline, 1 MI355X",
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), seed 0",
+        "config": {"workload": "na2d fused fwd+bwd, B=4 56x56 heads=4 head_dim=32 k=7 "
+                               "dilation=1 non-causal",
+                   "global_batch": B, "spatial": [HH, WW], "heads": HEADS, "head_dim": D,
+                   "kernel_size": K, "dilation": 1, "parallelism": "none (1 GPU)"},
+        "timing": dict(timing_of(r1), protocol="warmup 5, 20 trials, first 2 dropped, median "
+                                               "(final_perf_table.py:33-58)"),
+        "dilation4": timing_of(res[4]),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
 
 
 # ---------------------------------------------------------------------------
@@ -290,50 +445,97 @@ def _valid_pairs(spatial, ks, dil, caus):
     return total
 
 
-def _roof(call, nbytes, flops, ms, flop_peak):
-    achieved = nbytes / (ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None, "call": call,
-            "call_ms": round(ms, 5), "bytes": nbytes, "flops": flops,
-            "flop_frac": round(flops / (ms * 1e-3) / 1e12 / flop_peak, 6)}
-
-
-def _line(metric, value, unit, ms, dtype, config, roofline, extra=None):
+def _line(metric, value, unit, ms, dtype, config, roofline, cpu, extra=None):
     line = {"metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": dtype, "data": "synthetic, seed 0", "config": config,
-            "roofline": roofline, "cpu_baseline": None}
+            "roofline": roofline, "cpu_baseline": cpu}
     line.update(extra or {})
     return line
+
+
+def _step_ms(step, args):
+    r = step_timing(step, args.steps, args.warmup)
+    ok = r["graph_ms"] is not None and r["graph_ok"] is not False
+    ms = r["graph_ms"] if ok else r["eager_ms"]
+    return ms, {k2: (round(v2, 5) if isinstance(v2, float) else v2) for k2, v2 in r.items()}
+
+
+def wl_cfg1(args):
+    """Config 1: na1d fp32 forward [2,64,4,32], k 7 (the README quick-start
+    shape, which the reference runs on its CPU backend)."""
+    import natten_amd
+    from natten_amd._core import hip
+    from oracle import na as O
+
+    Bc, L, H, Dc, Kc = 2, 64, 4, 32, 7
+    q, k, v = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
+    a = ((Kc,), (1,), (1,), (False,), None)
+    step_ms, st = _step_ms(lambda: natten_amd.na1d(q, k, v, Kc), args)
+    t = call_timing(lambda: hip.fused_forward(q, k, v, *a, want_lse=False))
+    flops = Bc * L * H * 4 * Dc * Kc
+    nbytes = 4 * Bc * L * H * Dc * 4
+    roof = _roof("na_fwd", nbytes, flops, t, FP32_PEAK_TFLOPS)
+    cpu = None
+    if not args.no_cpu:
+        qc, kc, vc = (x.cpu() for x in (q, k, v))
+        med, runs, wall, thr = cpu_median(
+            lambda: O.na_forward(qc, kc, vc, Kc, compute_dtype=torch.float32), 10.0)
+        cpu = _cpu_line(flops / med / 1e12, "TFLOP/s", thr,
+                        "oracle forward (pure-backend restatement) in fp32 on the full workload",
+                        runs, wall, med)
+    cfg = {"workload": "na1d fused forward fp32 [2,64,4,32] k=7 d=1 non-causal", "global_batch": Bc}
+    return _line("na1d 64 k7 fp32 fwd ms & TFLOP/s, 1 MI355X", flops / (step_ms * 1e-3) / 1e12,
+                 "TFLOP/s", step_ms, "f32", cfg, roof, cpu,
+                 {"timing": dict(st, fwd_call_ms=round(t["warm_ms"], 5),
+                                 fwd_call_flushed_ms=round(t["flushed_ms"], 5)),
+                  "note": "a 262 KB problem: the time is the launch floor (an empty kernel "
+                          "replayed the same way costs about as much)"})
 
 
 def wl_split(args):
     """Config 2s: na2d_qk -> softmax -> na2d_av, bf16, B=4 56x56 heads 4 D 32 k 7."""
     from natten_amd._core import hip
+    from oracle import na as O
 
     q, k, v, do = make_inputs(torch.device("cuda:0"))
     a = ((K, K), (1, 1), (1, 1), (False, False))
     logits = hip.qk_forward(q, k, *a, None)
     attn = torch.softmax(logits, -1)
-    qk_ms = time_calls(lambda: hip.qk_forward(q, k, *a, None), args.steps)
-    av_ms = time_calls(lambda: hip.av_forward(attn, v, *a), args.steps)
+    tq = call_timing(lambda: hip.qk_forward(q, k, *a, None))
+    ta = call_timing(lambda: hip.av_forward(attn, v, *a))
     dl = _gen(logits.shape, torch.bfloat16, 5)
-    qkb_ms = time_calls(lambda: hip.qk_backward(q, k, dl, *a, None), args.steps)
-    avb_ms = time_calls(lambda: hip.av_backward(attn, v, do, *a), args.steps)
+    tqb = call_timing(lambda: hip.qk_backward(q, k, dl, *a, None))
+    tab = call_timing(lambda: hip.av_backward(attn, v, do, *a))
     t = B * HH * WW * HEADS * D * 2
     lg = B * HH * WW * HEADS * K * K * 2
     pairs = B * HEADS * _valid_pairs((HH, WW), (K, K), (1, 1), (False, False))
     qk_b, av_b = 2 * t + lg, lg + 2 * t
     fl = 2 * D * pairs
-    rq = _roof("na_qk_fwd", qk_b, fl, qk_ms, BF16_PEAK_TFLOPS)
-    ra = _roof("na_av_fwd", av_b, fl, av_ms, BF16_PEAK_TFLOPS)
-    value = (qk_b + av_b) / ((qk_ms + av_ms) * 1e-3) / 1e9
+    rq = _roof("na_qk_fwd", qk_b, fl, tq, BF16_PEAK_TFLOPS)
+    ra = _roof("na_av_fwd", av_b, fl, ta, BF16_PEAK_TFLOPS)
+    ms = tq["warm_ms"] + ta["warm_ms"]
+    value = (qk_b + av_b) / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        qc, kc, vc = (x[:1].cpu() for x in (q, k, v))
+
+        def once():
+            lg_ = O.na_qk(qc, kc, K, compute_dtype=torch.bfloat16)
+            O.na_av(torch.softmax(lg_, -1), vc, K, compute_dtype=torch.bfloat16)
+
+        med, runs, wall, thr = cpu_median(once, 10.0)
+        cpu = _cpu_line((qk_b + av_b) / (med * B) / 1e9, "GB/s", thr,
+                        "oracle split qk -> softmax -> av (pure-backend restatement) in bf16 on "
+                        "1 of the 4 images, scaled x4", runs, wall, med * B)
     cfg = {"workload": "na2d_qk + na2d_av split forward, bf16 B=4 56x56 heads=4 head_dim=32 "
                        "k=7 dilation=1", "global_batch": B}
-    return _line("na2d split qk/av bf16 HBM GB/s, 1 MI355X", value, "GB/s", qk_ms + av_ms,
-                 "bf16", cfg, rq if qk_ms >= av_ms else ra,
-                 {"calls": {"qk": rq, "av": ra,
-                            "qk_bwd_ms": round(qkb_ms, 5), "av_bwd_ms": round(avb_ms, 5)}})
+    return _line("na2d split qk/av bf16 HBM GB/s, 1 MI355X", value, "GB/s", ms, "bf16", cfg,
+                 rq if tq["warm_ms"] >= ta["warm_ms"] else ra, cpu,
+                 {"calls": {"qk": rq, "av": ra, "qk_bwd_ms": round(tqb["warm_ms"], 5),
+                            "av_bwd_ms": round(tab["warm_ms"], 5),
+                            "qk_bwd_flushed_ms": round(tqb["flushed_ms"], 5),
+                            "av_bwd_flushed_ms": round(tab["flushed_ms"], 5)}})
 
 
 def wl_cfg3(args):
@@ -341,8 +543,8 @@ def wl_cfg3(args):
     causal (T,F,F)."""
     import natten_amd
     from natten_amd._core import hip
+    from oracle import full as F
 
-    dev = torch.device("cuda:0")
     shape = (1, 16, 32, 32, 8, 64)
     q, k, v, do = (_gen(shape, torch.bfloat16, s) for s in range(4))
     ks, st, dl, ca = (3, 7, 7), (1, 1, 1), (1, 1, 1), (True, False, False)
@@ -353,28 +555,57 @@ def wl_cfg3(args):
         out, lse = natten_amd.na3d(q, k, v, ks, is_causal=ca, return_lse=True)
         return torch.autograd.grad(out, (q, k, v), do)
 
-    step_ms = _eager_ms(step, args)
+    step_ms, stt = _step_ms(step, args)
     qd, kd, vd = q.detach(), k.detach(), v.detach()
     out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
-    f_ms = time_calls(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None), args.steps)
-    b_ms = time_calls(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca,
-                                                 None), args.steps)
+    tf = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None))
+    tb = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca,
+                                                None))
     pairs = 8 * _valid_pairs(shape[1:4], ks, dl, ca)
-    tb = 16 * 32 * 32 * 8 * 64 * 2
+    tb_ = 16 * 32 * 32 * 8 * 64 * 2
     lse_b = 16 * 32 * 32 * 8 * 4
     fwd_f, bwd_f = 4 * 64 * pairs, 8 * 64 * pairs
-    fwd_b, bwd_b = 4 * tb + lse_b, 8 * tb + lse_b
-    rf = _roof("na_fwd", fwd_b, fwd_f, f_ms, BF16_PEAK_TFLOPS)
-    rb = _roof("na_bwd", bwd_b, bwd_f, b_ms, BF16_PEAK_TFLOPS)
+    fwd_b, bwd_b = 4 * tb_ + lse_b, 8 * tb_ + lse_b
+    rf = _roof("na_fwd", fwd_b, fwd_f, tf, BF16_PEAK_TFLOPS, measured_traffic("na_fwd", "cfg3"))
+    rb = _roof("na_bwd", bwd_b, bwd_f, tb, BF16_PEAK_TFLOPS, measured_traffic("na_bwd", "cfg3"))
+    rf["mfma_busy"] = measured_mfma_busy("na_fwd", "cfg3")
+    rb["mfma_busy"] = measured_mfma_busy("na_bwd", "cfg3")
+    cpu = None
+    if not args.no_cpu:
+        qc, kc, vc, doc = (x.detach().cpu() for x in (q, k, v, do))
+        rows = 512  # of the 16384 query positions
+
+        def once():
+            F.fused(qc, kc, vc, ks, 1, 1, ca, None, doc, None, chunk=256,
+                    compute_dtype=torch.bfloat16, max_rows=rows)
+
+        med, runs, wall, thr = cpu_median(once, 10.0)
+        per_step = med * (16 * 32 * 32) / rows
+        cpu = _cpu_line((fwd_f + bwd_f) / per_step / 1e12, "TFLOP/s", thr,
+                        f"oracle fwd+bwd (pure-backend restatement: gather, softmax, weighted "
+                        f"sum, autograd) in bf16 on the first {rows} of 16384 query positions "
+                        f"in chunks of 256, scaled to all", runs, wall, per_step)
     cfg = {"workload": "na3d fused fwd+bwd with return_lse, bf16 [1,16,32,32,8,64] "
                        "k=(3,7,7) causal=(T,F,F)", "global_batch": 1}
     return _line("na3d 16x32x32 k(3,7,7) causal bf16 fwd+bwd TFLOP/s, 1 MI355X",
                  (fwd_f + bwd_f) / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "bf16", cfg,
-                 rb if b_ms >= f_ms else rf,
-                 {"timing": {"fwd_call_ms": round(f_ms, 5), "bwd_call_ms": round(b_ms, 5),
-                             "calls_tflops": round((fwd_f + bwd_f) / ((f_ms + b_ms) * 1e-3)
-                                                   / 1e12, 3)},
+                 rb if tb["warm_ms"] >= tf["warm_ms"] else rf, cpu,
+                 {"timing": dict(stt, fwd_call_ms=round(tf["warm_ms"], 5),
+                                 bwd_call_ms=round(tb["warm_ms"], 5),
+                                 calls_tflops=round((fwd_f + bwd_f) / ((tf["warm_ms"] +
+                                                                        tb["warm_ms"]) * 1e-3)
+                                                    / 1e12, 3)),
                   "calls": {"fwd": rf, "bwd": rb}})
+
+
+def _cfg4_inputs():
+    Bc, L, H, Hkv, Dc, nx = 8, 4096, 16, 4, 64, 16
+    q = _gen((Bc, L, H, Dc), torch.float16, 0)
+    k, v = (_gen((Bc, L, Hkv, Dc), torch.float16, s) for s in (1, 2))
+    ak, av = (_gen((Bc, nx, Hkv, Dc), torch.float16, s) for s in (3, 4))
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(1024, 4097, (Bc,), generator=g, dtype=torch.int32)
+    return q, k, v, ak, av, lens
 
 
 def wl_cfg4(args):
@@ -382,48 +613,54 @@ def wl_cfg4(args):
     q [8,4096,16,64], k/v [8,4096,4,64], seq_lens ~ U{1024..4096}, k 63, d 2."""
     import natten_amd
     from natten_amd._core import hip
+    from oracle import full as F
 
-    Bc, L, H, Hkv, Dc, nx = 8, 4096, 16, 4, 64, 16
-    q = _gen((Bc, L, H, Dc), torch.float16, 0)
-    k, v = (_gen((Bc, L, Hkv, Dc), torch.float16, s) for s in (1, 2))
-    ak, av = (_gen((Bc, nx, Hkv, Dc), torch.float16, s) for s in (3, 4))
-    g = torch.Generator().manual_seed(5)
-    lens = torch.randint(1024, 4097, (Bc,), generator=g, dtype=torch.int32)
-    lens_d = lens.to("cuda:0")
-
-    def step():
-        return natten_amd.na1d_varlen_gqa(q, k, v, lens_d, 63, 2, additional_keys=ak,
-                                          additional_values=av)
-
-    step_ms = _eager_ms(step, args)
-    se = lens_d.reshape(Bc, 1).contiguous()
-    f_ms = time_calls(lambda: hip.fused_forward(q, k, v, (63,), (1,), (2,), (False,), None,
-                                                extra_k=ak, extra_v=av, sample_extent=se,
-                                                varlen_clamped=True),
-                      args.steps)
+    q, k, v, ak, av, lens = _cfg4_inputs()
+    Bc, L, H, Dc = q.shape
+    Hkv, nx = k.shape[2], ak.shape[1]
+    # host-side lengths (validated on the host; their device copy is cached,
+    # so the call neither synchronises nor copies and a graph can hold it)
+    step_ms, stt = _step_ms(lambda: natten_amd.na1d_varlen_gqa(
+        q, k, v, lens, 63, 2, additional_keys=ak, additional_values=av), args)
+    se = lens.to("cuda:0").reshape(Bc, 1).contiguous()
+    kw = dict(extra_k=ak, extra_v=av, sample_extent=se, varlen_clamped=True)
+    a = ((63,), (1,), (2,), (False,), None)
+    tf = call_timing(lambda: hip.fused_forward(q, k, v, *a, **kw))
     # the backward (dq, dk, dv and the additional tokens' gradients), timed
     # alongside; not part of `value`
-    out, lse = hip.fused_forward(q, k, v, (63,), (1,), (2,), (False,), None, extra_k=ak,
-                                 extra_v=av, sample_extent=se, varlen_clamped=True)
+    out, lse = hip.fused_forward(q, k, v, *a, **kw)
     do = _gen(out.shape, torch.float16, 6)
-    b_ms = time_calls(lambda: hip.fused_backward(q, k, v, out, lse, do, None, (63,), (1,),
-                                                 (2,), (False,), None, extra_k=ak,
-                                                 extra_v=av, sample_extent=se,
-                                                 varlen_clamped=True),
-                      args.steps)
+    tb = call_timing(lambda: hip.fused_backward(q, k, v, out, lse, do, None, *a, **kw))
     tokens = int(lens.sum())
     flops = tokens * H * 4 * Dc * (63 + nx)
     nbytes = tokens * (H * Dc * 2 + 2 * Hkv * Dc * 2 + H * Dc * 2) + 2 * Bc * nx * Hkv * Dc * 2
     nbytes_pad = nbytes + (Bc * L - tokens) * H * Dc * 2  # padded rows written as zeros
-    rf = _roof("na_fwd", nbytes_pad, flops, f_ms, BF16_PEAK_TFLOPS)
+    rf = _roof("na_fwd", nbytes_pad, flops, tf, BF16_PEAK_TFLOPS)
+    cpu = None
+    if not args.no_cpu:
+        rows = 1024
+        qc, kc, vc, akc, avc = (x.cpu() for x in (q, k, v, ak, av))
+
+        def once():
+            F.fused(qc[:1], kc[:1], vc[:1], 63, 1, 2, False, None, extra_k=akc[:1],
+                    extra_v=avc[:1], sizes=lens[:1], chunk=256, compute_dtype=torch.float16,
+                    max_rows=rows)
+
+        med, runs, wall, thr = cpu_median(once, 10.0)
+        per_step = med * tokens / rows
+        cpu = _cpu_line(flops / per_step / 1e12, "TFLOP/s", thr,
+                        f"oracle varlen GQA forward with the 16 extra tokens in the softmax "
+                        f"(pure-backend restatement) in fp16 on {rows} query rows of sample 0, "
+                        f"scaled to all {tokens} tokens", runs, wall, per_step)
     cfg = {"workload": "na1d varlen GQA (16 q heads / 4 kv heads) + 16 additional tokens, fp16 "
                        "forward, [8,4096,*,64], k=63 d=2", "global_batch": Bc,
            "seq_lens": lens.tolist(), "tokens": tokens}
     return _line("na1d varlen gqa+extra fp16 fwd TFLOP/s, 1 MI355X",
-                 flops / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "fp16", cfg, rf,
-                 {"timing": {"fwd_call_ms": round(f_ms, 5),
-                             "call_tflops": round(flops / (f_ms * 1e-3) / 1e12, 3),
-                             "bwd_call_ms": round(b_ms, 5)}})
+                 flops / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "fp16", cfg, rf, cpu,
+                 {"timing": dict(stt, fwd_call_ms=round(tf["warm_ms"], 5),
+                                 call_tflops=round(flops / (tf["warm_ms"] * 1e-3) / 1e12, 3),
+                                 bwd_call_ms=round(tb["warm_ms"], 5),
+                                 bwd_call_flushed_ms=round(tb["flushed_ms"], 5))})
 
 
 def wl_cfg5(args):
@@ -431,6 +668,7 @@ def wl_cfg5(args):
     K in {3,5,7} x d in {1,2,4,8}, scale 0.288 (forward, plus the backward
     calls timed alongside)."""
     from natten_amd._core import hip
+    from oracle import na as O
 
     Bc, L, H, Dc = 8, 2048, 12, 12
     q, k, v = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
@@ -443,31 +681,46 @@ def wl_cfg5(args):
         for d in (1, 2, 4, 8):
             logits = hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288)
             attn = torch.softmax(logits, -1)
-            qk_ms = time_calls(lambda: hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288), args.steps)
-            av_ms = time_calls(lambda: hip.rpb_av_forward(attn, v, Kx, d), args.steps)
-            qkb_ms = time_calls(lambda: hip.rpb_qk_backward(q, k, attn, Kx, d, 0.288),
-                                args.steps)
-            avb_ms = time_calls(lambda: hip.rpb_av_backward(attn, v, v, Kx, d), args.steps)
+            tq = call_timing(lambda: hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288))
+            ta = call_timing(lambda: hip.rpb_av_forward(attn, v, Kx, d))
+            tqb = call_timing(lambda: hip.rpb_qk_backward(q, k, attn, Kx, d, 0.288))
+            tab = call_timing(lambda: hip.rpb_av_backward(attn, v, v, Kx, d))
             lg = rows * Kx * 4
             qk_b, av_b = 2 * t + lg, lg + 2 * t
-            rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, qk_ms, 157.3)
-            ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, av_ms, 157.3)
-            table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd_ms": round(qkb_ms, 5),
-                                    "av_bwd_ms": round(avb_ms, 5)}
+            rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, tq, FP32_PEAK_TFLOPS)
+            ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, ta, FP32_PEAK_TFLOPS)
+            table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd_ms": round(tqb["warm_ms"], 5),
+                                    "av_bwd_ms": round(tab["warm_ms"], 5)}
             if Kx == 7 and d == 1:
-                best = (rq, ra, qk_ms + av_ms, (qk_b + av_b) / ((qk_ms + av_ms) * 1e-3) / 1e9)
-    rq, ra, ms, gbs = best
+                ms = tq["warm_ms"] + ta["warm_ms"]
+                best = (rq, ra, ms, (qk_b + av_b) / (ms * 1e-3) / 1e9, qk_b + av_b, rpb)
+    rq, ra, ms, gbs, pair_bytes, rpb7 = best
     # practical ceiling at this size: a device copy moving the same bytes as
     # one K=7 call (read + write of 12.2 MB)
-    src = torch.empty((rq["bytes"] // 2) // 4, dtype=torch.float32, device="cuda:0")
+    src = torch.empty((rq["algorithmic_bytes"] // 2) // 4, dtype=torch.float32, device="cuda:0")
     dst = torch.empty_like(src)
-    copy_ms = time_calls(lambda: dst.copy_(src), args.steps)
-    table["copy_same_bytes"] = {"call_ms": round(copy_ms, 5),
-                                "achieved": round(rq["bytes"] / (copy_ms * 1e-3) / 1e9, 2)}
+    tc = call_timing(lambda: dst.copy_(src))
+    table["copy_same_bytes"] = {"call_ms": round(tc["warm_ms"], 5),
+                                "achieved": round(rq["algorithmic_bytes"] /
+                                                  (tc["warm_ms"] * 1e-3) / 1e9, 2),
+                                "flushed_call_ms": round(tc["flushed_ms"], 5)}
+    cpu = None
+    if not args.no_cpu:
+        qc, kc, vc = (x[:1].cpu() for x in (q, k, v))
+        rc = rpb7.cpu()
+
+        def once():
+            lg_ = O.qk_rpb(qc, kc, rc, 7, 1, 0.288, compute_dtype=torch.float32)
+            O.av_rpb(torch.softmax(lg_, -1), vc, 7, 1, compute_dtype=torch.float32)
+
+        med, runs, wall, thr = cpu_median(once, 10.0)
+        cpu = _cpu_line(pair_bytes / (med * Bc) / 1e9, "GB/s", thr,
+                        "oracle qk_rpb -> softmax -> av (allin1 MLX-fallback restatement) in fp32 "
+                        "at K=7 d=1 on 1 of the 8 batch elements, scaled x8", runs, wall, med * Bc)
     cfg = {"workload": "allin1 na1d_qk_rpb + na1d_av_fused fp32 [8,2048,12,12] K=7 d=1 "
                        "(all K x d in 'sweep')", "global_batch": Bc}
     return _line("allin1 qk_rpb+av fp32 HBM GB/s (K=7 d=1), 1 MI355X", gbs, "GB/s", ms, "f32",
-                 cfg, rq if rq["call_ms"] >= ra["call_ms"] else ra, {"sweep": table})
+                 cfg, rq if rq["call_ms"] >= ra["call_ms"] else ra, cpu, {"sweep": table})
 
 
 def wl_merge(args):
@@ -478,6 +731,7 @@ def wl_merge(args):
     import torch.nn.functional as tF
 
     from natten_amd._core import hip
+    from oracle import na as O
 
     def torch_merge(outs, lses):
         ls = [l.unsqueeze(-1) for l in lses]
@@ -504,63 +758,116 @@ def wl_merge(args):
             part = rows * Dm * 2 + rows * 4
             fwd_b = (n + 1) * part
             bwd_b = (2 * n + 1) * part
-            f_ms = time_calls(lambda: hip.merge_forward(outs, lses), args.steps)
-            b_ms = time_calls(lambda: hip.merge_backward(outs, lses, dout, dlse, [True] * n,
-                                                         [True] * n), args.steps)
-            t_ms = time_calls(lambda: torch_merge(outs, lses), args.steps)
-            rf = _roof("na_merge_fwd", fwd_b, 2 * n * rows * Dm, f_ms, 157.3)
-            rb = _roof("na_merge_bwd", bwd_b, 4 * n * rows * Dm, b_ms, 157.3)
-            table[f"{name}_n{n}"] = {"fwd": rf, "bwd": rb, "torch_sigmoid_form_ms": round(t_ms, 5)}
+            tf = call_timing(lambda: hip.merge_forward(outs, lses))
+            tb = call_timing(lambda: hip.merge_backward(outs, lses, dout, dlse, [True] * n,
+                                                        [True] * n))
+            tt = call_timing(lambda: torch_merge(outs, lses))
+            rf = _roof("na_merge_fwd", fwd_b, 2 * n * rows * Dm, tf, FP32_PEAK_TFLOPS)
+            rb = _roof("na_merge_bwd", bwd_b, 4 * n * rows * Dm, tb, FP32_PEAK_TFLOPS)
+            table[f"{name}_n{n}"] = {"fwd": rf, "bwd": rb,
+                                     "torch_sigmoid_form_ms": round(tt["warm_ms"], 5)}
             if name == "cfg3" and n == 2:
-                main = (rf, rb, f_ms + b_ms, (fwd_b + bwd_b) / ((f_ms + b_ms) * 1e-3) / 1e9)
-    rf, rb, ms, gbs = main
+                ms = tf["warm_ms"] + tb["warm_ms"]
+                main = (rf, rb, ms, (fwd_b + bwd_b) / (ms * 1e-3) / 1e9, fwd_b,
+                        [o.cpu() for o in outs], [l.cpu() for l in lses])
+    rf, rb, ms, gbs, fwd_b, outs_c, lses_c = main
+    cpu = None
+    if not args.no_cpu:
+        med, runs, wall, thr = cpu_median(lambda: O.merge_attentions(outs_c, lses_c), 10.0)
+        cpu = _cpu_line(fwd_b / med / 1e9, "GB/s", thr,
+                        "oracle merge_attentions (merge.py sigmoid form, float32 inside) forward "
+                        "on the full 2-part config-3-size merge", runs, wall, med)
     cfg = {"workload": "merge_attentions, 2 bf16 parts [1,16,32,32,8,64] + fp32 LSEs, "
                        "forward + backward (other sizes in 'sweep')", "global_batch": 1}
     return _line("merge_attentions bf16 fwd+bwd HBM GB/s, 1 MI355X", gbs, "GB/s", ms, "bf16",
-                 cfg, rf if rf["call_ms"] >= rb["call_ms"] else rb, {"sweep": table})
+                 cfg, rf if rf["call_ms"] >= rb["call_ms"] else rb, cpu, {"sweep": table})
 
 
-def _eager_ms(step, args):
-    for _ in range(args.warmup):
-        step()
+WORKLOADS = {"cfg1": wl_cfg1, "split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4,
+             "cfg5": wl_cfg5, "merge": wl_merge}
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 counter passes
+
+def profile_calls(n: int, workload: str = "cfg2") -> None:
+    """Run n calls of each library entry point of a workload (for rocprofv3
+    counter passes); cfg2 and cfg3 also run a calibration copy of
+    COPY_BYTES each time."""
+    from natten_amd._core import hip
+
+    if workload == "split":
+        q, k, v, do = make_inputs(torch.device("cuda:0"))
+        a = ((K, K), (1, 1), (1, 1), (False, False))
+        logits = hip.qk_forward(q, k, *a, None)
+        attn = torch.softmax(logits, -1)
+        for _ in range(n):
+            hip.qk_forward(q, k, *a, None)
+            hip.av_forward(attn, v, *a)
+            hip.qk_backward(q, k, attn, *a, None)
+            hip.av_backward(attn, v, do, *a)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x split qk/av forward and backward done", flush=True)
+        return
+    if workload == "cfg5":
+        Bc, L, H, Dc = 8, 2048, 12, 12
+        qa, ka, va = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
+        rpb = _gen((H, 13), torch.float32, 17, std=0.02)
+        logits = hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
+        attn = torch.softmax(logits, -1)
+        for _ in range(n):
+            hip.rpb_qk_forward(qa, ka, rpb, 7, 1, 0.288)
+            hip.rpb_av_forward(attn, va, 7, 1)
+            hip.rpb_qk_backward(qa, ka, attn, 7, 1, 0.288)
+            hip.rpb_av_backward(attn, va, va, 7, 1)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x allin1 K=7 d=1 forward and backward done", flush=True)
+        return
+    if workload == "cfg4":
+        q, k, v, ak, av, lens = _cfg4_inputs()
+        se = lens.reshape(-1, 1).to("cuda:0")
+        a = ((63,), (1,), (2,), (False,), None)
+        kw = dict(extra_k=ak, extra_v=av, sample_extent=se, varlen_clamped=True)
+        out, lse = hip.fused_forward(q, k, v, *a, **kw)
+        doc = _gen(out.shape, torch.float16, 6)
+        for _ in range(n):
+            hip.fused_forward(q, k, v, *a, **kw)
+            hip.fused_backward(q, k, v, out, lse, doc, None, *a, **kw)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x config-4 forward and backward (with extras) done",
+              flush=True)
+        return
+    if workload == "merge":
+        shape = (1, 16, 32, 32, 8, 64)
+        outs = [_gen(shape, torch.bfloat16, s) for s in range(2)]
+        lses = [_gen(shape[:-1], torch.float32, 20 + s) for s in range(2)]
+        dout, dlse = _gen(shape, torch.bfloat16, 40), _gen(shape[:-1], torch.float32, 41)
+        for _ in range(n):
+            hip.merge_forward(outs, lses)
+            hip.merge_backward(outs, lses, dout, dlse, [True] * 2, [True] * 2)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x merge forward and backward (2 parts, config-3 size) done",
+              flush=True)
+        return
+    if workload == "cfg3":
+        shape = (1, 16, 32, 32, 8, 64)
+        q, k, v, do = (_gen(shape, torch.bfloat16, s) for s in range(4))
+        a = ((3, 7, 7), (1, 1, 1), (1, 1, 1), (True, False, False), None)
+    else:
+        q, k, v, do = make_inputs(torch.device("cuda:0"))
+        a = ((K, K), (1, 1), (1, 1), (False, False), None)
+    out, lse = hip.fused_forward(q, k, v, *a)
+    # calibration for the HBM byte counters: a plain device copy of a known
+    # size (COPY_BYTES read + COPY_BYTES written), far larger than the caches
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=q.device).uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        dst.copy_(src)
+        hip.fused_forward(q, k, v, *a)
+        hip.fused_backward(q, k, v, out, lse, do, None, *a)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / args.steps
-
-
-WORKLOADS = {"split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4, "cfg5": wl_cfg5,
-             "merge": wl_merge}
-
-
-def run_cpu_baseline():
-    """Oracle fwd+bwd in bf16 on a bounded sample: one of the B=4 images."""
-    from oracle import na as O
-
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(0)
-    shape = (1, HH, WW, HEADS, D)
-    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
-    for t in (q, k, v):
-        t.requires_grad_(True)
-
-    def once():
-        out = O.na_forward(q, k, v, K, 1, 1, False, None, compute_dtype=torch.bfloat16)
-        torch.autograd.grad(out, (q, k, v), do)
-
-    once()  # warmup
-    times = []
-    deadline = time.perf_counter() + 12.0
-    while len(times) < 3 or (len(times) < 40 and time.perf_counter() < deadline):
-        t0 = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    per_sample_s = times[len(times) // 2]
-    return per_sample_s * B, threads, len(times)  # scaled to the full B=4 step
+    print(f"profile-calls: {n} copies of {COPY_BYTES} B, {n} forward + {n} backward calls done "
+          f"({workload})", flush=True)
 
 
 def main(argv=None):
@@ -572,8 +879,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-calls", type=int, default=0, metavar="N",
                     help="only run N calls of each library entry point of --workload "
-                         "(cfg2: fused forward/backward at dilation 1; split; cfg5) for "
-                         "rocprofv3 passes, then exit")
+                         "(cfg2 / cfg3: fused forward and backward with a calibration copy; "
+                         "split; cfg4; cfg5; merge) for rocprofv3 passes, then exit")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
                     help="cfg2 (default) is the driver's bench line; the others measure the "
                          "remaining BASELINE.json configurations")
@@ -586,67 +893,16 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    from natten_amd._core import _lib
 
+    _lib.load()
     if args.profile_calls > 0:
         profile_calls(args.profile_calls, args.workload)
         return 0
     if args.workload != "cfg2":
         print(json.dumps(WORKLOADS[args.workload](args)), flush=True)
         return 0
-    res = run_gpu(args)
-    fwd_f, bwd_f, fwd_b, bwd_b = algorithmic(K * K)
-    r1 = res[1]
-    step_ms = r1["graph_ms"] if r1["graph_ms"] is not None and r1["graph_ok"] else r1["eager_ms"]
-    total_flops = fwd_f + bwd_f
-    value = total_flops / (step_ms * 1e-3) / 1e12
-
-    # dominant call: the one with the larger event-timed duration
-    if r1["bwd_ms"] >= r1["fwd_ms"]:
-        dom, dom_ms, dom_bytes, dom_flops = "na_bwd", r1["bwd_ms"], bwd_b, bwd_f
-    else:
-        dom, dom_ms, dom_bytes, dom_flops = "na_fwd", r1["fwd_ms"], fwd_b, fwd_f
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                "traffic": measured_traffic(dom), "algorithmic_bytes": dom_bytes,
-                "call": dom, "call_ms": round(dom_ms, 5),
-                "mfma_frac": round(dom_flops / (dom_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 6)}
-
-    cpu = None
-    if not args.no_cpu:
-        cpu_s, threads, runs = run_cpu_baseline()
-        cpu = {"value": round(total_flops / cpu_s / 1e12, 6), "unit": "TFLOP/s",
-               "cores": threads, "kind": "port",
-               "sample": f"oracle (pure-backend restatement) fwd+bwd in bf16 on 1 of the 4 "
-                         f"images, median of {runs} runs (~12 s), scaled x4 to the full step",
-               "ms_per_step": round(cpu_s * 1e3, 2)}
-
-    line = {
-        "metric": "na2d 56x56 k7 bf16 fwd+bwd ms & TFLOP/s; % MFMA/HBM roofline, 1 MI355X",
-        "value": round(value, 4),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic N(0,1), seed 0",
-        "config": {"workload": "na2d fused fwd+bwd, B=4 56x56 heads=4 head_dim=32 k=7 "
-                               "dilation=1 non-causal",
-                   "global_batch": B, "spatial": [HH, WW], "heads": HEADS, "head_dim": D,
-                   "kernel_size": K, "dilation": 1, "parallelism": "none (1 GPU)"},
-        "timing": {"graph_ms": r1["graph_ms"], "graph_replays_match_eager": r1["graph_ok"],
-                   "eager_ms": round(r1["eager_ms"], 5), "fwd_call_ms": round(r1["fwd_ms"], 5),
-                   "bwd_call_ms": round(r1["bwd_ms"], 5)},
-        "dilation4": {k2: (round(v2, 5) if isinstance(v2, float) else v2)
-                      for k2, v2 in res[4].items()},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(main_line(args)), flush=True)
     return 0
 
 

@@ -6,6 +6,7 @@ deterministic HIP backward with the saved forward output and LSE.
 """
 
 from .fused import (
+    device_extents,
     FusedSpec,
     na1d_varlen_with_grad,
     na1d_with_grad,
@@ -25,6 +26,7 @@ from .split import (
 )
 
 __all__ = [
+    "device_extents",
     "FusedSpec",
     "na_fused_with_grad",
     "na1d_with_grad",

@@ -82,11 +82,36 @@ def na3d_with_grad(q, k, v, kernel_size, stride, dilation, is_causal, scale):
     return _plain(q, k, v, kernel_size, stride, dilation, is_causal, scale)
 
 
+# Device copies of host-side per-sample extents, by content: a training
+# loop passes the same few length vectors again and again, and a cached copy
+# needs no host-to-device transfer (which would wait for the stream), so the
+# call stays asynchronous and can be captured in a HIP graph.  Entries are
+# never evicted (a captured graph may hold their addresses); past
+# _EXTENTS_MAX distinct vectors, further ones are copied per call.
+_extents_cache: dict = {}
+_EXTENTS_MAX = 1024
+
+
+def device_extents(sizes: torch.Tensor, batch: int, rank: int, device) -> torch.Tensor:
+    """Per-sample extents as a contiguous int32 ``[batch, rank]`` tensor on
+    ``device``; host tensors go through the content-keyed cache."""
+    if sizes.device.type != "cpu":
+        return sizes.to(device=device, dtype=torch.int32).reshape(batch, rank).contiguous()
+    key = (str(device), batch, rank, tuple(int(x) for x in sizes.reshape(-1).tolist()))
+    hit = _extents_cache.get(key)
+    if hit is not None:
+        return hit
+    t = sizes.to(torch.int32).reshape(batch, rank).contiguous().to(device)
+    if len(_extents_cache) < _EXTENTS_MAX:
+        _extents_cache[key] = t
+    return t
+
+
 def _varlen(q, k, v, sizes, kernel_size, dilation, scale):
     rank = q.dim() - 3
     host = sizes.detach().to("cpu", torch.int64).reshape(q.shape[0], rank)
     clamped = bool((host >= torch.tensor([d * kk for d, kk in zip(dilation, kernel_size)])).all())
-    se = sizes.to(device=q.device, dtype=torch.int32).reshape(q.shape[0], rank).contiguous()
+    se = device_extents(sizes, q.shape[0], rank, q.device)
     spec = FusedSpec(tuple(kernel_size), (1,) * rank, tuple(dilation), (False,) * rank, scale,
                      varlen_clamped=clamped)
     return na_fused_with_grad(q, k, v, spec, sample_extent=se)[0]

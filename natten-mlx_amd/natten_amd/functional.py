@@ -27,6 +27,7 @@ import torch
 
 from .autograd import (
     FusedSpec,
+    device_extents,
     na1d_av_with_grad,
     na1d_qk_with_grad,
     na2d_av_with_grad,
@@ -352,7 +353,7 @@ def na1d_varlen_gqa(query, key, value, seq_lens, kernel_size, dilation=1, scale=
     if min_len < dil[0] * ks[0]:
         raise ValueError(f"All seq_lens must be >= dilation * kernel_size ({dil[0] * ks[0]}).")
     scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
-    se = seq_lens.to(device=query.device, dtype=torch.int32).reshape(B, 1).contiguous()
+    se = device_extents(seq_lens, B, 1, query.device)
     spec = FusedSpec(tuple(ks), (1,), tuple(dil), (False,), scale_value, varlen_clamped=True)
     out, lse = na_fused_with_grad(query, key.to(query.dtype), value.to(query.dtype), spec,
                                   add_k, add_v, sample_extent=se)

@@ -47,11 +47,13 @@ def _tup(x, rank):
     return (int(x),) * rank
 
 
-def _one_sample(q, k, v, ek, ev, dout, dlse, ks, st, dil, caus, scale, chunk, need_grad):
+def _one_sample(q, k, v, ek, ev, dout, dlse, ks, st, dil, caus, scale, chunk, need_grad,
+                f64=torch.float64, max_rows=None):
     """One sample (leading batch axis of size 1 stripped): q ``[*S, H, D]``,
     k/v ``[*S, Hkv, D]``, ek/ev ``[N, Hkv, D]`` or None, dout ``[*O, H, D]``,
-    dlse ``[*O, H]`` or None.  Returns (out, lse, dq, dk, dv, dek, dev)."""
-    f64 = torch.float64
+    dlse ``[*O, H]`` or None.  Returns (out, lse, dq, dk, dv, dek, dev).
+    ``f64``: the compute dtype; ``max_rows``: stop after that many output
+    rows (a bounded sample, for timing only)."""
     spatial = tuple(q.shape[:-2])
     H, D = q.shape[-2], q.shape[-1]
     Hkv = k.shape[-2]
@@ -71,11 +73,12 @@ def _one_sample(q, k, v, ek, ev, dout, dlse, ks, st, dil, caus, scale, chunk, ne
         evf = ev.to(f64).detach().requires_grad_(need_grad)
     do = dout.to(f64).reshape(n_out, Hkv, rep, D) if need_grad else None
     dl = (dlse.to(f64).reshape(n_out, Hkv, rep) if (need_grad and dlse is not None) else None)
-    out = torch.empty((n_out, Hkv, rep, D), dtype=f64)
-    lse = torch.empty((n_out, Hkv, rep), dtype=f64)
+    out = torch.zeros((n_out, Hkv, rep, D), dtype=f64)
+    lse = torch.zeros((n_out, Hkv, rep), dtype=f64)
     dq_sel = torch.zeros((n_out, Hkv, rep, D), dtype=f64) if need_grad else None
-    for r0 in range(0, n_out, chunk):
-        r1 = min(n_out, r0 + chunk)
+    n_run = n_out if max_rows is None else min(n_out, max_rows)
+    for r0 in range(0, n_run, chunk):
+        r1 = min(n_run, r0 + chunk)
         qc = qsel[r0:r1].detach().requires_grad_(need_grad)
         idx = lin[r0:r1]
         kn = kf[idx.reshape(-1)].reshape(r1 - r0, kp, Hkv, D)
@@ -114,7 +117,8 @@ def _one_sample(q, k, v, ek, ev, dout, dlse, ks, st, dil, caus, scale, chunk, ne
 
 
 def fused(q, k, v, kernel_size, stride=1, dilation=1, is_causal=False, scale=None,
-          dout=None, dlse=None, extra_k=None, extra_v=None, sizes=None, chunk=256):
+          dout=None, dlse=None, extra_k=None, extra_v=None, sizes=None, chunk=256,
+          compute_dtype=torch.float64, max_rows=None):
     """Fused neighborhood attention over ``[B, *spatial, H, D]`` tensors (k, v
     with ``H_kv`` heads; extra_k / extra_v ``[B, N, H_kv, D]``), exactly in
     float64.  ``sizes``: per-sample extents ``[B]`` / ``[B, rank]`` (varlen,
@@ -124,6 +128,11 @@ def fused(q, k, v, kernel_size, stride=1, dilation=1, is_causal=False, scale=Non
     and, when ``dout`` is given, ``dq``, ``dk``, ``dv`` (and ``dek``,
     ``dev`` with extra tokens): gradients of
     ``sum(out * dout) + sum(lse * dlse)``.
+
+    ``compute_dtype`` other than float64 and ``max_rows`` (compute only the
+    first rows of each sample) exist for the benchmark's CPU baseline, which
+    times the reference's ``pure`` algorithm in the input dtype on a bounded
+    sample; parity checks use the defaults.
     """
     rank = q.dim() - 3
     ks, st, dil, caus = (_tup(kernel_size, rank), _tup(stride, rank),
@@ -131,7 +140,7 @@ def fused(q, k, v, kernel_size, stride=1, dilation=1, is_causal=False, scale=Non
     B, H, D = q.shape[0], q.shape[-2], q.shape[-1]
     sc = D ** -0.5 if scale is None else float(scale)
     need_grad = dout is not None
-    f64 = torch.float64
+    f64 = compute_dtype
     out_sp = tuple((s + t - 1) // t for s, t in zip(q.shape[1:-2], st))
     res = {"out": torch.zeros((B, *out_sp, H, D), dtype=f64),
            "lse": torch.zeros((B, *out_sp, H), dtype=f64)}
@@ -159,7 +168,7 @@ def fused(q, k, v, kernel_size, stride=1, dilation=1, is_causal=False, scale=Non
         dob = dout[b][osl] if need_grad else None
         dlb = dlse[b][osl] if (need_grad and dlse is not None) else None
         o, l, dq, dk, dv, dek, dev = _one_sample(qb, kb, vb, ekb, evb, dob, dlb, ks, st, dil,
-                                                 caus, sc, chunk, need_grad)
+                                                 caus, sc, chunk, need_grad, f64, max_rows)
         res["out"][b][osl] = o
         res["lse"][b][osl] = l
         if need_grad:

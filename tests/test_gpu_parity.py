@@ -338,3 +338,32 @@ def test_fused_backward_hook_reference_signature():
     ref = O.grads(lambda x, y, z: O.na_forward(x, y, z, (7, 5), 1, (2, 1)), (q, k, v), (go,))
     for g, r, n in zip(g_none, ref, "qkv"):
         assert_close(g, r, dt, f"hook d{n}")
+
+
+def test_varlen_host_lengths_graph_capture():
+    """Host-side seq_lens give the same result as device ones, with no
+    host-device synchronisation, so the call can be captured in a HIP graph:
+    replays (with other work between them) reproduce the eager output."""
+    import natten_amd
+
+    _say("[case] varlen host lengths + graph")
+    dt = torch.float16
+    q, k, v = _inputs(3, (96,), 4, 2, 64, dt, 71)
+    qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+    lens = torch.tensor([96, 40, 63], dtype=torch.int32)
+    ref = natten_amd.na1d_varlen_gqa(qd, kd, vd, lens.to(DEV), 7, 2)
+    got = natten_amd.na1d_varlen_gqa(qd, kd, vd, lens, 7, 2)
+    assert torch.equal(got, ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        natten_amd.na1d_varlen_gqa(qd, kd, vd, lens, 7, 2)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = natten_amd.na1d_varlen_gqa(qd, kd, vd, lens, 7, 2)
+    for i in range(3):
+        torch.zeros(1 << 20, device=DEV).add_(i)  # unrelated eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static, ref), f"replay {i}"
