@@ -13,6 +13,8 @@
 //            the queries q whose windows hold the key of
 //            a[q, slot(q, key)] * x_q (qk backward's dk: a = dlogits,
 //            x = q; av backward's dv: a = attn, x = dO)
+//   k_lqh, k_lah : k_lqk and k_lav with every query head of a tile of 16
+//            query positions in one workgroup (used where the heads fit)
 //
 // The tiling is the fused kernels' (na_lean.h): a wave owns 16 queries (or
 // keys) of one dilation phase, W waves stacked along one axis form a
@@ -31,6 +33,18 @@
 
 namespace na {
 namespace {
+
+// An unsigned word of BYTES bytes (vector copies of 2-byte elements).
+template <int BYTES>
+struct RawWord;
+template <>
+struct RawWord<16> { typedef uint4 type; };
+template <>
+struct RawWord<8> { typedef uint2 type; };
+template <>
+struct RawWord<4> { typedef uint32_t type; };
+template <>
+struct RawWord<2> { typedef uint16_t type; };
 
 // Stage a workgroup's box of rows of one tensor into LDS: box point (e0, e1,
 // e2) at layout row ((e0 * Em1 + e1) << lgP2) + e2 (rank 1: e2), element
@@ -252,6 +266,264 @@ __global__ void __launch_bounds__(512)
         if ((vb >> (p0 + j)) & 1) oe[row * kp + s] = vals[j];
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_lqh.  k_lqk with every query head of a tile of 16 query positions in one
+// workgroup (wave w computes head w): the compact rows of one position are
+// contiguous over the heads in memory ([.., position, H, kprod]), so the
+// workgroup's output is 16 runs of H * kprod elements that go out as
+// aligned vector stores.  The key rows of each chunk are read straight from
+// memory as the MFMA's A operand (a wave's 16 queries have their own key
+// sub-box, so nothing is shared through LDS and no barrier precedes the
+// products); scores go to the LDS row buffer branch-free (out-of-window
+// lanes write a per-lane spare slot past the rows).
+template <typename T, int D, int R, bool CPR1, int VW>
+__global__ void __launch_bounds__(1024)
+    k_lqh(LProb P, const T *__restrict__ x, const T *__restrict__ y,
+          T *__restrict__ out, float scale, float fill, int prefill,
+          FastDiv fups) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;
+  constexpr int NB = 256 / D;  // chunks whose operands are loaded together
+  extern __shared__ __align__(16) char smem[];
+
+  // tile: (sample, spatial tile of 16 queries); wave w: query head w
+  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const uint32_t bq = fdiv((uint32_t)tile, P.fGrid);
+  const uint32_t sp = (uint32_t)tile - bq * P.fGrid.d;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  LTile t;
+  t.b = (int)bq;
+  t.head = w;
+  t.hk = (int)fdiv((uint32_t)w, P.fRep);
+  const bool tile_any = tile_origin<R>(P, sp, t) & (t.b < P.B);
+  if (!tile_any) return;  // uniform over the workgroup
+  tile_box<R, false>(P, t, t.hk, P.Hkv);
+  const WSub ws = wave_sub<R>(P, t, 0);
+  bool qv;
+  int wl[3], ww[3], qi[3];
+  const int qrow = lane_row<R, false>(P, t, ws, n, t.head, P.H, qv, wl, ww, qi);
+  const int sq = (R == 3 ? (wl[0] + ww[0] - P.ax[0].K) * P.kst0 : 0) +
+                 (R >= 2 ? (wl[1] + ww[1] - P.ax[1].K) * P.kst1 : 0) +
+                 (wl[2] + (qv ? ww[2] : P.ax[2].K) - P.ax[2].K);
+  v8 qf[NT];
+#pragma unroll
+  for (int st = 0; st < NT; ++st) qf[st] = ld8(x, qrow * D + 32 * st + 8 * gq);
+
+  const int kp = P.kp;
+  const int rowlen = P.H * kp;  // one position: every head's compact row
+  E *ob = reinterpret_cast<E *>(smem);
+  E *mine = ob + n * rowlen + w * kp;
+  const int spare = 16 * rowlen + lane - (n * rowlen + w * kp);  // from mine
+  if (prefill) {
+    for (int i = lane; i < 16 * kp; i += 64) {
+      const int r = i / kp;  // small: division by the slot count
+      ob[r * rowlen + w * kp + (i - r * kp)] = (E)fill;
+    }
+    wave_lds_sync();
+  }
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  const int nch = ws.any ? (R == 3 ? ws.we[0] - ws.ws[0] : 1) * rows1 * ws.cpr : 0;
+  Cursor cc{R == 3 ? ws.ws[0] : 0, ws.ws[1], 0};
+  // element offset of key column c of box row (e0, e1), clamped onto the box
+  auto key_off = [&](int e0, int e1, int c) {
+    int off = t.kbase + 8 * gq;
+    if (R == 3) off += __umul24((unsigned)min(e0, t.E[0] - 1), (unsigned)t.SK[0]);
+    if (R >= 2) off += __umul24((unsigned)min(e1, t.E[1] - 1), (unsigned)t.SK[1]);
+    return off + __umul24((unsigned)min(c, t.E[2] - 1), (unsigned)t.SK[2]);
+  };
+  for (int c0 = 0; c0 < nch; c0 += NB) {
+    ChunkPos cp[NB];
+    v8 ka[NB][NT];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, 0, 0, wl, ww);
+      const int off = key_off(cp[j].e0, cp[j].e1, cp[j].col + n);
+#pragma unroll
+      for (int st = 0; st < NT; ++st) ka[j][st] = ld8(y, off + 32 * st);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      f32x4 sv = zero4();
+#pragma unroll
+      for (int st = 0; st < NT; ++st) sv = M::mma(ka[j][st], qf[st], sv);
+      const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
+        mine[ok ? cp[j].e01 + xc + r - sq : spare] = (E)(sv[r] * scale);
+      }
+    }
+  }
+  __syncthreads();  // every head's rows of the tile are in LDS
+
+  // write-out: position p's run of rowlen elements goes to row
+  // (token(p) * H) * kp, in units of VW elements (aligned: the host picks VW
+  // so that rowlen is a multiple of it)
+  typedef typename RawWord<VW * 2>::type VU;
+  const int ups = rowlen / VW;  // units per position
+  const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+  for (int u = tid; u < 16 * ups; u += nthr) {
+    const int p = (int)fdiv((uint32_t)u, fups);
+    const int iu = u - p * ups;
+    int uu[3];
+    uu[2] = p & (P.ax[2].T - 1);
+    uu[1] = (p >> lg2) & (P.ax[1].T - 1);
+    uu[0] = p >> (lg2 + lg1);
+    bool pv = true;
+    int tok = t.b * P.Ltot;
+#pragma unroll
+    for (int a = 3 - R; a < 3; ++a) {
+      const LAx &xa = P.ax[a];
+      pv = pv && uu[a] < t.nv[a];
+      tok += (t.r[a] + xa.d * (t.i0[a] + uu[a])) * xa.tok;
+    }
+    if (pv)
+      *reinterpret_cast<VU *>(out + (size_t)tok * rowlen + (size_t)iu * VW) =
+          *reinterpret_cast<const VU *>(ob + p * rowlen + iu * VW);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_lah.  k_lav with every query head of a tile of 16 query positions in one
+// workgroup (wave w computes head w): the tile's compact rows, contiguous
+// over the heads per position, come in as aligned vector loads; each wave
+// stages the Y rows of its own chunks (a group at a time) in a private LDS
+// area for the transposing read, so only the compact rows pass a
+// workgroup barrier.
+template <typename T, int D, int R, bool CPR1, int VW>
+__global__ void __launch_bounds__(1024)
+    k_lah(LProb P, const T *__restrict__ a, const T *__restrict__ y,
+          T *__restrict__ out, float scale, FastDiv fups) {
+  typedef L16<T> M;
+  typedef typename M::v8 v8;
+  typedef typename M::v4 v4;
+  typedef typename M::e E;
+  constexpr int NT = D / 32;
+  constexpr int NB = D == 128 ? 2 : 4;  // chunks staged together (even)
+  constexpr int NDB = D / 16;
+  constexpr int RS = lds_y(D);
+  extern __shared__ __align__(16) char smem[];
+
+  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const uint32_t bq = fdiv((uint32_t)tile, P.fGrid);
+  const uint32_t sp = (uint32_t)tile - bq * P.fGrid.d;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 15, gq = lane >> 4;
+  LTile t;
+  t.b = (int)bq;
+  t.head = w;
+  t.hk = (int)fdiv((uint32_t)w, P.fRep);
+  const bool tile_any = tile_origin<R>(P, sp, t) & (t.b < P.B);
+  if (!tile_any) return;  // uniform over the workgroup
+  tile_box<R, false>(P, t, t.hk, P.Hkv);
+  const WSub ws = wave_sub<R>(P, t, 0);
+  bool qv;
+  int wl[3], ww[3], qi[3];
+  const int qrow = lane_row<R, false>(P, t, ws, n, t.head, P.H, qv, wl, ww, qi);
+  const int sq = (R == 3 ? (wl[0] + ww[0] - P.ax[0].K) * P.kst0 : 0) +
+                 (R >= 2 ? (wl[1] + ww[1] - P.ax[1].K) * P.kst1 : 0) +
+                 (wl[2] + (qv ? ww[2] : P.ax[2].K) - P.ax[2].K);
+
+  const int kp = P.kp;
+  const int rowlen = P.H * kp;
+  E *ab = reinterpret_cast<E *>(smem);  // [16 positions][H][kp]
+  E *ys = ab + align16(16 * rowlen);     // per wave: NB chunks of 16 rows
+  E *yw = ys + w * NB * 16 * RS;
+  // the tile's compact rows, position by position (runs of rowlen)
+  typedef typename RawWord<VW * 2>::type VU;
+  const int ups = rowlen / VW;
+  const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
+  for (int u = tid; u < 16 * ups; u += nthr) {
+    const int p = (int)fdiv((uint32_t)u, fups);
+    const int iu = u - p * ups;
+    int uu[3];
+    uu[2] = p & (P.ax[2].T - 1);
+    uu[1] = (p >> lg2) & (P.ax[1].T - 1);
+    uu[0] = p >> (lg2 + lg1);
+    bool pv = true;
+    int tok = t.b * P.Ltot;
+#pragma unroll
+    for (int ax = 3 - R; ax < 3; ++ax) {
+      const LAx &xa = P.ax[ax];
+      pv = pv && uu[ax] < t.nv[ax];
+      tok += (t.r[ax] + xa.d * (t.i0[ax] + min(uu[ax], max(t.nv[ax] - 1, 0)))) * xa.tok;
+    }
+    VU val = *reinterpret_cast<const VU *>(a + (size_t)tok * rowlen + (size_t)iu * VW);
+    if (!pv) val = VU{};
+    *reinterpret_cast<VU *>(ab + p * rowlen + iu * VW) = val;
+  }
+  __syncthreads();
+  const E *mine = ab + n * rowlen + w * kp;
+
+  f32x4 o[NDB];
+#pragma unroll
+  for (int j = 0; j < NDB; ++j) o[j] = zero4();
+  const int tr_off = (4 * gq + (n >> 2)) * RS + 4 * (n & 3);
+  const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  const int nch = ws.any ? (R == 3 ? ws.we[0] - ws.ws[0] : 1) * rows1 * ws.cpr : 0;
+  Cursor cc{R == 3 ? ws.ws[0] : 0, ws.ws[1], 0};
+  auto row_off = [&](int e0, int e1, int c) {
+    int off = t.kbase + 8 * gq;
+    if (R == 3) off += __umul24((unsigned)min(e0, t.E[0] - 1), (unsigned)t.SK[0]);
+    if (R >= 2) off += __umul24((unsigned)min(e1, t.E[1] - 1), (unsigned)t.SK[1]);
+    return off + __umul24((unsigned)min(c, t.E[2] - 1), (unsigned)t.SK[2]);
+  };
+  for (int c0 = 0; c0 < nch; c0 += NB) {
+    ChunkPos cp[NB];
+    v8 yr[NB][NT];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, 0, 0, wl, ww);
+      const int off = row_off(cp[j].e0, cp[j].e1, cp[j].col + n);
+#pragma unroll
+      for (int st = 0; st < NT; ++st) yr[j][st] = ld8(y, off + 32 * st);
+    }
+    // B operand: query n's weights of keys 4 (l / 16) + r of each chunk
+    v8 bp[NB / 2];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
+        bp[j >> 1][4 * (j & 1) + r] = ok ? mine[cp[j].e01 + xc + r - sq] : (E)0.f;
+      }
+    }
+    wave_lds_sync();  // the previous group's transposing reads are done
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+        *reinterpret_cast<v8 *>(yw + (16 * j + n) * RS + 32 * st + 8 * gq) = yr[j][st];
+    wave_lds_sync();
+#pragma unroll
+    for (int jj = 0; jj < NB / 2; ++jj) {
+      const E *ca = yw + 32 * jj * RS + tr_off;
+      const E *cb = ca + 16 * RS;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const v4 lo4 = M::tr(ca + 16 * db);
+        const v4 hi4 = M::tr(cb + 16 * db);
+        const v8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[db] = M::mma(av, bp[jj], o[db]);
+      }
+    }
+  }
+  if (!qv) return;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    v4 wv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r] = (E)(o[db][r] * scale);
+    *reinterpret_cast<v4 *>(out + qrow * D + 16 * db + 4 * gq) = wv;
   }
 }
 
@@ -539,15 +811,77 @@ bool lsplit_eligible(const Prob &P, int dtype) {
     else by_d(f16_t());                                                         \
   } while (0)
 
+// k_lqh's launch: every query head of a 16-query tile in one workgroup
+// (at most 16 heads and 64 KB of rows), rows written in units of VW
+// elements; false when it does not apply.
+struct LqhPlan {
+  int vw;
+  size_t lds;
+};
+bool lqh_plan(const Prob &P, LqhPlan *pl) {
+  if (P.H > 16) return false;
+  const int rowlen = P.H * P.kprod;
+  pl->lds = (size_t)16 * rowlen * 2 + 64 * 2;
+  if (pl->lds > 65536) return false;
+  pl->vw = rowlen % 8 == 0 ? 8 : rowlen % 4 == 0 ? 4 : rowlen % 2 == 0 ? 2 : 1;
+  return true;
+}
+
 void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
                void *out, float scale, float fill, hipStream_t st) {
   const LChoice C = lean_choice(P, kLQK);
+  int prefill = 0;
+  for (int a = 0; a < 3; ++a) prefill |= P.ax[a].causal;
+  LqhPlan pl;
+  if (lqh_plan(P, &pl)) {
+    LChoice C1 = C;  // one wave tile per workgroup (waves are heads)
+    C1.W = 1;
+    LProb L = make_lprob(P, C1);
+    L.n_tiles = P.B * (int)L.fGrid.d;
+    L.n_launch = (L.n_tiles + 7) & ~7;
+    if (L.n_tiles == 0) return;
+    const FastDiv fups = make_fastdiv((uint32_t)(P.H * P.kprod / pl.vw));
+    const dim3 grid(L.n_launch), block(64 * P.H);
+    const size_t lds = pl.lds;
+    auto go = [&](auto tt, auto dd, auto rr, auto cc, auto vv) {
+      typedef decltype(tt) TT;
+      constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;
+      constexpr bool CC = decltype(cc)::value;
+      constexpr int VV = decltype(vv)::value;
+      hipLaunchKernelGGL((k_lqh<TT, DD, RR, CC, VV>), grid, block, lds, st, L,
+                         (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill,
+                         fups);
+    };
+    auto by_v = [&](auto tt, auto dd, auto rr, auto cc) {
+      if (pl.vw == 8) go(tt, dd, rr, cc, std::integral_constant<int, 8>());
+      else if (pl.vw == 4) go(tt, dd, rr, cc, std::integral_constant<int, 4>());
+      else if (pl.vw == 2) go(tt, dd, rr, cc, std::integral_constant<int, 2>());
+      else go(tt, dd, rr, cc, std::integral_constant<int, 1>());
+    };
+    auto by_r = [&](auto tt, auto dd) {
+      if (P.rank == 1)
+        by_v(tt, dd, std::integral_constant<int, 1>(), std::false_type());
+      else if (P.rank == 2) {
+        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 2>(), std::true_type());
+        else by_v(tt, dd, std::integral_constant<int, 2>(), std::false_type());
+      } else {
+        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
+        else by_v(tt, dd, std::integral_constant<int, 3>(), std::false_type());
+      }
+    };
+    auto by_d = [&](auto tt) {
+      if (P.D == 32) by_r(tt, std::integral_constant<int, 32>());
+      else if (P.D == 64) by_r(tt, std::integral_constant<int, 64>());
+      else by_r(tt, std::integral_constant<int, 128>());
+    };
+    if (dtype == NA_BF16) by_d(bf16_t());
+    else by_d(f16_t());
+    return;
+  }
   const LProb L = make_lprob(P, C);
   if (L.n_tiles == 0) return;
   const size_t lds = lean_lds_bytes(P, kLQK, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
-  int prefill = 0;
-  for (int a = 0; a < 3; ++a) prefill |= P.ax[a].causal;
 #define LS_ARGS_QK(TT) (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill
   LS_DISPATCH(k_lqk, LS_ARGS_QK(TT));
 #undef LS_ARGS_QK
@@ -556,6 +890,54 @@ void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
 void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
                void *out, float scale, hipStream_t st) {
   const LChoice C = lean_choice(P, kLQK);
+  LqhPlan pl;
+  // k_lah's LDS: the tile's compact rows and, per wave, NB chunks of 16 rows
+  const int nb = P.D == 128 ? 2 : 4;
+  const size_t lah_lds = (size_t)align16(16 * P.H * P.kprod) * 2 +
+                         (size_t)P.H * nb * 16 * lds_y(P.D) * 2;
+  if (lqh_plan(P, &pl) && lah_lds <= 65536) {
+    LChoice C1 = C;  // one wave tile per workgroup (waves are heads)
+    C1.W = 1;
+    LProb L = make_lprob(P, C1);
+    L.n_tiles = P.B * (int)L.fGrid.d;
+    L.n_launch = (L.n_tiles + 7) & ~7;
+    if (L.n_tiles == 0) return;
+    const FastDiv fups = make_fastdiv((uint32_t)(P.H * P.kprod / pl.vw));
+    const dim3 grid(L.n_launch), block(64 * P.H);
+    auto go = [&](auto tt, auto dd, auto rr, auto cc, auto vv) {
+      typedef decltype(tt) TT;
+      constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;
+      constexpr bool CC = decltype(cc)::value;
+      constexpr int VV = decltype(vv)::value;
+      hipLaunchKernelGGL((k_lah<TT, DD, RR, CC, VV>), grid, block, lah_lds, st, L,
+                         (const TT *)a, (const TT *)y, (TT *)out, scale, fups);
+    };
+    auto by_v = [&](auto tt, auto dd, auto rr, auto cc) {
+      if (pl.vw == 8) go(tt, dd, rr, cc, std::integral_constant<int, 8>());
+      else if (pl.vw == 4) go(tt, dd, rr, cc, std::integral_constant<int, 4>());
+      else if (pl.vw == 2) go(tt, dd, rr, cc, std::integral_constant<int, 2>());
+      else go(tt, dd, rr, cc, std::integral_constant<int, 1>());
+    };
+    auto by_r = [&](auto tt, auto dd) {
+      if (P.rank == 1)
+        by_v(tt, dd, std::integral_constant<int, 1>(), std::false_type());
+      else if (P.rank == 2) {
+        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 2>(), std::true_type());
+        else by_v(tt, dd, std::integral_constant<int, 2>(), std::false_type());
+      } else {
+        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
+        else by_v(tt, dd, std::integral_constant<int, 3>(), std::false_type());
+      }
+    };
+    auto by_d = [&](auto tt) {
+      if (P.D == 32) by_r(tt, std::integral_constant<int, 32>());
+      else if (P.D == 64) by_r(tt, std::integral_constant<int, 64>());
+      else by_r(tt, std::integral_constant<int, 128>());
+    };
+    if (dtype == NA_BF16) by_d(bf16_t());
+    else by_d(f16_t());
+    return;
+  }
   const LProb L = make_lprob(P, C);
   if (L.n_tiles == 0) return;
   const size_t lds = lean_lds_bytes(P, kLQK, L.ebox, C.W);
