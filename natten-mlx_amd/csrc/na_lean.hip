@@ -360,27 +360,25 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
   constexpr int OCT = D / 8;
   constexpr int RSE = lds_row(D);
   const int nun = P.ebox * OCT;
+  const int o = tid % OCT;  // the lane's unit in each of its rows
   for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
     v8 qr[4], dr[4], orr[4];
     float lr[4], dl[4];
-    int kk[4], o[4];
+    int g[4], la[4];
+    unit_walk<R, OCT, RSE>(P, t, u0, tid, nthr, s0, g, la);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int u = min(u0 + j * nthr + tid, nun - 1);
-      kk[j] = u / OCT;
-      o[j] = u % OCT;
-      const int g = unit_offset<R>(P, t, kk[j], o[j], s0);
-      const int row = (g - 8 * o[j]) / D;
-      qr[j] = ld8(q, g);
-      dr[j] = ld8(dout, g);
-      orr[j] = ld8(out, g);
+      const int row = (g[j] - 8 * o) / D;
+      qr[j] = ld8(q, g[j]);
+      dr[j] = ld8(dout, g[j]);
+      orr[j] = ld8(out, g[j]);
       lr[j] = ldf(lse, row);
       dl[j] = dlse != nullptr ? ldf(dlse, row) : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<v8 *>(qs + __umul24(kk[j], RSE) + 8 * o[j]) = qr[j];
-      *reinterpret_cast<v8 *>(os + __umul24(kk[j], RSE) + 8 * o[j]) = dr[j];
+      *reinterpret_cast<v8 *>(qs + la[j]) = qr[j];
+      *reinterpret_cast<v8 *>(os + la[j]) = dr[j];
       float part = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -393,8 +391,8 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
       }
 #pragma unroll
       for (int m = 1; m < OCT; m <<= 1) part += __shfl_xor(part, m);
-      if (o[j] == 0)
-        *reinterpret_cast<float2 *>(qs + __umul24(kk[j], RSE) + D) =
+      if (o == 0)
+        *reinterpret_cast<float2 *>(qs + la[j] + D) =
             make_float2(lr[j] * kLog2e, dl[j] - part);
     }
   }

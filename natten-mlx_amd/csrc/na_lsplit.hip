@@ -61,14 +61,10 @@ __device__ __forceinline__ void stage_box1(const LProb &P, const LTile &t,
   const int nun = P.ebox * OCT;
   for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
     v8 xr[4];
-    int la[4];
+    int g[4], la[4];
+    unit_walk<R, OCT, RS>(P, t, u0, tid, nthr, s0, g, la);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int u = min(u0 + j * nthr + tid, nun - 1);
-      const int kk = u / OCT, o = u % OCT;
-      xr[j] = ld8(x, unit_offset<R>(P, t, kk, o, s0));
-      la[j] = __umul24(kk, RS) + 8 * o;
-    }
+    for (int j = 0; j < 4; ++j) xr[j] = ld8(x, g[j]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<v8 *>(xs + la[j]) = xr[j];
   }
