@@ -399,6 +399,23 @@ __device__ __forceinline__ f32x4 zero4() {
   return z;
 }
 
+// Sum over G (4, 8 or 16) consecutive lanes, complete in the group's first
+// lane, by DPP lane moves (no LDS traffic): swaps within quads (the
+// butterfly's first two steps), then the row shifts by 4 and 8 that bring
+// the upper half of the group to its first lane.
+template <int G>
+__device__ __forceinline__ float dpp_group_sum(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v),
+                                                      decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  x += dpp(x, std::integral_constant<int, 0xb1>());    // quad_perm [1,0,3,2]
+  x += dpp(x, std::integral_constant<int, 0x4e>());    // quad_perm [2,3,0,1]
+  if (G >= 8) x += dpp(x, std::integral_constant<int, 0x104>());   // row_shl:4
+  if (G >= 16) x += dpp(x, std::integral_constant<int, 0x108>());  // row_shl:8
+  return x;
+}
+
 // Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 that hold one
 // query's scores (two lane-swap butterflies, no LDS traffic).
 __device__ __forceinline__ float quad_max(float x) {

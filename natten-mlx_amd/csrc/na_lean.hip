@@ -389,8 +389,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
         b2[1] = orr[j][e + 1];
         part = L16<T>::dot2(a2, b2, part);
       }
-#pragma unroll
-      for (int m = 1; m < OCT; m <<= 1) part += __shfl_xor(part, m);
+      part = dpp_group_sum<OCT>(part);
       if (o == 0)
         *reinterpret_cast<float2 *>(qs + la[j] + D) =
             make_float2(lr[j] * kLog2e, dl[j] - part);
@@ -590,7 +589,14 @@ __global__ void __launch_bounds__(512)
         df[st] = ld8(dout, qoff + 32 * st + 8 * gq);
         const v8 of = ld8(out, qoff + 32 * st + 8 * gq);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dsum = fmaf((float)df[st][e], (float)of[e], dsum);
+        for (int e = 0; e < 8; e += 2) {
+          typename M::v2 a2, b2;
+          a2[0] = df[st][e];
+          a2[1] = df[st][e + 1];
+          b2[0] = of[e];
+          b2[1] = of[e + 1];
+          dsum = M::dot2(a2, b2, dsum);
+        }
       }
       const float lse2 = ldf(lse, qoff / D) * kLog2e;
       const float dl = dlse != nullptr ? ldf(dlse, qoff / D) : 0.f;
