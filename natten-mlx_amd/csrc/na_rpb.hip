@@ -266,7 +266,8 @@ template <typename TX, typename TY, int VEC, bool YS>
 __global__ void __launch_bounds__(512)
     k_rpb_dot(RpbProb A, const TX *__restrict__ x, const TY *__restrict__ y,
               const float *__restrict__ rpb, float *__restrict__ out,
-              int scale_x, float fill, int staged, int G, int lgG) {
+              int scale_x, float fill, int staged, int G, int lgG,
+              int bias_lds) {
   const Group g = make_group(lgG, A.n_rows);
   const RPos p = rpos(A, (uint32_t)g.id);
   float xv[kNT][VEC];
@@ -279,10 +280,21 @@ __global__ void __launch_bounds__(512)
   extern __shared__ __align__(16) float stage[];
   const int lrow = (int)(threadIdx.x >> lgG);
   float *dst = staged ? stage + lrow * A.KK : out + g.id * A.KK;
+  // bias_lds: the bias table [H, R0 (, R1)] is copied to LDS (after the
+  // slot rows and the staged window) with the window's loads, so the slot
+  // loop's bias reads do not each wait on a memory round trip
+  const float *bias = rpb;
+  if (bias_lds) {
+    float *bs = stage + bias_lds;
+    const int nb = A.H * A.R0 * A.R1;
+    for (int i = (int)threadIdx.x; i < nb; i += (int)blockDim.x) bs[i] = rpb[i];
+    bias = bs;
+    if (A.rank != 1 || !YS) __syncthreads();  // else stage_window's barrier
+  }
   if (A.rank == 1) {
     // one axis: the row of key position j is this row + (j - i) * step
     const int64_t step = A.heads_first ? 1 : A.H;
-    const float *rb = rpb != nullptr ? rpb + p.h * A.R0 : nullptr;
+    const float *rb = rpb != nullptr ? bias + p.h * A.R0 : nullptr;
     const TY *ybase = y;
     int64_t ylo = 0;
     if constexpr (YS) {
@@ -311,7 +323,7 @@ __global__ void __launch_bounds__(512)
         if (v0 && j1 >= 0 && j1 < w1.e) {
           const TY *yr = y + rrow(A, p.b, p.h, j0, j1) * A.D;
           s = group_sum(dot_row<TY, VEC>(xv, yr, g.lane, G, A.D), G);
-          if (rpb != nullptr) s += rpb[bias_index(A, p.h, w0.pb + k0, w1.pb + k1)];
+          if (rpb != nullptr) s += bias[bias_index(A, p.h, w0.pb + k0, w1.pb + k1)];
         }
         if (g.live && g.lane == 0) dst[n] = s;
       }
@@ -641,13 +653,14 @@ dim3 rgrid(const RpbProb &A, int lgG, int rb = 256) {
 
 // Threads per block of the forward gathers (k_rpb_dot / k_rpb_gather):
 // 512 when the window reach K0 * d0 is at least 7 (the halo then weighs
-// on a 256-row block: measured at D = 12, K in {3, 5, 7}, d in {1..8}),
-// 256 otherwise; NATTEN_AMD_RPB_BLOCK overrides it (tuning).
+// on a 256-row block: measured at D = 12, K in {3, 5, 7}, d in {1..8};
+// 384, which splits config 5's rows into exactly two blocks per CU, is
+// slower), 256 otherwise; NATTEN_AMD_RPB_BLOCK overrides it (tuning).
 int rpb_block(const RpbProb &A) {
   static const int forced = [] {
     const char *e = std::getenv("NATTEN_AMD_RPB_BLOCK");
     const int v = e != nullptr ? std::atoi(e) : 0;
-    return v == 64 || v == 128 || v == 256 || v == 512 ? v : 0;
+    return v == 64 || v == 128 || v == 256 || v == 384 || v == 512 ? v : 0;
   }();
   if (forced > 0) return forced;
   return A.rank == 1 && A.K0 * A.d0 >= 7 ? 512 : 256;
@@ -688,10 +701,15 @@ void launch_dot(const RpbProb &A, const void *x, const void *y,
   const size_t lds = stage_bytes(A, s.lgG, rb);
   const int staged = lds > 0;
   const size_t wb = window_bytes<TY>(A, s.lgG, lds, rb);
+  // the bias table in LDS after the slot rows and the window (float index)
+  const size_t nbias = rpb != nullptr ? (size_t)A.H * A.R0 * A.R1 : 0;
+  const size_t bb = nbias > 0 && nbias * 4 <= 16384 ? nbias * 4 : 0;
+  const int bias_lds = bb > 0 ? (int)((lds + wb + 15) / 16 * 4) : 0;
+  const size_t total = bb > 0 ? (size_t)bias_lds * 4 + bb : lds + wb;
 #define DOT_(VV, YS)                                                          \
   hipLaunchKernelGGL((k_rpb_dot<TX, TY, VV, YS>), rgrid(A, s.lgG, rb), dim3(rb), \
-                     lds + wb, st, A, (const TX *)x, (const TY *)y, rpb, out,  \
-                     scale_x, fill, staged, s.G, s.lgG)
+                     total, st, A, (const TX *)x, (const TY *)y, rpb, out,     \
+                     scale_x, fill, staged, s.G, s.lgG, bias_lds)
   if (s.vec == V) {
     if (wb > 0) DOT_(V, true); else DOT_(V, false);
   } else {
