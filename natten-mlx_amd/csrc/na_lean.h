@@ -348,25 +348,25 @@ __device__ __forceinline__ int unit_offset(const LProb &P, const LTile &t,
 }
 
 // Global element offsets g[j] and LDS element offsets la[j] (layout row
-// stride RS) of a lane's four staging units u0 + j nthr + tid, j < 4 (u0 a
-// multiple of 4 nthr, nthr of OCT): layout row kk_j = (u0 + tid) / OCT +
+// stride RS) of a lane's NU staging units u0 + j nthr + tid, j < NU (u0 a
+// multiple of NU nthr, nthr of OCT): layout row kk_j = (u0 + tid) / OCT +
 // j nthr / OCT, unit o = tid % OCT.  Rank 1, and rank 2 when a step of
 // nthr / OCT layout rows is a whole number of box rows, step the box row
 // (two adds, a min and a 24-bit product per unit); otherwise unit_offset
 // per unit.  Units past the layout take its last row (the lane's unit of
 // it): real rows, staged again with the same values, and every row's OCT
 // units are held by OCT consecutive lanes.
-template <int R, int OCT, int RS>
+template <int R, int OCT, int RS, int NU = 4>
 __device__ __forceinline__ void unit_walk(const LProb &P, const LTile &t,
                                           int u0, int tid, int nthr, int s0,
-                                          int (&g)[4], int (&la)[4]) {
+                                          int (&g)[NU], int (&la)[NU]) {
   const int step = nthr / OCT;
   const int kk0 = u0 / OCT + tid / OCT, o = tid % OCT;
   const int P2 = R >= 2 ? 1 << P.lgP2 : 1;
   if (R == 1) {
     const int base = t.kbase + 8 * o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NU; ++j) {
       const int kk = min(kk0 + j * step, P.ebox - 1);
       g[j] = base + __umul24((unsigned)min(kk, t.E[2] - 1), (unsigned)t.SK[2]);
       la[j] = __umul24(kk, RS) + 8 * o;
@@ -379,7 +379,7 @@ __device__ __forceinline__ void unit_walk(const LProb &P, const LTile &t,
     const int base = t.kbase + 8 * o + __umul24((unsigned)min(e2, t.E[2] - 1), (unsigned)t.SK[2]);
     const int Em1 = P.ax[1].Em;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NU; ++j) {
       const int row = min(row0 + j * drow, Em1 - 1);
       g[j] = base + __umul24((unsigned)min(row, t.E[1] - 1), (unsigned)t.SK[1]);
       la[j] = __umul24((row << P.lgP2) + e2, RS) + 8 * o;
@@ -387,7 +387,7 @@ __device__ __forceinline__ void unit_walk(const LProb &P, const LTile &t,
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NU; ++j) {
     const int kk = min(kk0 + j * step, P.ebox - 1);
     g[j] = unit_offset<R>(P, t, kk, o, s0);
     la[j] = __umul24(kk, RS) + 8 * o;

@@ -359,15 +359,19 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
   typedef typename L16<T>::v8 v8;
   constexpr int OCT = D / 8;
   constexpr int RSE = lds_row(D);
+  // units per lane in flight: two for the wider rank-1 heads, whose
+  // backward keeps four waves per SIMD (its dK / dV accumulators and the
+  // key's own rows stay live across the staging)
+  constexpr int NU = R == 1 && D >= 64 ? 2 : 4;
   const int nun = P.ebox * OCT;
   const int o = tid % OCT;  // the lane's unit in each of its rows
-  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
-    v8 qr[4], dr[4], orr[4];
-    float lr[4], dl[4];
-    int g[4], la[4];
-    unit_walk<R, OCT, RSE>(P, t, u0, tid, nthr, s0, g, la);
+  for (int u0 = 0; u0 < nun; u0 += NU * nthr) {
+    v8 qr[NU], dr[NU], orr[NU];
+    float lr[NU], dl[NU];
+    int g[NU], la[NU];
+    unit_walk<R, OCT, RSE, NU>(P, t, u0, tid, nthr, s0, g, la);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NU; ++j) {
       const int row = (g[j] - 8 * o) / D;
       qr[j] = ld8(q, g[j]);
       dr[j] = ld8(dout, g[j]);
@@ -376,7 +380,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
       dl[j] = dlse != nullptr ? ldf(dlse, row) : 0.f;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NU; ++j) {
       *reinterpret_cast<v8 *>(qs + la[j]) = qr[j];
       *reinterpret_cast<v8 *>(os + la[j]) = dr[j];
       float part = 0.f;
@@ -479,6 +483,7 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
 // whole launch resident at once.
 template <typename T, int D, int R, bool CPR1, bool VX>
 __global__ void __launch_bounds__(512)
+    __attribute__((amdgpu_waves_per_eu(D == 64 && R == 1 ? 4 : 1)))
     k_wbwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, const T *__restrict__ out,
@@ -645,15 +650,20 @@ __global__ void __launch_bounds__(512)
             kr[h][st] = *reinterpret_cast<const v8 *>(ks + kb[h] * RSE + ka_off + 32 * st);
             vr[h][st] = *reinterpret_cast<const v8 *>(vs + kb[h] * RSE + ka_off + 32 * st);
           }
-        // K^T operands of dQ^T += K^T . dS^T, read now so their latency
-        // overlaps the score MFMAs and exponentials
+        // K^T operands of dQ^T += K^T . dS^T: read now so their latency
+        // overlaps the score MFMAs and exponentials, or after the scores
+        // for the wider rank-1 heads (as in the dK / dV half)
         v8 kt[NDB];
+        auto read_kt = [&]() {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const v4 lo4 = M::tr(ks + kb[0] * RSE + tr_off + 16 * db);
-          const v4 hi4 = M::tr(ks + kb[1] * RSE + tr_off + 16 * db);
-          kt[db] = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        }
+          for (int db = 0; db < NDB; ++db) {
+            const v4 lo4 = M::tr(ks + kb[0] * RSE + tr_off + 16 * db);
+            const v4 hi4 = M::tr(ks + kb[1] * RSE + tr_off + 16 * db);
+            kt[db] = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+          }
+        };
+        constexpr bool EARLY_KT = D == 32 || R != 1;
+        if (EARLY_KT) read_kt();
         __builtin_amdgcn_sched_barrier(0);  // keep every read of the pair ahead
         // S^T masked through its initial value, dP^T - delta through its
         f32x4 sc[2], dp[2];
@@ -685,6 +695,7 @@ __global__ void __launch_bounds__(512)
             const float p = __builtin_amdgcn_exp2f(fmaf(sc[h][r], sl2, -lse2));
             bs[4 * h + r] = (E)(p * dp[h][r]);
           }
+        if (!EARLY_KT) read_kt();
         // dQ^T += K^T . dS^T
 #pragma unroll
         for (int db = 0; db < NDB; ++db) acc[db] = M::mma(kt[db], bs, acc[db]);
@@ -783,18 +794,24 @@ __global__ void __launch_bounds__(512)
         for (int r = 0; r < 4; ++r)
           ls2[h][r] = *reinterpret_cast<const float *>(xs + kb[h] * RSE + pad_off + r * RSE);
       }
-      // dO^T and Q^T operands of the dV / dK MFMAs, read now so their
-      // latency overlaps the score MFMAs and exponentials
+      // dO^T and Q^T operands of the dV / dK MFMAs.  Head_dim 32: read now
+      // so their latency overlaps the score MFMAs and exponentials; wider
+      // heads read them after the scores (the Q / dO rows are dead by
+      // then), which keeps the rank-1 kernel within four waves per SIMD
       v8 ot[NDB], qt[NDB];
+      auto read_t = [&]() {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const v4 o0 = M::tr(ys + kb[0] * RSE + tr_off + 16 * db);
-        const v4 o1 = M::tr(ys + kb[1] * RSE + tr_off + 16 * db);
-        ot[db] = __builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7);
-        const v4 q0 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
-        const v4 q1 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
-        qt[db] = __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
+        for (int db = 0; db < NDB; ++db) {
+          const v4 o0 = M::tr(ys + kb[0] * RSE + tr_off + 16 * db);
+          const v4 o1 = M::tr(ys + kb[1] * RSE + tr_off + 16 * db);
+          ot[db] = __builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7);
+          const v4 q0 = M::tr(xs + kb[0] * RSE + tr_off + 16 * db);
+          const v4 q1 = M::tr(xs + kb[1] * RSE + tr_off + 16 * db);
+          qt[db] = __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      };
+      constexpr bool EARLY_T = D == 32 || R != 1;
+      if (EARLY_T) read_t();
       __builtin_amdgcn_sched_barrier(0);  // keep every read of the pair ahead
       // S masked through its initial value, dP - delta through its
       f32x4 sc[2], dp[2];
@@ -826,6 +843,7 @@ __global__ void __launch_bounds__(512)
           bp[4 * h + r] = (E)p;
           bs[4 * h + r] = (E)(p * dp[h][r]);
         }
+      if (!EARLY_T) read_t();
       // dV^T += dO^T . P, dK^T += Q^T . dS
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
