@@ -220,6 +220,8 @@ def _roof(call, nbytes, flops, timing, flop_peak, traffic=None):
             "call_ms": round(ms, 5), "algorithmic_bytes": nbytes, "flops": flops,
             "flop_frac": round(flops / (ms * 1e-3) / 1e12 / flop_peak, 6),
             "single_call_ms": round(timing["single_ms"], 5),
+            "cache": "warm: back-to-back calls, the inputs stay in the 256 MB Infinity "
+                     "Cache between them; mall_flushed: one call after a 512 MB read",
             "mall_flushed": {"call_ms": round(timing["flushed_ms"], 5),
                              "achieved": round(cold, 2),
                              "frac": round(cold / HBM_PEAK_GBS, 5)}}
