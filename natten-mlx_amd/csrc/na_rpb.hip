@@ -398,6 +398,145 @@ __global__ void __launch_bounds__(512)
   if (g.live) st_row<TO, VEC>(out + g.id * A.D, acc, post, g.lane, G, A.D);
 }
 
+// ---- rank 1, fp32, head_dim 4 NC <= 16, window side K fixed ----------------
+// The DiNAT 1-D shapes (fp32 rows of a few 16-byte units, K in 3..13) with
+// the neighbor window staged: one thread per row, the slot loop unrolled
+// over K with each slot row read from LDS at a constant stride from the
+// first.  LDS layout per block of nthr rows: the block's slot rows
+// (nthr * K floats, rounded to 16 bytes), the window of rows
+// [row0 - K d step, row0 + nthr + K d step) clamped to the tensor, then
+// (k_r1_dot) the bias table [H, 2K-1].
+
+// Window row range of the block and its first slot row / slot stride.
+struct R1Rows {
+  int lo, hi;  // staged rows [lo, hi)
+  int rows;    // live rows of the block
+  int r;       // this thread's row (clamped to the block's last live row)
+};
+
+template <int K>
+__device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
+  R1Rows o;
+  const int nthr = (int)blockDim.x;
+  const int row0 = (int)blockIdx.x * nthr;
+  o.rows = min(nthr, A.n_rows - row0);
+  o.r = row0 + min((int)threadIdx.x, o.rows - 1);
+  const int reach = K * A.d0 * step;
+  o.lo = max(0, row0 - reach);
+  o.hi = min(A.n_rows, row0 + o.rows + reach);
+  return o;
+}
+
+// logits / dattn: out[r, k] = <x'[r], y[nbr(r, k)]> (+ bias) or `fill`.
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1_dot(RpbProb A, const float *__restrict__ x, const float *__restrict__ y,
+             const float *__restrict__ rpb, float *__restrict__ out,
+             int scale_x, float fill) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const int step = A.heads_first ? 1 : A.H;
+  const R1Rows b = r1_rows<K>(A, step);
+  float *so = reinterpret_cast<float *>(sm4);
+  float4 *win = sm4 + (nthr * K + 3) / 4;
+  float4 xv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) xv[c] = reinterpret_cast<const float4 *>(x)[(int64_t)b.r * NC + c];
+  block_copy16(reinterpret_cast<uint4 *>(win),
+               reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC,
+               (int64_t)(b.hi - b.lo) * NC);
+  constexpr int R0 = 2 * K - 1;
+  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * K * A.d0 * step) * NC);
+  if (rpb != nullptr)
+    for (int i = tid; i < A.H * R0; i += nthr) bs[i] = rpb[i];
+  const RPos p = rpos(A, (uint32_t)b.r);
+  const RWin w = rwin_axis(K, A.d0, A.fd0, p.i0, A.L0);
+  if (scale_x) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      xv[c].x *= A.scale;
+      xv[c].y *= A.scale;
+      xv[c].z *= A.scale;
+      xv[c].w *= A.scale;
+    }
+  }
+  __syncthreads();
+  // slot k reads window row r - lo + (s + k d - i0) step; every such row
+  // (valid slot or not) lies in the staged range or the LDS after it
+  const float4 *yb = win + (b.r - b.lo + (w.s - p.i0) * step) * NC;
+  const int ys = A.d0 * step * NC;
+  const float *br = bs + p.h * R0;
+  float *sr = so + tid * K;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 t = yb[k * ys + c];
+      acc = fmaf(xv[c].x, t.x, acc);
+      acc = fmaf(xv[c].y, t.y, acc);
+      acc = fmaf(xv[c].z, t.z, acc);
+      acc = fmaf(xv[c].w, t.w, acc);
+    }
+    if (rpb != nullptr) acc += br[clampi(w.pb + k, 0, R0 - 1)];
+    sr[k] = w.s + k * A.d0 < w.e ? acc : fill;
+  }
+  __syncthreads();
+  block_copy_f32(out + (int64_t)blockIdx.x * nthr * K, so, (int64_t)b.rows * K);
+}
+
+// AV / dq: out[r] = post * sum_k w[r, k] * y[nbr(r, k)] over valid slots.
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1_gather(RpbProb A, const float *__restrict__ wgt,
+                const float *__restrict__ y, float *__restrict__ out,
+                float post) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const int step = A.heads_first ? 1 : A.H;
+  const R1Rows b = r1_rows<K>(A, step);
+  float *sw = reinterpret_cast<float *>(sm4);
+  float4 *win = sm4 + (nthr * K + 3) / 4;
+  block_copy_f32(sw, wgt + (int64_t)blockIdx.x * nthr * K, (int64_t)b.rows * K);
+  block_copy16(reinterpret_cast<uint4 *>(win),
+               reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC,
+               (int64_t)(b.hi - b.lo) * NC);
+  const RPos p = rpos(A, (uint32_t)b.r);
+  const RWin w = rwin_axis(K, A.d0, A.fd0, p.i0, A.L0);
+  __syncthreads();
+  const float4 *yb = win + (b.r - b.lo + (w.s - p.i0) * step) * NC;
+  const int ys = A.d0 * step * NC;
+  const float *wr = sw + tid * K;
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (w.s + k * A.d0 < w.e) {
+      const float wk = wr[k];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 t = yb[k * ys + c];
+        acc[c].x = fmaf(wk, t.x, acc[c].x);
+        acc[c].y = fmaf(wk, t.y, acc[c].y);
+        acc[c].z = fmaf(wk, t.z, acc[c].z);
+        acc[c].w = fmaf(wk, t.w, acc[c].w);
+      }
+    }
+  }
+  if (tid < b.rows) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float4 o = acc[c];
+      o.x *= post;
+      o.y *= post;
+      o.z *= post;
+      o.w *= post;
+      reinterpret_cast<float4 *>(out)[(int64_t)b.r * NC + c] = o;
+    }
+  }
+}
+
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
 // transpose of k_rpb_gather, evaluated per key row.  A query i can hold key
 // j only on j's dilation phase and within K*d of it, so the candidates
@@ -691,10 +830,96 @@ size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes, int rb) {
   return slot_bytes + b <= 65536 ? b : 0;
 }
 
+// LDS of the rank-1 fp32 kernels (k_r1_dot / k_r1_gather) for blocks of rb
+// rows, or 0 where they do not apply: rank 2, head_dim not a multiple of 4
+// or above 16, K outside {3, 5, .., 13}, K d > L (windows with slots before
+// the sequence), or a halo larger than the block's rows (large dilations:
+// the generic kernels read those rows directly).  With K d <= L every
+// window lies inside the sequence, so each slot row is in the staged range.
+size_t r1_lds(const RpbProb &A, int rb, bool bias) {
+  if (A.rank != 1 || A.D % 4 != 0 || A.D > 16) return 0;
+  if ((int64_t)A.K0 * A.d0 > A.L0) return 0;
+  if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
+  const int64_t step = A.heads_first ? 1 : A.H;
+  const int64_t wrows = rb + 2 * (int64_t)A.K0 * A.d0 * step;
+  if (wrows > 2 * (int64_t)rb) return 0;
+  const size_t b = ((size_t)rb * A.K0 * 4 + 15) / 16 * 16 + (size_t)wrows * A.D * 4 +
+                   (bias ? (size_t)A.H * A.R0 * 4 : 0);
+  return b <= 65536 ? b : 0;
+}
+
+#define R1_K(KK_, BODY)           \
+  switch (KK_) {                  \
+    case 3: BODY(3, NC_); break;  \
+    case 5: BODY(5, NC_); break;  \
+    case 7: BODY(7, NC_); break;  \
+    case 9: BODY(9, NC_); break;  \
+    case 11: BODY(11, NC_); break; \
+    default: BODY(13, NC_); break; \
+  }
+
+// The rank-1 fp32 dot / gather when r1_lds applies; false otherwise.
+bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
+            float *out, int scale_x, float fill, hipStream_t st) {
+  const int rb = rpb_block(A);
+  const size_t lds = r1_lds(A, rb, rpb != nullptr);
+  if (lds == 0) return false;
+  const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
+#define R1D_(KK, NC)                                                           \
+  hipLaunchKernelGGL((k_r1_dot<KK, NC>), grid, dim3(rb), lds, st, A, x, y, rpb, \
+                     out, scale_x, fill)
+  switch (A.D / 4) {
+#define NC_ 1
+    case 1: R1_K(A.K0, R1D_) break;
+#undef NC_
+#define NC_ 2
+    case 2: R1_K(A.K0, R1D_) break;
+#undef NC_
+#define NC_ 3
+    case 3: R1_K(A.K0, R1D_) break;
+#undef NC_
+#define NC_ 4
+    default: R1_K(A.K0, R1D_) break;
+#undef NC_
+  }
+#undef R1D_
+  return true;
+}
+
+bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
+               float post, hipStream_t st) {
+  const int rb = rpb_block(A);
+  const size_t lds = r1_lds(A, rb, false);
+  if (lds == 0) return false;
+  const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
+#define R1G_(KK, NC) \
+  hipLaunchKernelGGL((k_r1_gather<KK, NC>), grid, dim3(rb), lds, st, A, w, y, out, post)
+  switch (A.D / 4) {
+#define NC_ 1
+    case 1: R1_K(A.K0, R1G_) break;
+#undef NC_
+#define NC_ 2
+    case 2: R1_K(A.K0, R1G_) break;
+#undef NC_
+#define NC_ 3
+    case 3: R1_K(A.K0, R1G_) break;
+#undef NC_
+#define NC_ 4
+    default: R1_K(A.K0, R1G_) break;
+#undef NC_
+  }
+#undef R1G_
+  return true;
+}
+#undef R1_K
+
 template <typename TX, typename TY>
 void launch_dot(const RpbProb &A, const void *x, const void *y,
                 const float *rpb, float *out, int scale_x, float fill,
                 hipStream_t st) {
+  if constexpr (sizeof(TX) == 4 && sizeof(TY) == 4) {
+    if (r1_dot(A, (const float *)x, (const float *)y, rpb, out, scale_x, fill, st)) return;
+  }
   constexpr int V = vmax_of<TX, TY>();
   const RShape s = rshape(A.D, V);
   const int rb = rpb_block(A);
@@ -721,6 +946,9 @@ void launch_dot(const RpbProb &A, const void *x, const void *y,
 template <typename TY, typename TO>
 void launch_gather(const RpbProb &A, const float *w, const void *y, void *out,
                    float post, hipStream_t st) {
+  if constexpr (sizeof(TY) == 4 && sizeof(TO) == 4) {
+    if (r1_gather(A, w, (const float *)y, (float *)out, post, st)) return;
+  }
   constexpr int V = vmax_of<TY, TO>();
   const RShape s = rshape(A.D, V);
   const int rb = rpb_block(A);
