@@ -524,17 +524,22 @@ __global__ void __launch_bounds__(512)
       }
     }
   }
-  if (tid < b.rows) {
+  // the block's output rows are one contiguous range: write them through
+  // LDS (over the weights and window, once every thread has read them) as
+  // consecutive 16-byte units rather than one strided row per lane
+  __syncthreads();
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float4 o = acc[c];
-      o.x *= post;
-      o.y *= post;
-      o.z *= post;
-      o.w *= post;
-      reinterpret_cast<float4 *>(out)[(int64_t)b.r * NC + c] = o;
-    }
+  for (int c = 0; c < NC; ++c) {
+    float4 o = acc[c];
+    o.x *= post;
+    o.y *= post;
+    o.z *= post;
+    o.w *= post;
+    sm4[tid * NC + c] = o;
   }
+  __syncthreads();
+  block_copy16(reinterpret_cast<uint4 *>(out) + (int64_t)blockIdx.x * nthr * NC,
+               reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
 }
 
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
