@@ -632,13 +632,18 @@ LChoice lean_choice(const Prob &P, LMode mode) {
     if (a < lead) return 1;
     const Axis &x = P.ax[a];
     if (P.sample_extent != nullptr) {
-      // any sample: a box spans at most t + K - 1 points of a phase no
-      // longer than the tensor's; an inverse box on a non-causal axis up to
-      // t + 2 (K - 1) (keys within K of an end of the sample are in the
-      // windows of every query up to that end, and a short sample puts both
-      // ends in one tile's reach)
+      // any sample (phase length >= K): a box of a tile of t points
+      // spans at most t + K - 1 points of a phase no longer than the
+      // tensor's.  An inverse box on a non-causal axis spans more where the
+      // tile's keys are within K of an end of the sample (those keys are
+      // in the windows of every query up to that end): with tiles starting
+      // at multiples of t >= K, at most t + K - 1 + K / 2 (the last full
+      // tile before the sample's end), else t + 2 (K - 1).  Both bounds
+      // are attained.
       const bool inv = (mode == kLBwd || mode == kLInv) && !x.causal;
-      return std::min((x.L + x.d - 1) / x.d, t + (inv ? 2 : 1) * (x.K - 1));
+      const int e = !inv ? t + x.K - 1
+                         : (t >= x.K ? t + x.K - 1 + x.K / 2 : t + 2 * (x.K - 1));
+      return std::min((x.L + x.d - 1) / x.d, e);
     }
     if (mode == kLInv) return box_max(x, t, true);
     const int f = box_max(x, t, false);
