@@ -115,3 +115,40 @@ def test_plans_of_the_benchmarked_configs():
     small = _plan((3, 300, 8, 64), 2, (63,), (2,), (False,),
                   **dict(kw, sample_extent=torch.full((3, 1), 300, dtype=torch.int32)))
     assert small["path"] == "lean" and not small["grouped_heads"], small
+
+
+def _box_need(L, K, d, t, inverse):
+    """Largest box over the tiles [t0, t0 + t) (t0 = 0, t, 2t, ..) of every
+    dilation phase of a sample of L points, by enumeration of the window
+    rules: forward, the keys of the tile's queries; inverse, the queries
+    whose windows hold the tile's keys (non-causal axis)."""
+    nh = K // 2
+    best = 0
+    for r in range(min(d, L)):
+        Lr = (L - 1 - r) // d + 1
+        for t0 in range(0, Lr, t):
+            t1 = min(t0 + t, Lr) - 1
+            if inverse:
+                lo = 0 if t0 <= K - 1 else t0 - nh
+                hi = Lr if t1 >= Lr - K else t1 + nh + 1
+            else:
+                lo = min(max(t0 - nh, 0), Lr - K)
+                hi = min(max(t1 - nh, 0), Lr - K) + K
+            best = max(best, hi - lo)
+    return best
+
+
+def test_varlen_backward_box_covers_every_sample_length():
+    """With per-sample extents the staged box is planned for any sample
+    length the caller may pass (d K <= L_b <= L): it must hold the forward
+    and inverse boxes of every tile of every such length."""
+    for L, K, d, H in ((4096, 63, 2, 16), (700, 15, 1, 4), (900, 31, 3, 8)):
+        ext = torch.full((2, 1), L, dtype=torch.int32)
+        kw = dict(sample_extent=ext, dtype=torch.float16, varlen_clamped=True)
+        p = _plan((2, L, H, 64), H // 4 if H >= 4 else 1, (K,), (d,), (False,),
+                  backward=True, **kw)
+        assert p["path"] == "lean", p
+        t = p["tile"][2] * p["waves"]
+        need = max(max(_box_need(Lb, K, d, t, True), _box_need(Lb, K, d, t, False))
+                   for Lb in range(d * K, L + 1, 7 if L > 1000 else 1))
+        assert p["box"][2] >= need, (L, K, d, p, need)
