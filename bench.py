@@ -335,8 +335,10 @@ PROFILE_SUMMARIES = {
     "cfg2": [os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_hbm_traffic.md"),
              os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_lean_fwd_bwd.md")],
     "cfg3": [os.path.join(ROOT, "profiles", "na3d_16x32x32_k377_causal_bf16_lean_fwd_bwd.md")],
+    "cfg5": [os.path.join(ROOT, "profiles", "allin1_1d_2048x12_k7_f32_rpb.md")],
 }
-CALL_KERNEL = {"na_fwd": "k_wfwd", "na_bwd": "k_wbwd"}
+CALL_KERNEL = {"na_fwd": "k_wfwd", "na_bwd": "k_wbwd", "na_rpb_qk_fwd": "k_r1_dot",
+               "na_rpb_av_fwd": "k_r1_gather"}
 
 
 def _profile_figure(key: str, call: str, workload: str, kind):
@@ -689,8 +691,10 @@ def wl_cfg5(args):
             tab = call_timing(lambda: hip.rpb_av_backward(attn, v, v, Kx, d))
             lg = rows * Kx * 4
             qk_b, av_b = 2 * t + lg, lg + 2 * t
-            rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, tq, FP32_PEAK_TFLOPS)
-            ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, ta, FP32_PEAK_TFLOPS)
+            rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, tq, FP32_PEAK_TFLOPS,
+                       measured_traffic("na_rpb_qk_fwd", "cfg5") if (Kx, d) == (7, 1) else None)
+            ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, ta, FP32_PEAK_TFLOPS,
+                       measured_traffic("na_rpb_av_fwd", "cfg5") if (Kx, d) == (7, 1) else None)
             table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd_ms": round(tqb["warm_ms"], 5),
                                     "av_bwd_ms": round(tab["warm_ms"], 5)}
             if Kx == 7 and d == 1:
