@@ -427,12 +427,13 @@ __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
   return o;
 }
 
-// logits / dattn: out[r, k] = <x'[r], y[nbr(r, k)]> (+ bias) or `fill`.
+// logits / dattn: out[r, k] = <x'[r], y[nbr(r, k)]> (+ bias); every slot is
+// inside its window here, so no slot takes the `fill` value.
 template <int K, int NC>
 __global__ void __launch_bounds__(512)
     k_r1_dot(RpbProb A, const float *__restrict__ x, const float *__restrict__ y,
              const float *__restrict__ rpb, float *__restrict__ out,
-             int scale_x, float fill) {
+             int scale_x) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int step = A.heads_first ? 1 : A.H;
@@ -461,8 +462,9 @@ __global__ void __launch_bounds__(512)
     }
   }
   __syncthreads();
-  // slot k reads window row r - lo + (s + k d - i0) step; every such row
-  // (valid slot or not) lies in the staged range or the LDS after it
+  // slot k reads window row r - lo + (s + k d - i0) step.  With K d <= L
+  // (r1_lds) every window lies inside its sequence: all K slots are valid
+  // and their rows lie in the staged range
   const float4 *yb = win + (b.r - b.lo + (w.s - p.i0) * step) * NC;
   const int ys = A.d0 * step * NC;
   const float *br = bs + p.h * R0;
@@ -479,7 +481,7 @@ __global__ void __launch_bounds__(512)
       acc = fmaf(xv[c].w, t.w, acc);
     }
     if (rpb != nullptr) acc += br[clampi(w.pb + k, 0, R0 - 1)];
-    sr[k] = w.s + k * A.d0 < w.e ? acc : fill;
+    sr[k] = acc;
   }
   __syncthreads();
   block_copy_f32(out + (int64_t)blockIdx.x * nthr * K, so, (int64_t)b.rows * K);
@@ -512,16 +514,14 @@ __global__ void __launch_bounds__(512)
   for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    if (w.s + k * A.d0 < w.e) {
-      const float wk = wr[k];
+    const float wk = wr[k];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const float4 t = yb[k * ys + c];
-        acc[c].x = fmaf(wk, t.x, acc[c].x);
-        acc[c].y = fmaf(wk, t.y, acc[c].y);
-        acc[c].z = fmaf(wk, t.z, acc[c].z);
-        acc[c].w = fmaf(wk, t.w, acc[c].w);
-      }
+    for (int c = 0; c < NC; ++c) {
+      const float4 t = yb[k * ys + c];
+      acc[c].x = fmaf(wk, t.x, acc[c].x);
+      acc[c].y = fmaf(wk, t.y, acc[c].y);
+      acc[c].z = fmaf(wk, t.z, acc[c].z);
+      acc[c].w = fmaf(wk, t.w, acc[c].w);
     }
   }
   // the block's output rows are one contiguous range: write them through
@@ -863,16 +863,17 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
     default: BODY(13, NC_); break; \
   }
 
-// The rank-1 fp32 dot / gather when r1_lds applies; false otherwise.
+// The rank-1 fp32 dot / gather when r1_lds applies; false otherwise (no
+// slot of these shapes is outside its window, so `fill` is never written).
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
-            float *out, int scale_x, float fill, hipStream_t st) {
+            float *out, int scale_x, hipStream_t st) {
   const int rb = rpb_block(A);
   const size_t lds = r1_lds(A, rb, rpb != nullptr);
   if (lds == 0) return false;
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
 #define R1D_(KK, NC)                                                           \
   hipLaunchKernelGGL((k_r1_dot<KK, NC>), grid, dim3(rb), lds, st, A, x, y, rpb, \
-                     out, scale_x, fill)
+                     out, scale_x)
   switch (A.D / 4) {
 #define NC_ 1
     case 1: R1_K(A.K0, R1D_) break;
@@ -923,7 +924,7 @@ void launch_dot(const RpbProb &A, const void *x, const void *y,
                 const float *rpb, float *out, int scale_x, float fill,
                 hipStream_t st) {
   if constexpr (sizeof(TX) == 4 && sizeof(TY) == 4) {
-    if (r1_dot(A, (const float *)x, (const float *)y, rpb, out, scale_x, fill, st)) return;
+    if (r1_dot(A, (const float *)x, (const float *)y, rpb, out, scale_x, st)) return;
   }
   constexpr int V = vmax_of<TX, TY>();
   const RShape s = rshape(A.D, V);
