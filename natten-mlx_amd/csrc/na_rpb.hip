@@ -427,6 +427,26 @@ __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
   return o;
 }
 
+// A block copy of n >= 1 16-byte units in two steps: load() issues the
+// first four units of each thread (indices clamped onto the last unit), so
+// a kernel can issue its other loads beside them before any is waited on;
+// store() writes them to LDS (clamped indices rewrite the last unit with its
+// own value: no branch for the loads to sink into) and copies any further
+// units.
+struct R1Copy {
+  uint4 r[4];
+  __device__ __forceinline__ void load(const uint4 *src, int n, int tid, int nthr) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = src[min(tid + j * nthr, n - 1)];
+  }
+  __device__ __forceinline__ void store(uint4 *dst, const uint4 *src, int n, int tid,
+                                        int nthr) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[min(tid + j * nthr, n - 1)] = r[j];
+    block_copy16(dst + 4 * nthr, src + 4 * nthr, (int64_t)n - 4 * nthr);
+  }
+};
+
 // logits / dattn: out[r, k] = <x'[r], y[nbr(r, k)]> (+ bias); every slot is
 // inside its window here, so no slot takes the `fill` value.
 template <int K, int NC>
@@ -440,16 +460,22 @@ __global__ void __launch_bounds__(512)
   const R1Rows b = r1_rows<K>(A, step);
   float *so = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
+  constexpr int R0 = 2 * K - 1;
+  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * K * A.d0 * step) * NC);
+  // every load of the prologue is issued before any is waited on: the query
+  // row, one bias entry per thread (H (2K - 1) <= nthr; without a bias table
+  // a harmless read of x into the spare slot), the window's first units
   float4 xv[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) xv[c] = reinterpret_cast<const float4 *>(x)[(int64_t)b.r * NC + c];
-  block_copy16(reinterpret_cast<uint4 *>(win),
-               reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC,
-               (int64_t)(b.hi - b.lo) * NC);
-  constexpr int R0 = 2 * K - 1;
-  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * K * A.d0 * step) * NC);
-  if (rpb != nullptr)
-    for (int i = tid; i < A.H * R0; i += nthr) bs[i] = rpb[i];
+  const int nb = rpb != nullptr ? A.H * R0 : 1;
+  const float bv = (rpb != nullptr ? rpb : x)[min(tid, nb - 1)];
+  const uint4 *ysrc = reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC;
+  const int nwin = (b.hi - b.lo) * NC;
+  R1Copy cw;
+  cw.load(ysrc, nwin, tid, nthr);
+  bs[min(tid, nb - 1)] = bv;
+  cw.store(reinterpret_cast<uint4 *>(win), ysrc, nwin, tid, nthr);
   const RPos p = rpos(A, (uint32_t)b.r);
   const RWin w = rwin_axis(K, A.d0, A.fd0, p.i0, A.L0);
   if (scale_x) {
@@ -499,10 +525,29 @@ __global__ void __launch_bounds__(512)
   const R1Rows b = r1_rows<K>(A, step);
   float *sw = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
-  block_copy_f32(sw, wgt + (int64_t)blockIdx.x * nthr * K, (int64_t)b.rows * K);
-  block_copy16(reinterpret_cast<uint4 *>(win),
-               reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC,
-               (int64_t)(b.hi - b.lo) * NC);
+  // every load of the prologue is issued before any is waited on: the
+  // block's weight rows (16-byte aligned: row0 K is a multiple of 4) as
+  // units plus a tail of floats, and the window's first units
+  constexpr int JW = (K + 3) / 4;  // weight units per thread (rows <= nthr)
+  const int nwf = b.rows * K, nw4 = nwf >> 2;
+  const float *wg = wgt + (int64_t)blockIdx.x * nthr * K;
+  const uint4 *ysrc = reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC;
+  const int nwin = (b.hi - b.lo) * NC;
+  // without a whole weight unit the unit loads read the window instead and
+  // the tail rewrites the floats they covered
+  const uint4 *wsrc = nw4 > 0 ? reinterpret_cast<const uint4 *>(wg) : ysrc;
+  uint4 wu[JW];
+#pragma unroll
+  for (int j = 0; j < JW; ++j) wu[j] = wsrc[min(tid + j * nthr, max(nw4, 1) - 1)];
+  const int ti = min(4 * nw4 + tid, nwf - 1);  // the tail floats (clamped)
+  const float wt = wg[ti];
+  R1Copy cw;
+  cw.load(ysrc, nwin, tid, nthr);
+#pragma unroll
+  for (int j = 0; j < JW; ++j)
+    reinterpret_cast<uint4 *>(sw)[min(tid + j * nthr, max(nw4, 1) - 1)] = wu[j];
+  sw[ti] = wt;
+  cw.store(reinterpret_cast<uint4 *>(win), ysrc, nwin, tid, nthr);
   const RPos p = rpos(A, (uint32_t)b.r);
   const RWin w = rwin_axis(K, A.d0, A.fd0, p.i0, A.L0);
   __syncthreads();
@@ -845,11 +890,12 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
   if (A.rank != 1 || A.D % 4 != 0 || A.D > 16) return 0;
   if ((int64_t)A.K0 * A.d0 > A.L0) return 0;
   if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
+  if (bias && A.H * A.R0 > rb) return 0;  // one bias entry per thread
   const int64_t step = A.heads_first ? 1 : A.H;
   const int64_t wrows = rb + 2 * (int64_t)A.K0 * A.d0 * step;
   if (wrows > 2 * (int64_t)rb) return 0;
   const size_t b = ((size_t)rb * A.K0 * 4 + 15) / 16 * 16 + (size_t)wrows * A.D * 4 +
-                   (bias ? (size_t)A.H * A.R0 * 4 : 0);
+                   (bias ? (size_t)A.H * A.R0 * 4 : 4);  // the bias table or a spare float
   return b <= 65536 ? b : 0;
 }
 
