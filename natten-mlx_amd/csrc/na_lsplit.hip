@@ -364,25 +364,37 @@ __global__ void __launch_bounds__(1024)
   // so that rowlen is a multiple of it)
   typedef typename RawWord<VW * 2>::type VU;
   const int ups = rowlen / VW;  // units per position
+  const int nun = 16 * ups;
   const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
-  for (int u = tid; u < 16 * ups; u += nthr) {
-    const int p = (int)fdiv((uint32_t)u, fups);
-    const int iu = u - p * ups;
-    int uu[3];
-    uu[2] = p & (P.ax[2].T - 1);
-    uu[1] = (p >> lg2) & (P.ax[1].T - 1);
-    uu[0] = p >> (lg2 + lg1);
-    bool pv = true;
-    int tok = t.b * P.Ltot;
+  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
+    // four units per thread: their LDS reads together, then the stores
+    VU val[4];
+    size_t dst[4];
+    bool ok[4];
 #pragma unroll
-    for (int a = 3 - R; a < 3; ++a) {
-      const LAx &xa = P.ax[a];
-      pv = pv && uu[a] < t.nv[a];
-      tok += (t.r[a] + xa.d * (t.i0[a] + uu[a])) * xa.tok;
+    for (int j = 0; j < 4; ++j) {
+      const int u = min(u0 + tid + j * nthr, nun - 1);
+      const int p = (int)fdiv((uint32_t)u, fups);
+      const int iu = u - p * ups;
+      int uu[3];
+      uu[2] = p & (P.ax[2].T - 1);
+      uu[1] = (p >> lg2) & (P.ax[1].T - 1);
+      uu[0] = p >> (lg2 + lg1);
+      bool pv = u0 + tid + j * nthr < nun;
+      int tok = t.b * P.Ltot;
+#pragma unroll
+      for (int a = 3 - R; a < 3; ++a) {
+        const LAx &xa = P.ax[a];
+        pv = pv && uu[a] < t.nv[a];
+        tok += (t.r[a] + xa.d * (t.i0[a] + uu[a])) * xa.tok;
+      }
+      val[j] = *reinterpret_cast<const VU *>(ob + p * rowlen + iu * VW);
+      dst[j] = (size_t)tok * rowlen + (size_t)iu * VW;
+      ok[j] = pv;
     }
-    if (pv)
-      *reinterpret_cast<VU *>(out + (size_t)tok * rowlen + (size_t)iu * VW) =
-          *reinterpret_cast<const VU *>(ob + p * rowlen + iu * VW);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ok[j]) *reinterpret_cast<VU *>(out + dst[j]) = val[j];
   }
 }
 
@@ -433,28 +445,38 @@ __global__ void __launch_bounds__(1024)
   E *ab = reinterpret_cast<E *>(smem);  // [16 positions][H][kp]
   E *ys = ab + align16(16 * rowlen);     // per wave: NB chunks of 16 rows
   E *yw = ys + w * NB * 16 * RS;
-  // the tile's compact rows, position by position (runs of rowlen)
+  // the tile's compact rows, position by position (runs of rowlen), four
+  // units per thread in flight at a time.  Positions past the tile's valid
+  // extent load a valid position's row (clamped): only the rows of queries
+  // that are not stored read them.  Indices past the end are clamped onto
+  // the last unit, so neither the loads nor the stores branch.
   typedef typename RawWord<VW * 2>::type VU;
   const int ups = rowlen / VW;
+  const int nun = 16 * ups;
   const int lg2 = P.ax[2].lgT, lg1 = P.ax[1].lgT;
-  for (int u = tid; u < 16 * ups; u += nthr) {
-    const int p = (int)fdiv((uint32_t)u, fups);
-    const int iu = u - p * ups;
-    int uu[3];
-    uu[2] = p & (P.ax[2].T - 1);
-    uu[1] = (p >> lg2) & (P.ax[1].T - 1);
-    uu[0] = p >> (lg2 + lg1);
-    bool pv = true;
-    int tok = t.b * P.Ltot;
+  for (int u0 = 0; u0 < nun; u0 += 4 * nthr) {
+    VU val[4];
+    int dst[4];
 #pragma unroll
-    for (int ax = 3 - R; ax < 3; ++ax) {
-      const LAx &xa = P.ax[ax];
-      pv = pv && uu[ax] < t.nv[ax];
-      tok += (t.r[ax] + xa.d * (t.i0[ax] + min(uu[ax], max(t.nv[ax] - 1, 0)))) * xa.tok;
+    for (int j = 0; j < 4; ++j) {
+      const int u = min(u0 + tid + j * nthr, nun - 1);
+      const int p = (int)fdiv((uint32_t)u, fups);
+      const int iu = u - p * ups;
+      int uu[3];
+      uu[2] = p & (P.ax[2].T - 1);
+      uu[1] = (p >> lg2) & (P.ax[1].T - 1);
+      uu[0] = p >> (lg2 + lg1);
+      int tok = t.b * P.Ltot;
+#pragma unroll
+      for (int ax = 3 - R; ax < 3; ++ax) {
+        const LAx &xa = P.ax[ax];
+        tok += (t.r[ax] + xa.d * (t.i0[ax] + min(uu[ax], max(t.nv[ax] - 1, 0)))) * xa.tok;
+      }
+      val[j] = *reinterpret_cast<const VU *>(a + (size_t)tok * rowlen + (size_t)iu * VW);
+      dst[j] = p * rowlen + iu * VW;
     }
-    VU val = *reinterpret_cast<const VU *>(a + (size_t)tok * rowlen + (size_t)iu * VW);
-    if (!pv) val = VU{};
-    *reinterpret_cast<VU *>(ab + p * rowlen + iu * VW) = val;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<VU *>(ab + dst[j]) = val[j];
   }
   __syncthreads();
   const E *mine = ab + n * rowlen + w * kp;
@@ -489,8 +511,11 @@ __global__ void __launch_bounds__(1024)
       const int xc = (CPR1 ? ws.ws[2] : cp[j].col) + 4 * gq;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        // read unconditionally (slot 0 of the row outside the window), then
+        // select: no branch per element
         const bool ok = cp[j].rok && (unsigned)(xc + r - wl[2]) < (unsigned)ww[2];
-        bp[j >> 1][4 * (j & 1) + r] = ok ? mine[cp[j].e01 + xc + r - sq] : (E)0.f;
+        const E av = mine[ok ? cp[j].e01 + xc + r - sq : 0];
+        bp[j >> 1][4 * (j & 1) + r] = ok ? av : (E)0.f;
       }
     }
     wave_lds_sync();  // the previous group's transposing reads are done
