@@ -38,6 +38,26 @@ struct Row {
       if (d0 < D) VecIO<T, VEC>::store(row + d0, v[t]);
     }
   }
+  // load() without a branch: chunks past D read the row's last chunk and
+  // are zeroed by selection, so a load issued ahead of its use stays where
+  // it is issued (no branch for it to sink into).
+  __device__ __forceinline__ void load_nb(const T *row, int lane, int G, int D) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int d0 = (t * G + lane) * VEC;
+      float x[VEC];
+      VecIO<T, VEC>::load(row + min(d0, D - VEC), x);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[t][e] = d0 < D ? x[e] : 0.f;
+    }
+  }
+  // this = this * a + w * o
+  __device__ __forceinline__ void scale_add(float a, float w, const Row &o) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[t][e] = fmaf(v[t][e], a, w * o.v[t][e]);
+  }
   // Partial dot product with a row in memory (lane-local part).
   __device__ __forceinline__ float dot_mem(const T *row, int lane, int G,
                                            int D) const {

@@ -109,18 +109,57 @@ __global__ void __launch_bounds__(256)
     const AxisWin w2 = prob_window(P, 2, p.x[2], L[2]);
     const int32_t d0 = prob_step(P, 0), d1 = prob_step(P, 1),
                   d2 = prob_step(P, 2);
-    for (int32_t k0 = w0.lo; k0 < w0.hi; k0 += d0)
-      for (int32_t k1 = w1.lo; k1 < w1.hi; k1 += d1)
-        for (int32_t k2 = w2.lo; k2 < w2.hi; k2 += d2) {
-          const int64_t row = (tok_in(P, p.b, k0, k1, k2) * P.Hkv + hk) * D;
-          const float s = group_sum(qr.dot_mem(k + row, g.lane, G, D), G) * sl2;
-          const float mn = fmaxf(m, s);
-          const float alpha = exp2f(m - mn);
-          const float pr = exp2f(s - mn);
-          l = fmaf(l, alpha, pr);
-          acc.scale_add_mem(alpha, pr, v + row, g.lane, G, D);
-          m = mn;
+    // The window's keys in slot order (row-major over the axes) through two
+    // register sets that take turns: a key's K and V rows are loaded while
+    // the previous key is processed, so the loads overlap its arithmetic
+    // instead of each waiting alone.  Loads past the last key reload it.
+    auto count = [](const AxisWin &w, int32_t st) {
+      return w.hi > w.lo ? (w.hi - w.lo + st - 1) / st : 0;
+    };
+    const int32_t nk = count(w0, d0) * count(w1, d1) * count(w2, d2);
+    int32_t c0 = w0.lo, c1 = w1.lo, c2 = w2.lo;  // the next key to load
+    int32_t left = nk;                            // keys not yet loaded
+    // a key row (the query's own token's row where the window is empty)
+    int64_t last = (qt * P.Hkv + hk) * D;
+    auto next_row = [&]() -> int64_t {
+      if (left > 0) {
+        last = (tok_in(P, p.b, c0, c1, c2) * P.Hkv + hk) * D;
+        --left;
+        c2 += d2;
+        if (c2 >= w2.hi) {
+          c2 = w2.lo;
+          c1 += d1;
+          if (c1 >= w1.hi) {
+            c1 = w1.lo;
+            c0 += d0;
+          }
         }
+      }
+      return last;
+    };
+    auto step = [&](const Row<T, VEC, NT> &kr, const Row<T, VEC, NT> &vr) {
+      const float s = group_sum(qr.dot(kr), G) * sl2;
+      const float mn = fmaxf(m, s);
+      const float alpha = exp2f(m - mn);
+      const float pr = exp2f(s - mn);
+      l = fmaf(l, alpha, pr);
+      acc.scale_add(alpha, pr, vr);
+      m = mn;
+    };
+    Row<T, VEC, NT> ka, va, kb, vb;
+    int64_t r = next_row();
+    ka.load_nb(k + r, g.lane, G, D);
+    va.load_nb(v + r, g.lane, G, D);
+    for (int32_t i = 0; i < nk; i += 2) {
+      r = next_row();
+      kb.load_nb(k + r, g.lane, G, D);
+      vb.load_nb(v + r, g.lane, G, D);
+      step(ka, va);
+      r = next_row();
+      ka.load_nb(k + r, g.lane, G, D);
+      va.load_nb(v + r, g.lane, G, D);
+      if (i + 1 < nk) step(kb, vb);
+    }
     for (int32_t n = 0; n < P.n_extra; ++n) {
       const int64_t row = (((int64_t)p.b * P.n_extra + n) * P.Hkv + hk) * D;
       const float s = group_sum(qr.dot_mem(ek + row, g.lane, G, D), G) * sl2;
