@@ -311,6 +311,12 @@ __global__ void __launch_bounds__(kXThreads)
 // four waves' sums are added in LDS in wave order at the end.
 constexpr int kXMRows = 128;  // rows per workgroup step (4 waves x 32)
 
+// Row decode divisors of k_xmfma (row = ((o0 O1 + o1) O2 + o2) rep + head):
+// query heads per key/value head, O1 O2 and O2 of the output grid.
+struct XDiv {
+  FastDiv rep, o12, o2;
+};
+
 // delta == nullptr: delta of each row is computed here, rowsum(dO * O) -
 // dlse, from the O row loaded beside the dO row.
 template <typename T, int D>
@@ -319,7 +325,8 @@ __global__ void __launch_bounds__(256)
             const T *__restrict__ ev, const float *__restrict__ lse,
             const float *__restrict__ delta, const T *__restrict__ dout,
             const T *__restrict__ out, const float *__restrict__ dlse,
-            float *__restrict__ part, int ntt, int nsg, int nper, int64_t nrows) {
+            float *__restrict__ part, int ntt, int nsg, int nper, int64_t nrows,
+            XDiv xd) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -384,13 +391,14 @@ __global__ void __launch_bounds__(256)
     st.l2 = INFINITY;
     st.dl = 0.f;
     if (lane < 32) {
-      const int64_t ri = r0 + lane;
-      bool ok = ri < nrows;
-      const int64_t of = ok ? ri / P.rep : 0;
-      const int hr = (int)(ri - of * P.rep);
-      const int o0 = (int)(of / O12);
-      const int rem = (int)(of - (int64_t)o0 * O12);
-      const int o1 = rem / P.ax[2].O;
+      // rows are below 2^31 (xmfma_ok): 32-bit decode by multiply-shift
+      const uint32_t ri = (uint32_t)(r0 + lane);
+      bool ok = ri < (uint64_t)nrows;
+      const uint32_t of = ok ? fdiv(ri, xd.rep) : 0u;
+      const int hr = (int)(ri - of * (uint32_t)P.rep);
+      const int o0 = (int)fdiv(of, xd.o12);
+      const int rem = (int)(of - (uint32_t)o0 * (uint32_t)O12);
+      const int o1 = (int)fdiv((uint32_t)rem, xd.o2);
       const int o2 = rem - o1 * P.ax[2].O;
       ok = ok && o0 < O[0] && o1 < O[1] && o2 < O[2];
       const int h = hk * P.rep + hr;
@@ -564,11 +572,14 @@ void dextra(const Prob &P, int dtype, const void *q, const void *ek,
     const unsigned g1 = (unsigned)((int64_t)P.B * P.Hkv * x.ntt * x.nsg);
     const int64_t n2 = (int64_t)P.B * P.n_extra * P.Hkv * P.D;
     const unsigned g2 = (unsigned)((n2 + kXThreads - 1) / kXThreads);
+    const XDiv xd{make_fastdiv((uint32_t)P.rep),
+                  make_fastdiv((uint32_t)(P.ax[1].O * P.ax[2].O)),
+                  make_fastdiv((uint32_t)P.ax[2].O)};
 #define XM_(TT, DD)                                                              \
   hipLaunchKernelGGL((k_xmfma<TT, DD>), dim3(g1), dim3(256), lds, st, P,         \
                      (const TT *)q, (const TT *)ek, (const TT *)ev, lse, delta,  \
                      (const TT *)dout, (const TT *)out, dlse, part, x.ntt,       \
-                     x.nsg, x.nper, x.nrows)
+                     x.nsg, x.nper, x.nrows, xd)
 #define XMD_(TT)          \
   do {                    \
     if (P.D == 32)        \
