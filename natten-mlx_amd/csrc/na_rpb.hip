@@ -534,8 +534,10 @@ __global__ void __launch_bounds__(512)
   const uint4 *ysrc = reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC;
   const int nwin = (b.hi - b.lo) * NC;
   // without a whole weight unit the unit loads read the window instead and
-  // the tail rewrites the floats they covered
+  // their stores go to the spare unit after the window
   const uint4 *wsrc = nw4 > 0 ? reinterpret_cast<const uint4 *>(wg) : ysrc;
+  uint4 *wdst = nw4 > 0 ? reinterpret_cast<uint4 *>(sw)
+                        : reinterpret_cast<uint4 *>(win + (nthr + 2 * K * A.d0 * step) * NC);
   uint4 wu[JW];
 #pragma unroll
   for (int j = 0; j < JW; ++j) wu[j] = wsrc[min(tid + j * nthr, max(nw4, 1) - 1)];
@@ -544,8 +546,7 @@ __global__ void __launch_bounds__(512)
   R1Copy cw;
   cw.load(ysrc, nwin, tid, nthr);
 #pragma unroll
-  for (int j = 0; j < JW; ++j)
-    reinterpret_cast<uint4 *>(sw)[min(tid + j * nthr, max(nw4, 1) - 1)] = wu[j];
+  for (int j = 0; j < JW; ++j) wdst[min(tid + j * nthr, max(nw4, 1) - 1)] = wu[j];
   sw[ti] = wt;
   cw.store(reinterpret_cast<uint4 *>(win), ysrc, nwin, tid, nthr);
   const RPos p = rpos(A, (uint32_t)b.r);
@@ -895,7 +896,7 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
   const int64_t wrows = rb + 2 * (int64_t)A.K0 * A.d0 * step;
   if (wrows > 2 * (int64_t)rb) return 0;
   const size_t b = ((size_t)rb * A.K0 * 4 + 15) / 16 * 16 + (size_t)wrows * A.D * 4 +
-                   (bias ? (size_t)A.H * A.R0 * 4 : 4);  // the bias table or a spare float
+                   (bias ? (size_t)A.H * A.R0 * 4 : 16);  // the bias table or a spare unit
   return b <= 65536 ? b : 0;
 }
 

@@ -80,6 +80,17 @@ def test_allin1_1d(K, d):
     _check_qk_av(q, k, v, rpb, K, d, 0.288, torch.float32, f"1d K{K} d{d}")
 
 
+@pytest.mark.parametrize("B,L,H,D,K,d", [(1, 257, 1, 12, 3, 1), (2, 300, 3, 8, 5, 2),
+                                           (1, 129, 1, 4, 3, 1), (3, 77, 5, 16, 7, 1)])
+def test_allin1_1d_partial_blocks(B, L, H, D, K, d):
+    """Row counts that leave the last block of the rank-1 fp32 kernels
+    partly empty, down to a single row (fewer than four weight floats)"""
+    _say(f"[case] allin1 1d partial blocks B={B} L={L} H={H} D={D} K={K} d={d}")
+    q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (31, 32, 33))
+    rpb = randn((H, 2 * K - 1), torch.float32, 34, std=0.02)
+    _check_qk_av(q, k, v, rpb, K, d, D ** -0.5, torch.float32, f"1d partial L{L} K{K} d{d}")
+
+
 CASES_2D = [
     # (K, d, Hh, Hw, D)
     (3, 1, 8, 20, 12),
