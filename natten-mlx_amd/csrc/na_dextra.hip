@@ -496,7 +496,9 @@ __global__ void __launch_bounds__(256)
     if (hn) cur = nxt;
     have = hn;
   }
-  // the four waves' sums, added in wave order: red[w][2][16][D]
+  // the four waves' sums, added in wave order: red[w][2][16][D + 1] (the
+  // odd row stride spreads a write's 16 rows over distinct banks)
+  constexpr int RR = D + 1;
   __syncthreads();
   float *red = reinterpret_cast<float *>(xsm);
 #pragma unroll
@@ -504,15 +506,16 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int c = 16 * db + 4 * g + r;
-      red[(w * 2 * 16 + n) * D + c] = adk[db][r];
-      red[(w * 2 * 16 + 16 + n) * D + c] = adv[db][r];
+      red[(w * 2 * 16 + n) * RR + c] = adk[db][r];
+      red[(w * 2 * 16 + 16 + n) * RR + c] = adv[db][r];
     }
   __syncthreads();
   float *dst = part + (((int64_t)(b * P.Hkv + hk) * ntt + tt) * nsg + sg) * 2 * 16 * D;
   for (int i = threadIdx.x; i < 2 * 16 * D; i += 256) {
-    float acc = red[i];
+    const int ri = i / D, ci = i % D;  // D is a power of two
+    float acc = red[ri * RR + ci];
 #pragma unroll
-    for (int ww = 1; ww < 4; ++ww) acc += red[ww * 2 * 16 * D + i];
+    for (int ww = 1; ww < 4; ++ww) acc += red[(ww * 2 * 16 + ri) * RR + ci];
     dst[i] = acc;
   }
 }
