@@ -350,13 +350,13 @@ __device__ __forceinline__ int unit_offset(const LProb &P, const LTile &t,
 // Global element offsets g[j] and LDS element offsets la[j] (layout row
 // stride RS) of a lane's NU staging units u0 + j nthr + tid, j < NU (u0 a
 // multiple of NU nthr, nthr of OCT): layout row kk_j = (u0 + tid) / OCT +
-// j nthr / OCT, unit o = tid % OCT.  Rank 1, and rank 2 when a step of
-// nthr / OCT layout rows is a whole number of box rows, step the box row
-// (two adds, a min and a 24-bit product per unit); otherwise unit_offset
-// per unit.  Units past the layout take its last row (the lane's unit of
+// j nthr / OCT, unit o = tid % OCT.  Rank 1, and rank 2 (or rank 3 staging
+// one layer per slab) when a step of nthr / OCT layout rows is a whole
+// number of box rows, step the box row (two adds, a min and a 24-bit
+// product per unit); otherwise unit_offset per unit.  Units past the layout take its last row (the lane's unit of
 // it): real rows, staged again with the same values, and every row's OCT
 // units are held by OCT consecutive lanes.
-template <int R, int OCT, int RS, int NU = 4>
+template <int R, int OCT, int RS, int NU = 4, bool LAYER3 = true>
 __device__ __forceinline__ void unit_walk(const LProb &P, const LTile &t,
                                           int u0, int tid, int nthr, int s0,
                                           int (&g)[NU], int (&la)[NU]) {
@@ -373,10 +373,13 @@ __device__ __forceinline__ void unit_walk(const LProb &P, const LTile &t,
     }
     return;
   }
-  if (R == 2 && (step & (P2 - 1)) == 0) {
+  // rank 2, and rank 3 staged one box layer (axis 0 = s0) per slab: step
+  // box rows of the layer
+  if ((R == 2 || (R == 3 && LAYER3 && P.sl == 1)) && (step & (P2 - 1)) == 0) {
     const int e2 = kk0 & (P2 - 1);
     const int row0 = kk0 >> P.lgP2, drow = step >> P.lgP2;
-    const int base = t.kbase + 8 * o + __umul24((unsigned)min(e2, t.E[2] - 1), (unsigned)t.SK[2]);
+    int base = t.kbase + 8 * o + __umul24((unsigned)min(e2, t.E[2] - 1), (unsigned)t.SK[2]);
+    if (R == 3) base += __umul24((unsigned)min(s0, t.E[0] - 1), (unsigned)t.SK[0]);
     const int Em1 = P.ax[1].Em;
 #pragma unroll
     for (int j = 0; j < NU; ++j) {

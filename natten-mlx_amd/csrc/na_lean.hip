@@ -369,7 +369,7 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
     v8 qr[NU], dr[NU], orr[NU];
     float lr[NU], dl[NU];
     int g[NU], la[NU];
-    unit_walk<R, OCT, RSE, NU>(P, t, u0, tid, nthr, s0, g, la);
+    unit_walk<R, OCT, RSE, NU, false>(P, t, u0, tid, nthr, s0, g, la);
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
       const int row = (g[j] - 8 * o) / D;
