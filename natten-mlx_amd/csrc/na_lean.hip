@@ -442,14 +442,16 @@ __device__ __forceinline__ int lane_rows(const LProb &P, const LTile &t,
 // Rows of chunk pair (a, b) of a wave's sub-box: first LDS row, row test
 // and column segment of each (padding chunks: row 0 of the sub-box, masked).
 // Closed forms where the walk is one box row (rank 1: chunk c is columns
-// 16 c..) or one chunk per row (rank 2, CPR1: chunk c is row ws1 + c);
-// otherwise the cursor walks rows and segments.
+// 16 c..) or one chunk per row (rank 2, CPR1: chunk c is row ws1 + c; rank
+// 3, CPR1, a slab of one layer a0: the same on that layer, whose row test
+// l0ok is the caller's); otherwise the cursor walks rows and segments.
 template <int R, bool CPR1>
 __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
                                           int nch, int s0, int Em1, int lgP2,
                                           int key0,
                                           const int wl[3], const int ww[3],
-                                          int kb[2], bool rok[2], int cs[2]) {
+                                          int kb[2], bool rok[2], int cs[2],
+                                          bool layer = false, bool l0ok = false) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c = c0 + h;
@@ -458,10 +460,10 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
       kb[h] = key0 + (real ? 16 * c : 0);
       cs[h] = c;
       rok[h] = real;
-    } else if (R == 2 && CPR1) {
+    } else if ((R == 2 || layer) && CPR1) {
       kb[h] = key0 + (real ? c << lgP2 : 0);
       cs[h] = 0;
-      rok[h] = real && (unsigned)(ws.ws[1] + c - wl[1]) < (unsigned)ww[1];
+      rok[h] = real && (unsigned)(ws.ws[1] + c - wl[1]) < (unsigned)ww[1] && (R == 2 || l0ok);
     } else {
       kb[h] = real ? (((cc.e0 - s0) * Em1 + cc.e1) << lgP2) + ws.ws[2] + 16 * cc.cs : key0;
       cs[h] = cc.cs;
@@ -625,11 +627,15 @@ __global__ void __launch_bounds__(512)
       const int nchb = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
       const int nch = nchb + (si == nsl - 1 ? nxc : 0);
       const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+      // a slab of one layer (rank 3): its chunks are the rows of layer a0
+      const bool layer = R == 3 && P.sl == 1;
+      const bool l0ok = (unsigned)(a0 - wl[0]) < (unsigned)ww[0];
       Cursor cc{a0, ws.ws[1], 0};
       for (int c0 = 0; c0 < nch; c0 += 2) {
         int kb[2], cs[2];
         bool rok[2];
-        pair_rows<R, CPR1>(ws, cc, c0, nchb, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+        pair_rows<R, CPR1>(ws, cc, c0, nchb, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs,
+                           layer, l0ok);
         bool ext[2] = {false, false};
         if (VX) {
 #pragma unroll
@@ -776,11 +782,14 @@ __global__ void __launch_bounds__(512)
     const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
     const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
     const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
+    const bool layer = R == 3 && P.sl == 1;
+    const bool l0ok = (unsigned)(a0 - wl[0]) < (unsigned)ww[0];
     Cursor cc{a0, ws.ws[1], 0};
     for (int c0 = 0; c0 < nch; c0 += 2) {
       int kb[2], cs[2];
       bool rok[2];
-      pair_rows<R, CPR1>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs);
+      pair_rows<R, CPR1>(ws, cc, c0, nch, s0, Em1, P.lgP2, key0, wl, ww, kb, rok, cs,
+                         layer, l0ok);
       v8 qr[2][NT], orr[2][NT];
       float ls2[2][4];
 #pragma unroll
