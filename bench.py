@@ -155,6 +155,20 @@ def call_timing(fn, reps: int = 20) -> dict:
             "flushed_ms": cold["median"]}
 
 
+def eager_call_ms(fn, reps: int = 20) -> float:
+    """Device time (ms) of one call of ``fn`` run eagerly: the protocol's
+    median trial of ``reps`` back-to-back calls between two events, over
+    ``reps``."""
+    def many():
+        for _ in range(reps):
+            fn()
+    return protocol_ms(many)["median"] / reps
+
+
+def _progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _as_list(x):
     return list(x) if isinstance(x, (tuple, list)) else [x]
 
@@ -789,8 +803,94 @@ def wl_merge(args):
                  cfg, rf if rf["call_ms"] >= rb["call_ms"] else rb, cpu, {"sweep": table})
 
 
+def _roof_mfma(call, flops, nbytes, timing):
+    """Roofline of a matrix-core-bound call: TFLOP/s against the bf16 peak."""
+    ms = timing["warm_ms"]
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 5), "traffic": None,
+            "call": call, "call_ms": round(ms, 5), "algorithmic_bytes": nbytes, "flops": flops,
+            "single_call_ms": round(timing["single_ms"], 5),
+            "mall_flushed": {"call_ms": round(timing["flushed_ms"], 5)}}
+
+
+def wl_fmha(args):
+    """Dense (FMHA) mode: na1d with kernel_size equal to the extent, the
+    reference's dense-attention route (``functional.py:141-187``), bf16
+    [4,4096,16,64] forward + backward through the public API; torch's own
+    SDPA on the same tensors is timed beside it for comparison."""
+    import natten_amd
+    from natten_amd._core import hip
+    from oracle import na as O
+
+    Bc, L, H, Dc = 4, 4096, 16, 64
+    shape = (Bc, L, H, Dc)
+    q, k, v, do = (_gen(shape, torch.bfloat16, s) for s in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        out = natten_amd.na1d(q, k, v, L)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    _progress("fmha: step timing")
+    step_ms, stt = _step_ms(step, args)
+    _progress("fmha: call timing")
+    a = ((L,), (1,), (1,), (False,), None)
+    qd, kd, vd = q.detach(), k.detach(), v.detach()
+    out, lse = hip.fused_forward(qd, kd, vd, *a, dense=True)
+    tf = call_timing(lambda: hip.fused_forward(qd, kd, vd, *a, dense=True))
+    tb = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, *a, dense=True))
+    pairs = Bc * H * L * L
+    fwd_f, bwd_f = 4 * Dc * pairs, 8 * Dc * pairs
+    tb_ = Bc * L * H * Dc * 2
+    rf = _roof_mfma("na_fwd", fwd_f, 4 * tb_ + Bc * L * H * 4, tf)
+    rb = _roof_mfma("na_bwd", bwd_f, 8 * tb_ + Bc * L * H * 4, tb)
+    # torch's scaled_dot_product_attention on [B, H, L, D] copies of the
+    # inputs, timed eagerly (no graph capture: its backward runs on the
+    # stream of its forward)
+    _progress("fmha: torch sdpa")
+    qt, kt, vt, dot = (x.detach().transpose(1, 2).contiguous() for x in (q, k, v, do))
+    F_ = torch.nn.functional
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (qt, kt, vt))
+    og = F_.scaled_dot_product_attention(qg, kg, vg)
+    sdpa = {"fwd_call_ms": round(eager_call_ms(
+                lambda: F_.scaled_dot_product_attention(qt, kt, vt)), 5),
+            "bwd_call_ms": round(eager_call_ms(
+                lambda: torch.autograd.grad(og, (qg, kg, vg), dot, retain_graph=True)), 5),
+            "timing": "eager, median of the protocol's trials of 20 back-to-back calls"}
+    _progress("fmha: cpu baseline")
+    cpu = None
+    if not args.no_cpu:
+        sc = Dc ** -0.5
+        qc, kc, vc, doc = (x.detach()[:1, :, :1].cpu() for x in (q, k, v, do))
+
+        def once():
+            xs = [t.clone().requires_grad_(True) for t in (qc, kc, vc)]
+            o = O.dense_attention(*xs, sc, compute_dtype=torch.bfloat16)
+            torch.autograd.grad(o, xs, doc)
+
+        med, runs, wall, thr = cpu_median(once, 10.0)
+        per_step = med * Bc * H
+        cpu = _cpu_line((fwd_f + bwd_f) / per_step / 1e12, "TFLOP/s", thr,
+                        f"oracle dense attention fwd+bwd (softmax(q k^T) v, autograd) in bf16 "
+                        f"on 1 of the {Bc * H} (sample, head) pairs, scaled x{Bc * H}",
+                        runs, wall, per_step)
+    cfg = {"workload": "na1d fused fwd+bwd, kernel_size = extent (dense / FMHA mode), bf16 "
+                       "[4,4096,16,64]", "global_batch": Bc}
+    return _line("na1d dense (FMHA) 4096 bf16 fwd+bwd TFLOP/s, 1 MI355X",
+                 (fwd_f + bwd_f) / (step_ms * 1e-3) / 1e12, "TFLOP/s", step_ms, "bf16", cfg,
+                 rb if tb["warm_ms"] >= tf["warm_ms"] else rf, cpu,
+                 {"timing": dict(stt, fwd_call_ms=round(tf["warm_ms"], 5),
+                                 bwd_call_ms=round(tb["warm_ms"], 5)),
+                  "calls": {"fwd": rf, "bwd": rb}, "torch_sdpa": sdpa,
+                  "note": "flops count the algorithmic products (forward 4 D, backward 8 D "
+                          "per (query, key) pair); the backward's recomputation of the "
+                          "scores is not counted"})
+
+
 WORKLOADS = {"cfg1": wl_cfg1, "split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg4,
-             "cfg5": wl_cfg5, "merge": wl_merge}
+             "cfg5": wl_cfg5, "merge": wl_merge, "fmha": wl_fmha}
 
 
 # ---------------------------------------------------------------------------
