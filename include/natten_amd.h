@@ -137,7 +137,8 @@ int na_mfma_selftest(int32_t dtype, float *out, void *stream);
 enum na_kernel_path_t {
   NA_PATH_GENERIC = 0, /* vector-ALU kernels: every dtype / head_dim / stride */
   NA_PATH_MFMA = 1,    /* 32-query matrix-core kernels */
-  NA_PATH_LEAN = 2     /* workgroup-staged 16x16x32 matrix-core kernels */
+  NA_PATH_LEAN = 2,    /* workgroup-staged 16x16x32 matrix-core kernels */
+  NA_PATH_DENSE = 3    /* dense (FMHA) forward: key tiles streamed through LDS */
 };
 int na_kernel_path(const na_params *p, int32_t backward);
 

@@ -59,6 +59,7 @@ def sources() -> list[str]:
 EXTRA_FLAGS = {
     "na_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "na_lean.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "na_dense.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -118,6 +118,10 @@ bool use_mfma(const na_params *p, const na::Prob &P) {
   return (p->flags & NA_FLAG_GENERIC) == 0 && na::mfma_eligible(P, p->dtype);
 }
 
+bool use_dense(const na_params *p, const na::Prob &P) {
+  return (p->flags & NA_FLAG_GENERIC) == 0 && na::dense_fwd_eligible(P, p->dtype);
+}
+
 bool use_lean(const na_params *p, const na::Prob &P) {
   return (p->flags & (NA_FLAG_GENERIC | NA_FLAG_NO_LEAN)) == 0 &&
          na::lean_eligible(P, p->dtype);
@@ -350,6 +354,7 @@ int na_kernel_path(const na_params *p, int32_t backward) {
     return NA_PATH_GENERIC;
   }
   if (backward ? use_lean_bwd(p, P) : use_lean(p, P)) return NA_PATH_LEAN;
+  if (!backward && use_dense(p, P)) return NA_PATH_DENSE;
   if (use_mfma(p, P)) return NA_PATH_MFMA;
   return NA_PATH_GENERIC;
 }
@@ -363,7 +368,10 @@ int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan) {
   if (rc != NA_OK) return rc;
   *plan = na_plan{};
   const bool lean = backward ? use_lean_bwd(p, P) : use_lean(p, P);
-  plan->path = lean ? NA_PATH_LEAN : use_mfma(p, P) ? NA_PATH_MFMA : NA_PATH_GENERIC;
+  plan->path = lean                         ? NA_PATH_LEAN
+               : !backward && use_dense(p, P) ? NA_PATH_DENSE
+               : use_mfma(p, P)               ? NA_PATH_MFMA
+                                              : NA_PATH_GENERIC;
   if (lean) {
     na::LeanPlanInfo L{};
     if (na::lean_plan(P, p->dtype, backward != 0, &L)) {
@@ -411,6 +419,9 @@ int na_fwd(const na_params *p, const void *q, const void *k, const void *v,
   if (use_lean(p, P))
     na::lean_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
                  as_stream(stream));
+  else if (use_dense(p, P))
+    na::dense_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
+                  as_stream(stream));
   else if (use_mfma(p, P))
     na::mfma_fwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse,
                  as_stream(stream));

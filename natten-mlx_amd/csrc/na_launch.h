@@ -54,6 +54,13 @@ void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
 
 // Matrix-core kernels (na_mfma.hip): bf16/fp16, head_dim 32/64/128,
 // stride 1, odd kernel size on every non-causal axis.
+// Dense (FMHA) forward: bf16 / fp16, head_dim 32 / 64 / 128, no per-sample
+// extents (na_dense.hip).
+bool dense_fwd_eligible(const Prob &P, int dtype);
+void dense_fwd(const Prob &P, int dtype, const void *q, const void *k,
+               const void *v, const void *ek, const void *ev, void *out,
+               float *lse, hipStream_t st);
+
 bool mfma_eligible(const Prob &P, int dtype);
 void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev, void *out,

@@ -151,7 +151,7 @@ def fused_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale,
     return out, lse
 
 
-KERNEL_PATHS = {0: "generic", 1: "mfma", 2: "lean"}
+KERNEL_PATHS = {0: "generic", 1: "mfma", 2: "lean", 3: "dense"}
 
 
 def kernel_path(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_extra=0,
