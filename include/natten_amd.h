@@ -138,7 +138,8 @@ enum na_kernel_path_t {
   NA_PATH_GENERIC = 0, /* vector-ALU kernels: every dtype / head_dim / stride */
   NA_PATH_MFMA = 1,    /* 32-query matrix-core kernels */
   NA_PATH_LEAN = 2,    /* workgroup-staged 16x16x32 matrix-core kernels */
-  NA_PATH_DENSE = 3    /* dense (FMHA) forward: key tiles streamed through LDS */
+  NA_PATH_DENSE = 3    /* dense (FMHA) kernels: key or query tiles streamed
+                          through LDS */
 };
 int na_kernel_path(const na_params *p, int32_t backward);
 
@@ -160,7 +161,9 @@ typedef struct na_plan {
   int32_t workgroups;      /* workgroups launched */
   int32_t lds_bytes;       /* LDS per workgroup */
   int32_t extra_reduction; /* backward with additional tokens: their
-                              gradients on 1 = vector ALU, 2 = matrix cores */
+                              gradients on 1 = vector ALU, 2 = matrix cores
+                              (0 on the dense path: they are keys of its
+                              key-side kernel) */
 } na_plan;
 int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan);
 

@@ -152,7 +152,7 @@ size_t delta_bytes(const na::Prob &P) {
 // (rowsum(dO * O) - dlse per query and head) where a kernel reads them, then
 // the additional tokens' gradient partials.  Sized as if the extra-token
 // gradients are requested (the workspace query sees no pointers).
-enum BwdPath { kBwdLean, kBwdMfma, kBwdGeneric };
+enum BwdPath { kBwdLean, kBwdDense, kBwdMfma, kBwdGeneric };
 struct BwdPlan {
   BwdPath path;
   bool matrix;       // the extra-token reduction may use matrix cores
@@ -169,6 +169,13 @@ BwdPlan bwd_plan(const na_params *p, const na::Prob &P) {
     b.path = kBwdLean;
     b.xdelta = extra && na::dextra_fuses_delta(P, p->dtype, b.matrix);
     b.need_delta = extra && !b.xdelta;
+  } else if (use_dense(p, P)) {
+    // the additional tokens are keys of the dense kernels: no reduction pass
+    b.path = kBwdDense;
+    b.need_delta = true;
+    b.delta = delta_bytes(P);
+    b.total = b.delta;
+    return b;
   } else if (use_mfma(p, P)) {
     b.path = kBwdMfma;
     b.need_delta = extra || na::mfma_bwd_reads_delta(P);
@@ -354,7 +361,7 @@ int na_kernel_path(const na_params *p, int32_t backward) {
     return NA_PATH_GENERIC;
   }
   if (backward ? use_lean_bwd(p, P) : use_lean(p, P)) return NA_PATH_LEAN;
-  if (!backward && use_dense(p, P)) return NA_PATH_DENSE;
+  if (use_dense(p, P)) return NA_PATH_DENSE;
   if (use_mfma(p, P)) return NA_PATH_MFMA;
   return NA_PATH_GENERIC;
 }
@@ -369,7 +376,7 @@ int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan) {
   *plan = na_plan{};
   const bool lean = backward ? use_lean_bwd(p, P) : use_lean(p, P);
   plan->path = lean                         ? NA_PATH_LEAN
-               : !backward && use_dense(p, P) ? NA_PATH_DENSE
+               : use_dense(p, P)              ? NA_PATH_DENSE
                : use_mfma(p, P)               ? NA_PATH_MFMA
                                               : NA_PATH_GENERIC;
   if (lean) {
@@ -386,7 +393,7 @@ int na_kernel_plan(const na_params *p, int32_t backward, na_plan *plan) {
       plan->lds_bytes = L.lds;
     }
   }
-  if (backward && P.n_extra > 0)
+  if (backward && P.n_extra > 0 && plan->path != NA_PATH_DENSE)
     plan->extra_reduction =
         na::dextra_uses_matrix(P, p->dtype, (p->flags & NA_FLAG_GENERIC) == 0) ? 2 : 1;
   g_error.clear();
@@ -470,6 +477,11 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
     if (dextra && !plan.xdelta) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::lean_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
                  dq, dk, dv, st);
+  } else if (plan.path == kBwdDense) {
+    na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
+    na::dense_bwd(P, p->dtype, q, k, v, extra_k, extra_v, dout, lse, delta, dq, dk, dv,
+                  dextra ? d_extra_k : nullptr, dextra ? d_extra_v : nullptr, st);
+    return launch_status("na_bwd");
   } else if (plan.path == kBwdMfma) {
     if (dextra || na::mfma_bwd_reads_delta(P))
       na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);

@@ -60,6 +60,13 @@ bool dense_fwd_eligible(const Prob &P, int dtype);
 void dense_fwd(const Prob &P, int dtype, const void *q, const void *k,
                const void *v, const void *ek, const void *ev, void *out,
                float *lse, hipStream_t st);
+// Dense backward (same problems): k_ddkv (dk, dv and, when dek / dev are
+// non-null, the additional tokens' gradients) and k_ddq (dq); delta rows
+// (rowsum(dO * O) - dLSE) from the delta pass.
+void dense_bwd(const Prob &P, int dtype, const void *q, const void *k,
+               const void *v, const void *ek, const void *ev, const void *dout,
+               const float *lse, const float *delta, void *dq, void *dk, void *dv,
+               void *dek, void *dev, hipStream_t st);
 
 bool mfma_eligible(const Prob &P, int dtype);
 void mfma_fwd(const Prob &P, int dtype, const void *q, const void *k,

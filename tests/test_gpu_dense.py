@@ -49,7 +49,7 @@ def _run(q, k, v, go, gl, ek=None, ev=None):
     assert hip.kernel_path(qd, kd, *a, n_extra=nx, dense=True) == (
         "dense" if lowp else "generic")
     assert hip.kernel_path(qd, kd, *a, n_extra=nx, dense=True, backward=True) == (
-        "mfma" if lowp else "generic")
+        "dense" if lowp else "generic")
     out, lse = hip.fused_forward(qd, kd, vd, *a, extra_k=ekd, extra_v=evd, dense=True)
     dq, dk, dv, dek, dev = hip.fused_backward(qd, kd, vd, out, lse, god, gld, *a,
                                               extra_k=ekd, extra_v=evd, dense=True)
