@@ -955,6 +955,18 @@ def profile_calls(n: int, workload: str = "cfg2") -> None:
         print(f"profile-calls: {n} x merge forward and backward (2 parts, config-3 size) done",
               flush=True)
         return
+    if workload == "fmha":
+        L = 4096
+        q, k, v, do = (_gen((4, L, 16, 64), torch.bfloat16, s) for s in range(4))
+        a = ((L,), (1,), (1,), (False,), None)
+        out, lse = hip.fused_forward(q, k, v, *a, dense=True)
+        for _ in range(n):
+            hip.fused_forward(q, k, v, *a, dense=True)
+            hip.fused_backward(q, k, v, out, lse, do, None, *a, dense=True)
+        torch.cuda.synchronize()
+        print(f"profile-calls: {n} x dense [4,4096,16,64] forward and backward done",
+              flush=True)
+        return
     if workload == "cfg3":
         shape = (1, 16, 32, 32, 8, 64)
         q, k, v, do = (_gen(shape, torch.bfloat16, s) for s in range(4))
@@ -986,7 +998,7 @@ def main(argv=None):
     ap.add_argument("--profile-calls", type=int, default=0, metavar="N",
                     help="only run N calls of each library entry point of --workload "
                          "(cfg2 / cfg3: fused forward and backward with a calibration copy; "
-                         "split; cfg4; cfg5; merge) for rocprofv3 passes, then exit")
+                         "split; cfg4; cfg5; merge; fmha) for rocprofv3 passes, then exit")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
                     help="cfg2 (default) is the driver's bench line; the others measure the "
                          "remaining BASELINE.json configurations")

@@ -123,10 +123,13 @@ __global__ void __launch_bounds__(kDThreads)
   store_tile(buf0);
   __syncthreads();
   const int nkt = (P.Lk + kDTileKeys - 1) / kDTileKeys;
-  for (int j = 0; j < nkt; ++j) {
+  // One 64-key tile.  Only the last tile can hold keys past the sample's
+  // last token: its scores start at 0 or -inf per key, every other tile's
+  // at zero (the MFMA's zero accumulator operand, no per-element setup).
+  auto run_tile = [&](const int j, auto last_tile) {
+    constexpr bool LAST = decltype(last_tile)::value;
     const int t0 = j * kDTileKeys;
-    const bool more = j + 1 < nkt;
-    if (more) load_tile(t0 + kDTileKeys);  // in flight during this tile
+    if (!LAST) load_tile(t0 + kDTileKeys);  // in flight during this tile
     const E *ks = buf0 + (j & 1) * (kDTileKeys * RSE);
     const E *vs = ks + lds_y(D);
     v8 ka[4][NT];
@@ -135,13 +138,12 @@ __global__ void __launch_bounds__(kDThreads)
 #pragma unroll
       for (int st = 0; st < NT; ++st)
         ka[ch][st] = *reinterpret_cast<const v8 *>(ks + 16 * ch * RSE + ka_off + 32 * st);
-    // keys past the sample's last token (last tile only): -inf scores
     float cb[4][4];
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        cb[ch][r] = t0 + 16 * ch + 4 * gq + r < P.Lk ? 0.f : -INFINITY;
+        cb[ch][r] = !LAST || t0 + 16 * ch + 4 * gq + r < P.Lk ? 0.f : -INFINITY;
     v8 bp[NQ][2];
 #pragma unroll
     for (int qi = 0; qi < NQ; ++qi) {
@@ -196,9 +198,11 @@ __global__ void __launch_bounds__(kDThreads)
 #pragma unroll
       for (int qi = 0; qi < NQ; ++qi) lacc[qi] = M::mma(ones, bp[qi][jj], lacc[qi]);
     }
-    if (more) store_tile(buf0 + ((j + 1) & 1) * (kDTileKeys * RSE));
+    if (!LAST) store_tile(buf0 + ((j + 1) & 1) * (kDTileKeys * RSE));
     __syncthreads();
-  }
+  };
+  for (int j = 0; j + 1 < nkt; ++j) run_tile(j, std::false_type{});
+  run_tile(nkt - 1, std::true_type{});
 
   // ---- epilogue: l over the query's 4 lanes, normalise, store ----
 #pragma unroll
