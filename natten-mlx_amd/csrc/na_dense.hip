@@ -507,10 +507,12 @@ __global__ void __launch_bounds__(kDThreads)
   store_tile(0);
   __syncthreads();
   const int nkt = (P.Lk + kDTileKeys - 1) / kDTileKeys;
-  for (int j = 0; j < nkt; ++j) {
+  // only the last tile can hold keys past the sample's last token (scores
+  // start at -inf there); every other tile's scores start at zero
+  auto run_tile = [&](const int j, auto last_tile) {
+    constexpr bool LAST = decltype(last_tile)::value;
     const int t0 = j * kDTileKeys;
-    const bool more = j + 1 < nkt;
-    if (more) load_tile(t0 + kDTileKeys);
+    if (!LAST) load_tile(t0 + kDTileKeys);
     const E *ks = buf0 + (j & 1) * TILE;
     const E *vs = ks + lds_y(D);
 #pragma unroll
@@ -527,7 +529,7 @@ __global__ void __launch_bounds__(kDThreads)
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          cb[hh][r] = t0 + 32 * cp + 16 * hh + 4 * gq + r < P.Lk ? 0.f : -INFINITY;
+          cb[hh][r] = !LAST || t0 + 32 * cp + 16 * hh + 4 * gq + r < P.Lk ? 0.f : -INFINITY;
       }
       // K^T operand (dims x 32 keys), shared by the sub-tiles
       v8 kt[NDB];
@@ -565,9 +567,11 @@ __global__ void __launch_bounds__(kDThreads)
         for (int db = 0; db < NDB; ++db) acc[qi][db] = M::mma(kt[db], bs, acc[qi][db]);
       }
     }
-    if (more) store_tile((j + 1) & 1);
+    if (!LAST) store_tile((j + 1) & 1);
     __syncthreads();
-  }
+  };
+  for (int j = 0; j + 1 < nkt; ++j) run_tile(j, std::false_type{});
+  run_tile(nkt - 1, std::true_type{});
 
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
