@@ -598,7 +598,7 @@ constexpr int dense_nk() {
 }
 template <int D>
 constexpr int dense_nq_bwd() {
-  return D == 128 ? 2 : 4;
+  return D == 128 ? 1 : 4;  // head_dim 128: 208 VGPRs, two waves per SIMD
 }
 
 DProb make_dprob(const Prob &P, int nq) {
