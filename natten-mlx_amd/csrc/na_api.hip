@@ -156,8 +156,8 @@ enum BwdPath { kBwdLean, kBwdDense, kBwdMfma, kBwdGeneric };
 struct BwdPlan {
   BwdPath path;
   bool matrix;       // the extra-token reduction may use matrix cores
-  bool xdelta;       // that reduction forms delta itself (lean path)
-  bool need_delta;   // a delta pass runs and its rows live in the workspace
+  bool need_delta;   // delta rows live in the workspace (written by a delta
+                     // pass, or by the lean backward for the reduction)
   size_t delta, total;  // bytes: delta rows, whole workspace
 };
 
@@ -167,8 +167,7 @@ BwdPlan bwd_plan(const na_params *p, const na::Prob &P) {
   const bool extra = P.n_extra > 0;
   if (use_lean_bwd(p, P)) {
     b.path = kBwdLean;
-    b.xdelta = extra && na::dextra_fuses_delta(P, p->dtype, b.matrix);
-    b.need_delta = extra && !b.xdelta;
+    b.need_delta = extra;
   } else if (use_dense(p, P)) {
     // the additional tokens are keys of the dense kernels: no reduction pass
     b.path = kBwdDense;
@@ -471,12 +470,11 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
   const hipStream_t st = as_stream(stream);
   const bool dextra =
       P.n_extra > 0 && d_extra_k != nullptr && d_extra_v != nullptr;
-  // the lean backward computes delta inside; the matrix-core extra-token
-  // reduction can too (from O and dO), else it reads a delta pass
+  // the lean backward computes delta inside, and writes its rows for the
+  // extra-token reduction that follows it
   if (plan.path == kBwdLean) {
-    if (dextra && !plan.xdelta) na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::lean_bwd(P, p->dtype, q, k, v, extra_k, extra_v, out, lse, dout, dlse,
-                 dq, dk, dv, st);
+                 dq, dk, dv, dextra ? delta : nullptr, st);
   } else if (plan.path == kBwdDense) {
     na::valu_delta(P, p->dtype, out, dout, dlse, delta, st);
     na::dense_bwd(P, p->dtype, q, k, v, extra_k, extra_v, dout, lse, delta, dq, dk, dv,
@@ -492,9 +490,8 @@ int na_bwd(const na_params *p, const void *q, const void *k, const void *v,
                  dq, dk, dv, delta, st);
   }
   if (dextra)
-    na::dextra(P, p->dtype, q, extra_k, extra_v, lse,
-               plan.path == kBwdLean && plan.xdelta ? nullptr : delta, dout, out, dlse,
-               d_extra_k, d_extra_v, xpart, plan.matrix, st);
+    na::dextra(P, p->dtype, q, extra_k, extra_v, lse, delta, dout, d_extra_k,
+               d_extra_v, xpart, plan.matrix, st);
   return launch_status("na_bwd");
 }
 

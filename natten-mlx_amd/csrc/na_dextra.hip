@@ -317,14 +317,13 @@ struct XDiv {
   FastDiv rep, o12, o2;
 };
 
-// delta == nullptr: delta of each row is computed here, rowsum(dO * O) -
-// dlse, from the O row loaded beside the dO row.
+// delta: rowsum(dO * O) - dlse per row, written by the backward kernel that
+// runs before this one (or a delta pass).
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     k_xmfma(Prob P, const T *__restrict__ q, const T *__restrict__ ek,
             const T *__restrict__ ev, const float *__restrict__ lse,
             const float *__restrict__ delta, const T *__restrict__ dout,
-            const T *__restrict__ out, const float *__restrict__ dlse,
             float *__restrict__ part, int ntt, int nsg, int nper, int64_t nrows,
             XDiv xd) {
   typedef L16<T> M;
@@ -373,15 +372,14 @@ __global__ void __launch_bounds__(256)
   const int tr_off = (4 * g + (n >> 2)) * RS + 4 * (n & 3);
 
   // One step's rows: lanes 0..31 decode the wave's 32 rows (q / dO
-  // offsets, lse * log2(e): +inf outside the sample, P = 0; delta or -dlse
-  // when it is computed here), then the 16-byte units u = lane + 64 j of
-  // the q, dO (and O) rows are loaded.  Steps are software-pipelined: the
-  // next step's loads are issued before this step's matrix work.
-  const bool fuse = delta == nullptr;
+  // offsets, lse * log2(e): +inf outside the sample, P = 0; delta), then
+  // the 16-byte units u = lane + 64 j of the q and dO rows are loaded.
+  // Steps are software-pipelined: the next step's loads are issued before
+  // this step's matrix work.
   struct Step {
     int32_t qo, dof;  // element offsets (tensors below 2^31 elements)
     float l2, dl;
-    v8 xq[UPL], xd[UPL], xo[UPL];
+    v8 xq[UPL], xd[UPL];
   };
   auto fetch = [&](int ci, Step &st) -> bool {
     const int64_t r0 = ((int64_t)sg * nper + ci) * kXMRows + 32 * w;
@@ -408,7 +406,7 @@ __global__ void __launch_bounds__(256)
         st.qo = (int32_t)((qt * P.H + h) * D);
         st.dof = (int32_t)((ot * P.H + h) * D);
         st.l2 = lse[ot * P.H + h] * kLog2e;
-        st.dl = !fuse ? delta[ot * P.H + h] : (dlse != nullptr ? -dlse[ot * P.H + h] : 0.f);
+        st.dl = delta[ot * P.H + h];
       }
     }
 #pragma unroll
@@ -417,7 +415,6 @@ __global__ void __launch_bounds__(256)
       const int32_t a = __shfl(st.qo, row), c = __shfl(st.dof, row);
       st.xq[j] = a >= 0 ? ld8(q, a + 8 * c8) : zero;
       st.xd[j] = c >= 0 ? ld8(dout, c + 8 * c8) : zero;
-      if (fuse) st.xo[j] = c >= 0 ? ld8(out, c + 8 * c8) : zero;
     }
     return true;
   };
@@ -425,28 +422,7 @@ __global__ void __launch_bounds__(256)
   Step cur;
   bool have = fetch(0, cur);
   for (int ci = 0; have; ++ci) {
-    float dl = cur.dl;
-    if (fuse) {
-      // rowsum(dO * O): unit j's partial dot, summed over the C8 lanes that
-      // hold its row; lane L < 32 then takes row L's sum (unit L C8 / 64,
-      // lane L C8 % 64).  Rows outside the sample: dO = 0, sum 0, dl 0.
-      float rs[UPL];
-#pragma unroll
-      for (int j = 0; j < UPL; ++j) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf((float)cur.xd[j][e], (float)cur.xo[j][e], acc);
-        rs[j] = group_sum(acc, C8);
-      }
-      const int src = lane * C8;
-      float sum = 0.f;
-#pragma unroll
-      for (int j = 0; j < UPL; ++j) {
-        const float x = __shfl(rs[j], src & 63);
-        if ((src >> 6) == j) sum = x;
-      }
-      dl += sum;
-    }
+    const float dl = cur.dl;
     const float l2 = cur.l2;
     wave_lds_sync();  // the previous step's reads of the slice are done
 #pragma unroll
@@ -530,10 +506,6 @@ bool xmfma_ok(const Prob &P, int dtype) {
 
 }  // namespace
 
-bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix) {
-  return matrix && xmfma_ok(P, dtype);
-}
-
 bool dextra_uses_matrix(const Prob &P, int dtype, bool matrix) {
   return matrix && xmfma_ok(P, dtype);
 }
@@ -566,8 +538,8 @@ size_t dextra_workspace_bytes(const Prob &P) {
 
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, const void *out, const float *dlse, void *dek,
-            void *dev, float *part, bool matrix, hipStream_t st) {
+            const void *dout, void *dek, void *dev, float *part, bool matrix,
+            hipStream_t st) {
   if (P.n_extra <= 0 || P.B == 0) return;
   if (matrix && xmfma_ok(P, dtype)) {
     const XPlan x = xplan_mfma(P);
@@ -581,8 +553,7 @@ void dextra(const Prob &P, int dtype, const void *q, const void *ek,
 #define XM_(TT, DD)                                                              \
   hipLaunchKernelGGL((k_xmfma<TT, DD>), dim3(g1), dim3(256), lds, st, P,         \
                      (const TT *)q, (const TT *)ek, (const TT *)ev, lse, delta,  \
-                     (const TT *)dout, (const TT *)out, dlse, part, x.ntt,       \
-                     x.nsg, x.nper, x.nrows, xd)
+                     (const TT *)dout, part, x.ntt, x.nsg, x.nper, x.nrows, xd)
 #define XMD_(TT)          \
   do {                    \
     if (P.D == 32)        \

@@ -100,13 +100,14 @@ bool lean_plan(const Prob &P, int dtype, bool backward, LeanPlanInfo *o);
 // Lean fused backward: one launch, no workspace (delta is computed in the
 // kernel); dlse may be null.  Per-sample extents and additional tokens as
 // in lean_fwd (ek / ev: their contribution to dq; their own gradients come
-// from dextra).
+// from dextra).  delta_out (nullable; with additional tokens only): the
+// kernel also writes each query row's delta there, for dextra.
 bool lean_bwd_eligible(const Prob &P, int dtype);
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev,
               const void *out, const float *lse,
               const void *dout, const float *dlse, void *dq, void *dk,
-              void *dv, hipStream_t st);
+              void *dv, float *delta_out, hipStream_t st);
 
 // Lean split ops (na_lsplit.hip): the lean problem class without varlen,
 // additional tokens or dense mode, where the compact rows fit LDS.
@@ -154,15 +155,12 @@ void valu_delta(const Prob &P, int dtype, const void *out, const void *dout,
 // dlse per (query, head)); `part` is a float workspace of
 // dextra_workspace_bytes(P); `matrix` allows the matrix-core variant
 // (bf16 / fp16, head_dim 32 / 64 / 128).
-// With delta == nullptr (only where dextra_fuses_delta) the matrix-core
-// variant computes delta from out, dout and dlse (nullable) itself.
 size_t dextra_workspace_bytes(const Prob &P);
-bool dextra_fuses_delta(const Prob &P, int dtype, bool matrix);
 // Whether dextra runs the matrix-core reduction (else the vector-ALU one).
 bool dextra_uses_matrix(const Prob &P, int dtype, bool matrix);
 void dextra(const Prob &P, int dtype, const void *q, const void *ek,
             const void *ev, const float *lse, const float *delta,
-            const void *dout, const void *out, const float *dlse, void *dek,
-            void *dev, float *part, bool matrix, hipStream_t st);
+            const void *dout, void *dek, void *dev, float *part, bool matrix,
+            hipStream_t st);
 
 }  // namespace na

@@ -491,7 +491,7 @@ __global__ void __launch_bounds__(512)
            const T *__restrict__ ev, const T *__restrict__ out,
            const float *__restrict__ lse, const T *__restrict__ dout,
            const float *__restrict__ dlse, T *__restrict__ dq,
-           T *__restrict__ dk, T *__restrict__ dv) {
+           T *__restrict__ dk, T *__restrict__ dv, float *__restrict__ dlt) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -715,6 +715,8 @@ __global__ void __launch_bounds__(512)
           for (int r = 0; r < 4; ++r) wv[r] = (E)(acc[db][r] * P.scale);
           *reinterpret_cast<v4 *>(dq + qoff + 16 * db + 4 * gq) = wv;
         }
+        // VX: the row's delta, for the additional tokens' gradient pass
+        if (VX && dlt != nullptr && gq == 0) dlt[qoff / D] = delta;
       }
     }
   }
@@ -990,7 +992,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
               const void *v, const void *ek, const void *ev,
               const void *out, const float *lse,
               const void *dout, const float *dlse, void *dq, void *dk,
-              void *dv, hipStream_t st) {
+              void *dv, float *delta_out, hipStream_t st) {
   const LChoice C = lean_choice(P, kLBwd);
   const LProb L = lean_bwd_lprob(P, C);
   if (L.n_tiles == 0) return;
@@ -1001,7 +1003,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
   hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV>), grid, block, lds, st, L,    \
                      (const TT *)q, (const TT *)k, (const TT *)v,              \
                      (const TT *)ek, (const TT *)ev, (const TT *)out, lse,     \
-                     (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv)
+                     (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out)
 #define LB_LAUNCH(TT, DD, RR, CC)                                             \
   do {                                                                        \
     if (vx) LB_LAUNCH1(TT, DD, RR, CC, true);                                 \
