@@ -294,13 +294,20 @@ __global__ void __launch_bounds__(kDThreads)
   const int nqt = (P.L + kDTileKeys - 1) / kDTileKeys;
   v8 pre[NU];
   float pre_l = 0.f, pre_d = 0.f;
-  auto load_tile = [&](int it) {
-    const int hr = it / nqt, t0 = (it - hr * nqt) * kDTileKeys;
+  // query tile (head hk rep + hr, rows t0 ..): unit i reads row t0 + r0 + RPP i
+  const int qstep = P.H * D;
+  auto load_tile = [&](int hr, int t0) {
     const int h = hk * rep + hr;
+    if (t0 + kDTileKeys <= P.L) {  // wave-uniform
+      const int o0 = ((b * P.L + t0 + r0) * P.H + h) * D + col;
 #pragma unroll
-    for (int i = 0; i < NU; ++i) {
-      const int qq = min(t0 + r0 + RPP * i, P.L - 1);
-      pre[i] = ld8(src, ((b * P.L + qq) * P.H + h) * D + col);
+      for (int i = 0; i < NU; ++i) pre[i] = ld8(src, o0 + RPP * i * qstep);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int qq = min(t0 + r0 + RPP * i, P.L - 1);
+        pre[i] = ld8(src, ((b * P.L + qq) * P.H + h) * D + col);
+      }
     }
     if (tid < kDTileKeys) {
       const int qq = t0 + tid;
@@ -334,12 +341,18 @@ __global__ void __launch_bounds__(kDThreads)
   const int tr_off = (4 * gq + (n >> 2)) * RSE + 4 * (n & 3);
 
   const int nit = rep * nqt;
-  load_tile(0);
+  load_tile(0, 0);
   store_tile(0);
   __syncthreads();
+  int nhr = 0, nt0 = 0;  // the next tile's head of the group and first row
   for (int it = 0; it < nit; ++it) {
     const bool more = it + 1 < nit;
-    if (more) load_tile(it + 1);
+    nt0 += kDTileKeys;
+    if (nt0 >= P.L) {
+      nt0 = 0;
+      ++nhr;
+    }
+    if (more) load_tile(nhr, nt0);
     const E *qs = buf0 + (it & 1) * TILE;
     const E *ds = qs + lds_y(D);
     const float *fl = fl0 + (it & 1) * 128;
