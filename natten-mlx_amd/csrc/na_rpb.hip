@@ -414,6 +414,11 @@ struct R1Rows {
   int r;       // this thread's row (clamped to the block's last live row)
 };
 
+// A window holds its query and spans (K - 1) d positions, so every key row
+// of a block lies within (K - 1) d steps of the block's rows.  With d = 1
+// the window start and end are non-decreasing along a sequence (and later
+// sequences lie at later rows), so the block's first and last rows bound
+// the staged range exactly.
 template <int K>
 __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
   R1Rows o;
@@ -421,9 +426,18 @@ __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
   const int row0 = (int)blockIdx.x * nthr;
   o.rows = min(nthr, A.n_rows - row0);
   o.r = row0 + min((int)threadIdx.x, o.rows - 1);
-  const int reach = K * A.d0 * step;
-  o.lo = max(0, row0 - reach);
-  o.hi = min(A.n_rows, row0 + o.rows + reach);
+  if (A.d0 == 1) {
+    const int rl = row0 + o.rows - 1;
+    const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)rl);
+    const RWin wf = rwin_axis(K, 1, A.fd0, pf.i0, A.L0);
+    const RWin wl = rwin_axis(K, 1, A.fd0, pl.i0, A.L0);
+    o.lo = row0 + (wf.s - pf.i0) * step;
+    o.hi = rl + (wl.s + K - 1 - pl.i0) * step + 1;
+  } else {
+    const int reach = (K - 1) * A.d0 * step;
+    o.lo = max(0, row0 - reach);
+    o.hi = min(A.n_rows, row0 + o.rows + reach);
+  }
   return o;
 }
 
