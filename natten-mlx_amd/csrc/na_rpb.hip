@@ -414,11 +414,19 @@ struct R1Rows {
   int r;       // this thread's row (clamped to the block's last live row)
 };
 
-// A window holds its query and spans (K - 1) d positions, so every key row
-// of a block lies within (K - 1) d steps of the block's rows.  With d = 1
-// the window start and end are non-decreasing along a sequence (and later
-// sequences lie at later rows), so the block's first and last rows bound
-// the staged range exactly.
+// Rows a block stages beyond its own on each side, at most: a window holds
+// its query and spans (K - 1) d positions, and a block's range is widened
+// to whole positions (spatial-first rows hold the heads of a position).
+__host__ __device__ __forceinline__ int r1_halo(int K, int d, int step) {
+  return ((K - 1) * d + 1) * step;
+}
+
+// The staged key rows of a block.  With d = 1 the window start and end are
+// non-decreasing along a sequence (and later sequences lie at later rows),
+// so the first row's window start and the last row's window end bound the
+// range, taken over every head of those positions in the spatial-first
+// layout (a row of a lower position may carry a higher head).  Otherwise
+// the rows widened by (K - 1) d positions per side (same head).
 template <int K>
 __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
   R1Rows o;
@@ -431,8 +439,9 @@ __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
     const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)rl);
     const RWin wf = rwin_axis(K, 1, A.fd0, pf.i0, A.L0);
     const RWin wl = rwin_axis(K, 1, A.fd0, pl.i0, A.L0);
-    o.lo = row0 + (wf.s - pf.i0) * step;
-    o.hi = rl + (wl.s + K - 1 - pl.i0) * step + 1;
+    const int hf = A.heads_first ? 0 : pf.h, hl = A.heads_first ? 0 : pl.h;
+    o.lo = row0 - hf + (wf.s - pf.i0) * step;
+    o.hi = rl - hl + (wl.s + K - 1 - pl.i0) * step + step;
   } else {
     const int reach = (K - 1) * A.d0 * step;
     o.lo = max(0, row0 - reach);
@@ -475,7 +484,7 @@ __global__ void __launch_bounds__(512)
   float *so = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   constexpr int R0 = 2 * K - 1;
-  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * K * A.d0 * step) * NC);
+  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * r1_halo(K, A.d0, step)) * NC);
   // every load of the prologue is issued before any is waited on: the query
   // row, one bias entry per thread (H (2K - 1) <= nthr; without a bias table
   // a harmless read of x into the spare slot), the window's first units
@@ -551,7 +560,7 @@ __global__ void __launch_bounds__(512)
   // their stores go to the spare unit after the window
   const uint4 *wsrc = nw4 > 0 ? reinterpret_cast<const uint4 *>(wg) : ysrc;
   uint4 *wdst = nw4 > 0 ? reinterpret_cast<uint4 *>(sw)
-                        : reinterpret_cast<uint4 *>(win + (nthr + 2 * K * A.d0 * step) * NC);
+                        : reinterpret_cast<uint4 *>(win + (nthr + 2 * r1_halo(K, A.d0, step)) * NC);
   uint4 wu[JW];
 #pragma unroll
   for (int j = 0; j < JW; ++j) wu[j] = wsrc[min(tid + j * nthr, max(nw4, 1) - 1)];
@@ -855,11 +864,17 @@ dim3 rgrid(const RpbProb &A, int lgG, int rb = 256) {
   return dim3((unsigned)((threads + rb - 1) / rb));
 }
 
-// Threads per block of the forward gathers (k_rpb_dot / k_rpb_gather):
-// 512 when the window reach K0 * d0 is at least 7 (the halo then weighs
-// on a 256-row block: measured at D = 12, K in {3, 5, 7}, d in {1..8};
-// 384, which splits config 5's rows into exactly two blocks per CU, is
-// slower), 256 otherwise; NATTEN_AMD_RPB_BLOCK overrides it (tuning).
+size_t r1_lds(const RpbProb &A, int rb, bool bias);
+
+// Threads per block of the forward gathers (k_rpb_dot / k_rpb_gather and
+// the staged rank-1 kernels).  Rank 1 with a window reach K0 * d0 of at
+// least 7: 256 rows for d0 = 1 (a block stages exactly its windows' rows),
+// 384 for larger dilations, where the staged kernels take that block
+// (with a bias table), else 512 (the halo weighs on smaller blocks);
+// everything else 256.  Measured at D = 12, K in {3, 5, 7},
+// d in {1..8}: K=7 d=1 qk / av 5.27 / 5.81 us at 512 rows, 5.01 / 5.29-5.35
+// at 256; K=7 d=2 5.93 / 6.20 at 512, 5.74 / 5.79 at 384.
+// NATTEN_AMD_RPB_BLOCK overrides it (tuning).
 int rpb_block(const RpbProb &A) {
   static const int forced = [] {
     const char *e = std::getenv("NATTEN_AMD_RPB_BLOCK");
@@ -867,7 +882,9 @@ int rpb_block(const RpbProb &A) {
     return v == 64 || v == 128 || v == 256 || v == 384 || v == 512 ? v : 0;
   }();
   if (forced > 0) return forced;
-  return A.rank == 1 && A.K0 * A.d0 >= 7 ? 512 : 256;
+  if (A.rank != 1 || A.K0 * A.d0 < 7) return 256;
+  const int rb = A.d0 == 1 ? 256 : 384;
+  return r1_lds(A, rb, true) != 0 ? rb : 512;
 }
 
 template <typename A_, typename B_>
@@ -907,7 +924,7 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
   if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
   if (bias && A.H * A.R0 > rb) return 0;  // one bias entry per thread
   const int64_t step = A.heads_first ? 1 : A.H;
-  const int64_t wrows = rb + 2 * (int64_t)A.K0 * A.d0 * step;
+  const int64_t wrows = rb + 2 * (int64_t)r1_halo(A.K0, A.d0, (int)step);
   if (wrows > 2 * (int64_t)rb) return 0;
   const size_t b = ((size_t)rb * A.K0 * 4 + 15) / 16 * 16 + (size_t)wrows * A.D * 4 +
                    (bias ? (size_t)A.H * A.R0 * 4 : 16);  // the bias table or a spare unit
