@@ -91,6 +91,22 @@ def test_allin1_1d_partial_blocks(B, L, H, D, K, d):
     _check_qk_av(q, k, v, rpb, K, d, D ** -0.5, torch.float32, f"1d partial L{L} K{K} d{d}")
 
 
+# Shapes whose rank-1 blocks of 256, 384 and 512 rows each start inside a
+# sequence's clamped first windows with a head above 0 and end inside its
+# clamped last windows below the last head (found by enumeration over the
+# window rule): a block's staged key rows must then cover the other heads
+# of the edge positions, which share those windows.
+EDGE_1D = [(2, 86, 9, 12, 7), (3, 109, 7, 12, 5), (3, 29, 9, 8, 7)]
+
+
+@pytest.mark.parametrize("B,L,H,D,K", EDGE_1D)
+def test_allin1_1d_block_edges(B, L, H, D, K):
+    _say(f"[case] allin1 1d block edges B={B} L={L} H={H} D={D} K={K}")
+    q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (41, 42, 43))
+    rpb = randn((H, 2 * K - 1), torch.float32, 44, std=0.02)
+    _check_qk_av(q, k, v, rpb, K, 1, 0.288, torch.float32, f"1d edges L{L} H{H} K{K}")
+
+
 CASES_2D = [
     # (K, d, Hh, Hw, D)
     (3, 1, 8, 20, 12),
