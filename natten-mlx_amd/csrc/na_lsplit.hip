@@ -38,9 +38,9 @@ namespace {
 template <int BYTES>
 struct RawWord;
 template <>
-struct RawWord<16> { typedef uint4 type; };
+struct RawWord<16> { typedef unsigned int type __attribute__((ext_vector_type(4))); };
 template <>
-struct RawWord<8> { typedef uint2 type; };
+struct RawWord<8> { typedef unsigned int type __attribute__((ext_vector_type(2))); };
 template <>
 struct RawWord<4> { typedef uint32_t type; };
 template <>
@@ -392,9 +392,12 @@ __global__ void __launch_bounds__(1024)
       dst[j] = (size_t)tok * rowlen + (size_t)iu * VW;
       ok[j] = pv;
     }
+    // streaming stores: the compact rows are not read again here, and
+    // they do not displace the inputs from the caches (qk 7.31 -> 7.0 us
+    // at config 2)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (ok[j]) *reinterpret_cast<VU *>(out + dst[j]) = val[j];
+      if (ok[j]) __builtin_nontemporal_store(val[j], reinterpret_cast<VU *>(out + dst[j]));
   }
 }
 

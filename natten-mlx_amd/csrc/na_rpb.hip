@@ -203,31 +203,49 @@ __device__ __forceinline__ void scale_round(float (&v)[kNT][VEC], float s) {
 // units per thread costs one memory latency rather than one per unit.  The
 // trip count is uniform and indices past the end are clamped onto the last
 // unit (its copies write the same value), so nothing branches per lane.
+// NT: the stores are nontemporal (streaming), for a kernel's output rows
+// that this kernel does not read again: they do not displace the inputs
+// from the caches (config 5, K=7 d=1: qk 5.18 -> 4.86 us, av 5.52 -> 4.76).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT = false>
 __device__ __forceinline__ void block_copy16(uint4 *dst, const uint4 *src,
                                              int64_t n) {
   constexpr int kB = 4;
   if (n <= 0) return;
   const int nn = (int)n, nt = (int)blockDim.x, tid = (int)threadIdx.x;
+  u32x4 *d = reinterpret_cast<u32x4 *>(dst);
+  const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
   for (int base = 0; base < nn; base += kB * nt) {
-    uint4 r[kB];
+    u32x4 r[kB];
     int ix[kB];
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
       ix[j] = min(base + j * nt + tid, nn - 1);
-      r[j] = src[ix[j]];
+      r[j] = s[ix[j]];
     }
 #pragma unroll
-    for (int j = 0; j < kB; ++j) dst[ix[j]] = r[j];
+    for (int j = 0; j < kB; ++j) {
+      if (NT)
+        __builtin_nontemporal_store(r[j], d + ix[j]);
+      else
+        d[ix[j]] = r[j];
+    }
   }
 }
 
 // Block-wide copy of n floats between 16-byte aligned ranges: 16-byte
 // units through block_copy16, then the tail.
+template <bool NT = false>
 __device__ __forceinline__ void block_copy_f32(float *dst, const float *src,
                                                int64_t n) {
   const int64_t n4 = n >> 2;
-  block_copy16(reinterpret_cast<uint4 *>(dst), reinterpret_cast<const uint4 *>(src), n4);
-  for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+  block_copy16<NT>(reinterpret_cast<uint4 *>(dst), reinterpret_cast<const uint4 *>(src), n4);
+  for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) {
+    if (NT)
+      __builtin_nontemporal_store(src[i], dst + i);
+    else
+      dst[i] = src[i];
+  }
 }
 
 // Rank 1: the keys (or values) of every row of a block lie within K*d
@@ -334,7 +352,7 @@ __global__ void __launch_bounds__(512)
     const int64_t row0 = ((int64_t)blockIdx.x * blockDim.x) >> lgG;
     const int64_t rows = min((int64_t)(blockDim.x >> lgG), (int64_t)A.n_rows - row0);
     const int64_t nv = rows * A.KK;
-    block_copy_f32(out + row0 * A.KK, stage, nv);
+    block_copy_f32<true>(out + row0 * A.KK, stage, nv);
   }
 }
 
@@ -533,7 +551,7 @@ __global__ void __launch_bounds__(512)
     sr[k] = acc;
   }
   __syncthreads();
-  block_copy_f32(out + (int64_t)blockIdx.x * nthr * K, so, (int64_t)b.rows * K);
+  block_copy_f32<true>(out + (int64_t)blockIdx.x * nthr * K, so, (int64_t)b.rows * K);
 }
 
 // AV / dq: out[r] = post * sum_k w[r, k] * y[nbr(r, k)] over valid slots.
@@ -607,7 +625,7 @@ __global__ void __launch_bounds__(512)
     sm4[tid * NC + c] = o;
   }
   __syncthreads();
-  block_copy16(reinterpret_cast<uint4 *>(out) + (int64_t)blockIdx.x * nthr * NC,
+  block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)blockIdx.x * nthr * NC,
                reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
 }
 
