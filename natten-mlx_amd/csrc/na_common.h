@@ -53,6 +53,11 @@ __device__ __forceinline__ float round_to(float x) {
 }
 
 // ---- vector I/O: VEC consecutive elements as one wide access ---------------
+// store_nt: the same store, nontemporal (streaming) where the access is 16
+// bytes, for output rows written in long contiguous runs (the merge
+// kernels: two bf16 parts at config-3 size, forward 11.4 -> 10.7 us,
+// backward 19.1 -> 17.4 us).  Scattered per-row stores stay ordinary: the
+// allin1 backward's dk / dv rows ran 15.1 -> 17.1 us with them streaming.
 template <typename T, int VEC>
 struct VecIO;
 
@@ -64,6 +69,7 @@ struct VecIO<T, 1> {
   static __device__ __forceinline__ void store(T *p, const float *x) {
     p[0] = from_f32<T>(x[0]);
   }
+  static __device__ __forceinline__ void store_nt(T *p, const float *x) { store(p, x); }
 };
 
 template <>
@@ -77,6 +83,11 @@ struct VecIO<float, 4> {
   }
   static __device__ __forceinline__ void store(float *p, const float *x) {
     *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  }
+  static __device__ __forceinline__ void store_nt(float *p, const float *x) {
+    typedef float f32v4 __attribute__((ext_vector_type(4)));
+    const f32v4 v = {x[0], x[1], x[2], x[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<f32v4 *>(p));
   }
 };
 
@@ -105,10 +116,19 @@ struct VecIO16x8 {  // 8 x 16-bit elements = one 16-byte access
       __builtin_memcpy(&b, &hi, 2);
       w[i] = (uint32_t)a | ((uint32_t)b << 16);
     }
-    // a streaming store: every user writes output rows it does not read
-    // back, and they do not displace its inputs from the caches (merge of
-    // two bf16 parts at config-3 size: forward 11.4 -> 10.7 us, backward
-    // 19.1 -> 17.4 us)
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  static __device__ __forceinline__ void store_nt(T *p, const float *x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const T lo = from_f32<T>(x[2 * i]);
+      const T hi = from_f32<T>(x[2 * i + 1]);
+      uint16_t a, b;
+      __builtin_memcpy(&a, &lo, 2);
+      __builtin_memcpy(&b, &hi, 2);
+      w[i] = (uint32_t)a | ((uint32_t)b << 16);
+    }
     typedef unsigned int u32v4 __attribute__((ext_vector_type(4)));
     const u32v4 wv = {w[0], w[1], w[2], w[3]};
     __builtin_nontemporal_store(wv, reinterpret_cast<u32v4 *>(p));
@@ -146,6 +166,7 @@ struct VecIO16x4 {  // 4 x 16-bit elements = one 8-byte access
     }
     *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
   }
+  static __device__ __forceinline__ void store_nt(T *p, const float *x) { store(p, x); }
 };
 template <>
 struct VecIO<bf16_t, 4> : VecIO16x4<bf16_t> {};

@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(256)
       for (int e = 0; e < VEC; ++e) acc[e] = fmaf(w[i], x[e], acc[e]);
     }
   }
-  VecIO<T, VEC>::store(out + e0, acc);
+  VecIO<T, VEC>::store_nt(out + e0, acc);
   if (idx == r * per_row) lse[r] = L;
 }
 
@@ -110,7 +110,7 @@ __global__ void __launch_bounds__(256)
     if (Gd.dout[i] != nullptr) {
       Row<T, VEC, NT> t = d;
       t.mul(w[i]);
-      t.store(static_cast<T *>(Gd.dout[i]) + r * D, g.lane, G, D);
+      t.store_nt(static_cast<T *>(Gd.dout[i]) + r * D, g.lane, G, D);
     }
     if (Gd.dlse[i] != nullptr && g.lane == 0)
       Gd.dlse[i][r] = w[i] * (p[i] - pw + dl);

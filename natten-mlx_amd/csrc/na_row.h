@@ -38,6 +38,13 @@ struct Row {
       if (d0 < D) VecIO<T, VEC>::store(row + d0, v[t]);
     }
   }
+  __device__ __forceinline__ void store_nt(T *row, int lane, int G, int D) const {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int d0 = (t * G + lane) * VEC;
+      if (d0 < D) VecIO<T, VEC>::store_nt(row + d0, v[t]);
+    }
+  }
   // load() without a branch: chunks past D read the row's last chunk and
   // are zeroed by selection, so a load issued ahead of its use stays where
   // it is issued (no branch for it to sink into).
