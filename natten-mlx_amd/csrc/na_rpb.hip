@@ -629,6 +629,103 @@ __global__ void __launch_bounds__(512)
                reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
 }
 
+// dk / dv: out[j] = post * sum over the queries i whose window holds key j
+// of w[i, slot of j] * x[i] (the transpose of k_r1_gather), for the shapes
+// of k_r1_dot / k_r1_gather.  One thread per key row; the block stages the
+// query rows and weight rows within (K - 1) d positions of its keys (same
+// head), tests the 2K - 1 candidates i = j + t d, |t| < K, against the
+// window rule, and writes its output rows through LDS as consecutive
+// 16-byte units (streaming stores).
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1_inverse(RpbProb A, const float *__restrict__ w,
+                 const float *__restrict__ x, float *__restrict__ out, float post) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const int step = A.heads_first ? 1 : A.H;
+  const int row0 = (int)blockIdx.x * nthr;
+  const int rows = min(nthr, A.n_rows - row0);
+  const int r = row0 + min(tid, rows - 1);
+  const int reach = (K - 1) * A.d0 * step;
+  const int lo = max(0, row0 - reach), hi = min(A.n_rows, row0 + rows + reach);
+  const int cap = nthr + 2 * r1_halo(K, A.d0, step);  // staged rows, at most
+  float4 *xs = sm4;
+  float *ws = reinterpret_cast<float *>(sm4 + cap * NC);
+  // every load of the prologue is issued before any is waited on
+  const uint4 *xsrc = reinterpret_cast<const uint4 *>(x) + (int64_t)lo * NC;
+  const int nx = (hi - lo) * NC;
+  // weight floats [f0, f1) at ws[f - base], base = f0 rounded down to a
+  // 16-byte unit: whole units [u0, u1) as float4, the few floats before u0
+  // and after u1 one by one (no read past the tensor)
+  const int f0 = lo * K, f1 = hi * K;
+  const int base = f0 & ~3, u0 = (f0 + 3) & ~3, u1 = f1 & ~3;
+  const int nu = u1 > u0 ? (u1 - u0) >> 2 : 0;
+  R1Copy cx;
+  cx.load(xsrc, nx, tid, nthr);
+  const float4 *wu = reinterpret_cast<const float4 *>(w + u0);
+  float4 *wd = reinterpret_cast<float4 *>(ws + (u0 - base));
+  float4 wr0 = make_float4(0.f, 0.f, 0.f, 0.f), wr1 = wr0;
+  if (nu > 0) {
+    wr0 = wu[min(tid, nu - 1)];
+    wr1 = wu[min(tid + nthr, nu - 1)];
+  }
+  const int nh = min(u0, f1) - f0, nt = u1 >= u0 ? f1 - u1 : 0;
+  const float hv = tid < nh ? w[f0 + tid] : 0.f;
+  const float tv = tid < nt ? w[u1 + tid] : 0.f;
+  cx.store(reinterpret_cast<uint4 *>(xs), xsrc, nx, tid, nthr);
+  if (nu > 0) {
+    wd[min(tid, nu - 1)] = wr0;
+    wd[min(tid + nthr, nu - 1)] = wr1;
+    for (int i = tid + 2 * nthr; i < nu; i += nthr) wd[i] = wu[i];
+  }
+  if (tid < nh) ws[f0 - base + tid] = hv;
+  if (tid < nt) ws[u1 - base + tid] = tv;
+  const RPos p = rpos(A, (uint32_t)r);
+  const int wrow0 = f0 - base;  // ws offset of staged row 0
+  __syncthreads();
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  // four candidates per step keep the loads in flight without holding all
+  // 2K - 1 candidates' rows in registers
+#pragma unroll 4
+  for (int t = -(K - 1); t <= K - 1; ++t) {
+    const int i = p.i0 + t * A.d0;
+    bool ok = i >= 0 && i < A.L0;
+    int k = 0;
+    if (ok) {
+      const RWin wi = rwin_axis(K, A.d0, A.fd0, i, A.L0);
+      const int off = p.i0 - wi.s;  // a multiple of d (same phase)
+      k = A.d0 == 1 ? off : (int)fdiv((uint32_t)max(off, 0), A.fd0);
+      ok = off >= 0 && k < K;
+    }
+    const int sr = r - lo + t * A.d0 * step;  // the candidate's staged row
+    const float wk = ok ? ws[wrow0 + sr * K + k] : 0.f;
+    const float4 *xr = xs + (ok ? sr : r - lo) * NC;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 v = xr[c];
+      acc[c].x = fmaf(wk, v.x, acc[c].x);
+      acc[c].y = fmaf(wk, v.y, acc[c].y);
+      acc[c].z = fmaf(wk, v.z, acc[c].z);
+      acc[c].w = fmaf(wk, v.w, acc[c].w);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float4 o = acc[c];
+    o.x *= post;
+    o.y *= post;
+    o.z *= post;
+    o.w *= post;
+    sm4[tid * NC + c] = o;
+  }
+  __syncthreads();
+  block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)row0 * NC,
+                     reinterpret_cast<const uint4 *>(sm4), (int64_t)rows * NC);
+}
+
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
 // transpose of k_rpb_gather, evaluated per key row.  A query i can hold key
 // j only on j's dilation phase and within K*d of it, so the candidates
@@ -1013,6 +1110,36 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
 #undef R1G_
   return true;
 }
+
+// The rank-1 fp32 inverse (dk / dv) where the staged dot / gather apply.
+bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
+                float post, hipStream_t st) {
+  const int rb = rpb_block(A);
+  if (r1_lds(A, rb, false) == 0) return false;
+  const int step = A.heads_first ? 1 : A.H;
+  const size_t cap = (size_t)rb + 2 * (size_t)r1_halo(A.K0, A.d0, step);
+  const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
+  if (lds > 65536) return false;
+  const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
+#define R1I_(KK, NC) \
+  hipLaunchKernelGGL((k_r1_inverse<KK, NC>), grid, dim3(rb), lds, st, A, w, x, out, post)
+  switch (A.D / 4) {
+#define NC_ 1
+    case 1: R1_K(A.K0, R1I_) break;
+#undef NC_
+#define NC_ 2
+    case 2: R1_K(A.K0, R1I_) break;
+#undef NC_
+#define NC_ 3
+    case 3: R1_K(A.K0, R1I_) break;
+#undef NC_
+#define NC_ 4
+    default: R1_K(A.K0, R1I_) break;
+#undef NC_
+  }
+#undef R1I_
+  return true;
+}
 #undef R1_K
 
 template <typename TX, typename TY>
@@ -1072,6 +1199,12 @@ void launch_gather(const RpbProb &A, const float *w, const void *y, void *out,
 template <typename TX, typename TO>
 void launch_inverse(const RpbProb &A, const float *w, const void *x, void *out,
                     int scale_x, hipStream_t st) {
+  if constexpr (sizeof(TX) == 4 && sizeof(TO) == 4) {
+    // fp32 x: x scale is exact up to rounding, so the scale is applied to
+    // the sums instead
+    if (r1_inverse(A, w, (const float *)x, (float *)out, scale_x ? A.scale : 1.f, st))
+      return;
+  }
   constexpr int V = vmax_of<TX, TO>();
   const RShape s = rshape(A.D, V);
   if (s.vec == V)
