@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(512)
 // head), tests the 2K - 1 candidates i = j + t d, |t| < K, against the
 // window rule, and writes its output rows through LDS as consecutive
 // 16-byte units (streaming stores).
-template <int K, int NC>
+template <int K, int NC, bool D1>
 __global__ void __launch_bounds__(512)
     k_r1_inverse(RpbProb A, const float *__restrict__ w,
                  const float *__restrict__ x, float *__restrict__ out, float post) {
@@ -693,10 +693,14 @@ __global__ void __launch_bounds__(512)
     const int i = p.i0 + t * A.d0;
     bool ok = i >= 0 && i < A.L0;
     int k = 0;
-    if (ok) {
+    if (D1) {
+      // d = 1 (K <= L): window start clamp(i - K / 2, 0, L - K)
+      k = p.i0 - min(max(i - K / 2, 0), A.L0 - K);
+      ok = ok && k >= 0 && k < K;
+    } else if (ok) {
       const RWin wi = rwin_axis(K, A.d0, A.fd0, i, A.L0);
       const int off = p.i0 - wi.s;  // a multiple of d (same phase)
-      k = A.d0 == 1 ? off : (int)fdiv((uint32_t)max(off, 0), A.fd0);
+      k = (int)fdiv((uint32_t)max(off, 0), A.fd0);
       ok = off >= 0 && k < K;
     }
     const int sr = r - lo + t * A.d0 * step;  // the candidate's staged row
@@ -1121,8 +1125,15 @@ bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
   const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
   if (lds > 65536) return false;
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
-#define R1I_(KK, NC) \
-  hipLaunchKernelGGL((k_r1_inverse<KK, NC>), grid, dim3(rb), lds, st, A, w, x, out, post)
+#define R1I_(KK, NC)                                                              \
+  do {                                                                            \
+    if (A.d0 == 1)                                                                \
+      hipLaunchKernelGGL((k_r1_inverse<KK, NC, true>), grid, dim3(rb), lds, st, A, \
+                         w, x, out, post);                                        \
+    else                                                                          \
+      hipLaunchKernelGGL((k_r1_inverse<KK, NC, false>), grid, dim3(rb), lds, st,   \
+                         A, w, x, out, post);                                     \
+  } while (0)
   switch (A.D / 4) {
 #define NC_ 1
     case 1: R1_K(A.K0, R1I_) break;
