@@ -629,6 +629,213 @@ __global__ void __launch_bounds__(512)
                reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
 }
 
+// ---- rank 1, spatial-first, dilation d > 1: rows in phase-major order ----
+// A block takes rows in the order (sample, phase r, index m in the phase,
+// head): phase r of a sample is an undilated sequence of plen(r) positions
+// i = r + d m whose windows stay in the phase (the partition rule: in phase
+// units the window of m starts at clamp(m - K/2, 0, plen - K)), so a block
+// stages exactly the positions its windows reach, as at d = 1, instead of
+// (K - 1) d positions on each side.  Memory keeps the [B, L, H, ...] order:
+// the copies map each virtual position (b L + pstart(r) + m) to its memory
+// position (b L + r + d m), whose rows of all heads form one run.
+struct PhMap {
+  int32_t q, rem;      // L / d and L % d: phase r holds q + (r < rem) positions
+  FastDiv fq, fq1;     // q, q + 1
+};
+
+struct PhPos {
+  int b, r, m, plen, pstart;
+};
+
+__device__ __forceinline__ PhPos ph_pos(const RpbProb &A, const PhMap &M, int pos) {
+  PhPos o;
+  o.b = (int)fdiv((uint32_t)pos, A.fL0);
+  const int p = pos - o.b * A.L0;
+  const int c1 = M.rem * (M.q + 1);
+  if (p < c1) {
+    o.r = (int)fdiv((uint32_t)p, M.fq1);
+    o.m = p - o.r * (M.q + 1);
+  } else {
+    const int r2 = (int)fdiv((uint32_t)(p - c1), M.fq);
+    o.r = M.rem + r2;
+    o.m = p - c1 - r2 * M.q;
+  }
+  o.plen = M.q + (o.r < M.rem ? 1 : 0);
+  o.pstart = o.r * M.q + min(o.r, M.rem);
+  return o;
+}
+
+// Copy n 16-byte units of the virtual range starting at unit g0 (ru units per
+// position) between memory and LDS, four per thread in flight.  LOAD: memory
+// to LDS; else LDS to memory with streaming stores.
+template <bool LOAD>
+__device__ __forceinline__ void ph_copy(const RpbProb &A, const PhMap &M, int ru,
+                                        FastDiv fru, const uint4 *gsrc, uint4 *gdst,
+                                        uint4 *lds, int g0, int n) {
+  constexpr int kB = 4;
+  if (n <= 0) return;
+  const int nt = (int)blockDim.x, tid = (int)threadIdx.x;
+  for (int base = 0; base < n; base += kB * nt) {
+    u32x4 r[kB];
+    int ix[kB], mu[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      ix[j] = min(base + j * nt + tid, n - 1);
+      const int g = g0 + ix[j];
+      const int pos = (int)fdiv((uint32_t)g, fru);
+      const PhPos o = ph_pos(A, M, pos);
+      mu[j] = (o.b * A.L0 + o.r + A.d0 * o.m) * ru + (g - pos * ru);
+      r[j] = LOAD ? reinterpret_cast<const u32x4 *>(gsrc)[mu[j]]
+                  : reinterpret_cast<const u32x4 *>(lds)[ix[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (LOAD)
+        reinterpret_cast<u32x4 *>(lds)[ix[j]] = r[j];
+      else
+        __builtin_nontemporal_store(r[j], reinterpret_cast<u32x4 *>(gdst) + mu[j]);
+    }
+  }
+}
+
+// The block's rows [row0, row0 + rows) and the virtual positions [lo, hi)
+// of their windows; the thread's row: virtual position, head, phase place.
+struct PhRows {
+  int row0, rows, lo, hi;
+  int h, mrow;  // the thread's head and memory row
+  PhPos o;      // the thread's phase place
+  int wsm;      // its window start in phase units
+};
+
+template <int K>
+__device__ __forceinline__ PhRows ph_rows(const RpbProb &A, const PhMap &M) {
+  PhRows R;
+  const int nthr = (int)blockDim.x;
+  R.row0 = (int)blockIdx.x * nthr;
+  R.rows = min(nthr, A.n_rows - R.row0);
+  const PhPos f = ph_pos(A, M, (int)fdiv((uint32_t)R.row0, A.fH));
+  const PhPos l = ph_pos(A, M, (int)fdiv((uint32_t)(R.row0 + R.rows - 1), A.fH));
+  R.lo = f.b * A.L0 + f.pstart + min(max(f.m - K / 2, 0), f.plen - K);
+  R.hi = l.b * A.L0 + l.pstart + min(max(l.m - K / 2, 0), l.plen - K) + K;
+  const int v = R.row0 + min((int)threadIdx.x, R.rows - 1);
+  const int vpos = (int)fdiv((uint32_t)v, A.fH);
+  R.h = v - vpos * A.H;
+  R.o = ph_pos(A, M, vpos);
+  R.mrow = (R.o.b * A.L0 + R.o.r + A.d0 * R.o.m) * A.H + R.h;
+  R.wsm = min(max(R.o.m - K / 2, 0), R.o.plen - K);
+  return R;
+}
+
+// Unit counts and their divisors for the phase-major copies: key / value
+// rows (H NC units per position), slot rows (H K / 4 units per position).
+struct PhUnits {
+  int ry, rk;
+  FastDiv fry, frk;
+};
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_dot(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ x,
+              const float *__restrict__ y, const float *__restrict__ rpb,
+              float *__restrict__ out, int scale_x) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const PhRows R = ph_rows<K>(A, M);
+  float *so = reinterpret_cast<float *>(sm4);
+  float4 *win = sm4 + (nthr * K + 3) / 4;
+  constexpr int R0 = 2 * K - 1;
+  float *bs = reinterpret_cast<float *>(win + (nthr + 2 * r1_halo(K, 1, A.H)) * NC);
+  float4 xv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) xv[c] = reinterpret_cast<const float4 *>(x)[(int64_t)R.mrow * NC + c];
+  const int nb = rpb != nullptr ? A.H * R0 : 1;
+  const float bv = (rpb != nullptr ? rpb : x)[min(tid, nb - 1)];
+  ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(y), nullptr,
+                reinterpret_cast<uint4 *>(win), R.lo * U.ry, (R.hi - R.lo) * U.ry);
+  bs[min(tid, nb - 1)] = bv;
+  const RWin w = rwin_axis(K, A.d0, A.fd0, R.o.r + A.d0 * R.o.m, A.L0);
+  if (scale_x) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      xv[c].x *= A.scale;
+      xv[c].y *= A.scale;
+      xv[c].z *= A.scale;
+      xv[c].w *= A.scale;
+    }
+  }
+  __syncthreads();
+  const float4 *yb =
+      win + ((R.o.b * A.L0 + R.o.pstart + R.wsm - R.lo) * A.H + R.h) * NC;
+  const int ys = A.H * NC;
+  const float *br = bs + R.h * R0;
+  float *sr = so + tid * K;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 t = yb[k * ys + c];
+      acc = fmaf(xv[c].x, t.x, acc);
+      acc = fmaf(xv[c].y, t.y, acc);
+      acc = fmaf(xv[c].z, t.z, acc);
+      acc = fmaf(xv[c].w, t.w, acc);
+    }
+    if (rpb != nullptr) acc += br[clampi(w.pb + k, 0, R0 - 1)];
+    sr[k] = acc;
+  }
+  __syncthreads();
+  ph_copy<false>(A, M, U.rk, U.frk, nullptr, reinterpret_cast<uint4 *>(out),
+                 reinterpret_cast<uint4 *>(so), R.row0 * K / 4, R.rows * K / 4);
+}
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_gather(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ wgt,
+                 const float *__restrict__ y, float *__restrict__ out, float post) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const PhRows R = ph_rows<K>(A, M);
+  float *sw = reinterpret_cast<float *>(sm4);
+  float4 *win = sm4 + (nthr * K + 3) / 4;
+  ph_copy<true>(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(wgt), nullptr,
+                reinterpret_cast<uint4 *>(sw), R.row0 * K / 4, R.rows * K / 4);
+  ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(y), nullptr,
+                reinterpret_cast<uint4 *>(win), R.lo * U.ry, (R.hi - R.lo) * U.ry);
+  __syncthreads();
+  const float4 *yb =
+      win + ((R.o.b * A.L0 + R.o.pstart + R.wsm - R.lo) * A.H + R.h) * NC;
+  const int ys = A.H * NC;
+  const float *wr = sw + tid * K;
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float wk = wr[k];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 t = yb[k * ys + c];
+      acc[c].x = fmaf(wk, t.x, acc[c].x);
+      acc[c].y = fmaf(wk, t.y, acc[c].y);
+      acc[c].z = fmaf(wk, t.z, acc[c].z);
+      acc[c].w = fmaf(wk, t.w, acc[c].w);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float4 o = acc[c];
+    o.x *= post;
+    o.y *= post;
+    o.z *= post;
+    o.w *= post;
+    sm4[tid * NC + c] = o;
+  }
+  __syncthreads();
+  ph_copy<false>(A, M, U.ry, U.fry, nullptr, reinterpret_cast<uint4 *>(out),
+                 reinterpret_cast<uint4 *>(sm4), R.row0 * NC, R.rows * NC);
+}
+
 // dk / dv: out[j] = post * sum over the queries i whose window holds key j
 // of w[i, slot of j] * x[i] (the transpose of k_r1_gather), for the shapes
 // of k_r1_dot / k_r1_gather.  One thread per key row; the block stages the
@@ -1064,11 +1271,70 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
 
 // The rank-1 fp32 dot / gather when r1_lds applies; false otherwise (no
 // slot of these shapes is outside its window, so `fill` is never written).
+// The phase-major kernels (k_r1p_*), where the contiguous staged kernels do
+// not apply (halos above twice the block's rows: large dilations):
+// spatial-first rows, d > 1, the staged shapes of r1_lds, and runs of H K
+// slot floats that are whole 16-byte units.  Blocks of 256 rows; LDS as
+// r1_lds with a halo of K positions of H rows per side.  Config 5: K=5 d=8
+// qk / av 8.15 / 9.31 -> 5.6 / 6.2 us, K=7 d=8 10.2 / 10.9 -> 5.9 / 5.95 us
+// (where the contiguous kernels apply they are faster: the phase-major
+// copies map every 16-byte unit to its memory position).
+constexpr int kPhBlock = 256;
+size_t ph_lds(const RpbProb &A, bool bias) {
+  if (A.heads_first || A.rank != 1 || A.d0 < 2 || (A.H * A.K0) % 4 != 0) return 0;
+  if (A.D % 4 != 0 || A.D > 16) return 0;
+  if ((int64_t)A.K0 * A.d0 > A.L0) return 0;
+  if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
+  if (bias && A.H * A.R0 > kPhBlock) return 0;
+  const int64_t wrows = kPhBlock + 2 * (int64_t)r1_halo(A.K0, 1, A.H);
+  if (wrows > 3 * (int64_t)kPhBlock) return 0;
+  const size_t b = ((size_t)kPhBlock * A.K0 * 4 + 15) / 16 * 16 + (size_t)wrows * A.D * 4 +
+                   (bias ? (size_t)A.H * A.R0 * 4 : 16);
+  return b <= 65536 ? b : 0;
+}
+
+void ph_maps(const RpbProb &A, PhMap *M, PhUnits *U) {
+  M->q = A.L0 / A.d0;
+  M->rem = A.L0 % A.d0;
+  M->fq = make_fastdiv((uint32_t)M->q);
+  M->fq1 = make_fastdiv((uint32_t)(M->q + 1));
+  U->ry = A.H * (A.D / 4);
+  U->rk = A.H * A.K0 / 4;
+  U->fry = make_fastdiv((uint32_t)U->ry);
+  U->frk = make_fastdiv((uint32_t)U->rk);
+}
+
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
             float *out, int scale_x, hipStream_t st) {
   const int rb = rpb_block(A);
   const size_t lds = r1_lds(A, rb, rpb != nullptr);
-  if (lds == 0) return false;
+  if (lds == 0) {
+    const size_t pl = ph_lds(A, rpb != nullptr);
+    if (pl == 0) return false;
+    PhMap M;
+    PhUnits U;
+    ph_maps(A, &M, &U);
+    const dim3 pg((unsigned)((A.n_rows + kPhBlock - 1) / kPhBlock));
+#define R1PD_(KK, NC)                                                                \
+  hipLaunchKernelGGL((k_r1p_dot<KK, NC>), pg, dim3(kPhBlock), pl, st, A, M, U, x, y, \
+                     rpb, out, scale_x)
+    switch (A.D / 4) {
+#define NC_ 1
+      case 1: R1_K(A.K0, R1PD_) break;
+#undef NC_
+#define NC_ 2
+      case 2: R1_K(A.K0, R1PD_) break;
+#undef NC_
+#define NC_ 3
+      case 3: R1_K(A.K0, R1PD_) break;
+#undef NC_
+#define NC_ 4
+      default: R1_K(A.K0, R1PD_) break;
+#undef NC_
+    }
+#undef R1PD_
+    return true;
+  }
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
 #define R1D_(KK, NC)                                                           \
   hipLaunchKernelGGL((k_r1_dot<KK, NC>), grid, dim3(rb), lds, st, A, x, y, rpb, \
@@ -1095,7 +1361,33 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
                float post, hipStream_t st) {
   const int rb = rpb_block(A);
   const size_t lds = r1_lds(A, rb, false);
-  if (lds == 0) return false;
+  if (lds == 0) {
+    const size_t pl = ph_lds(A, false);
+    if (pl == 0) return false;
+    PhMap M;
+    PhUnits U;
+    ph_maps(A, &M, &U);
+    const dim3 pg((unsigned)((A.n_rows + kPhBlock - 1) / kPhBlock));
+#define R1PG_(KK, NC)                                                                \
+  hipLaunchKernelGGL((k_r1p_gather<KK, NC>), pg, dim3(kPhBlock), pl, st, A, M, U, w, \
+                     y, out, post)
+    switch (A.D / 4) {
+#define NC_ 1
+      case 1: R1_K(A.K0, R1PG_) break;
+#undef NC_
+#define NC_ 2
+      case 2: R1_K(A.K0, R1PG_) break;
+#undef NC_
+#define NC_ 3
+      case 3: R1_K(A.K0, R1PG_) break;
+#undef NC_
+#define NC_ 4
+      default: R1_K(A.K0, R1PG_) break;
+#undef NC_
+    }
+#undef R1PG_
+    return true;
+  }
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
 #define R1G_(KK, NC) \
   hipLaunchKernelGGL((k_r1_gather<KK, NC>), grid, dim3(rb), lds, st, A, w, y, out, post)
