@@ -107,6 +107,22 @@ def test_allin1_1d_block_edges(B, L, H, D, K):
     _check_qk_av(q, k, v, rpb, K, 1, 0.288, torch.float32, f"1d edges L{L} H{H} K{K}")
 
 
+# Dilations whose contiguous blocks' halos are too wide, so the rows run in
+# phase-major order (k_r1p_*): L not a multiple of d (phases of unequal
+# length), blocks spanning phases and samples.
+PHASE_1D = [(2, 203, 12, 12, 7, 8), (3, 150, 16, 8, 5, 8), (1, 333, 16, 4, 7, 7)]
+
+
+@pytest.mark.parametrize("B,L,H,D,K,d", PHASE_1D)
+def test_allin1_1d_phase_major(B, L, H, D, K, d):
+    from natten_amd._core import hip  # noqa: F401  (the library is loaded)
+
+    _say(f"[case] allin1 1d phase-major B={B} L={L} H={H} D={D} K={K} d={d}")
+    q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (51, 52, 53))
+    rpb = randn((H, 2 * K - 1), torch.float32, 54, std=0.02)
+    _check_qk_av(q, k, v, rpb, K, d, 0.288, torch.float32, f"1d phase L{L} K{K} d{d}")
+
+
 CASES_2D = [
     # (K, d, Hh, Hw, D)
     (3, 1, 8, 20, 12),
