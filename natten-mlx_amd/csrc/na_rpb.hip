@@ -559,7 +559,7 @@ template <int K, int NC>
 __global__ void __launch_bounds__(512)
     k_r1_gather(RpbProb A, const float *__restrict__ wgt,
                 const float *__restrict__ y, float *__restrict__ out,
-                float post) {
+                float post, double *__restrict__ bpart) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int step = A.heads_first ? 1 : A.H;
@@ -592,6 +592,10 @@ __global__ void __launch_bounds__(512)
   cw.store(reinterpret_cast<uint4 *>(win), ysrc, nwin, tid, nthr);
   const RPos p = rpos(A, (uint32_t)b.r);
   const RWin w = rwin_axis(K, A.d0, A.fd0, p.i0, A.L0);
+  // bias-gradient partials (QK backward's dq pass): each row's first bias
+  // cell, after the window and its spare unit
+  int *spb = reinterpret_cast<int *>(win + (nthr + 2 * r1_halo(K, A.d0, step)) * NC + 1);
+  if (bpart != nullptr) spb[tid] = w.pb;
   __syncthreads();
   const float4 *yb = win + (b.r - b.lo + (w.s - p.i0) * step) * NC;
   const int ys = A.d0 * step * NC;
@@ -609,6 +613,24 @@ __global__ void __launch_bounds__(512)
       acc[c].y = fmaf(wk, t.y, acc[c].y);
       acc[c].z = fmaf(wk, t.z, acc[c].z);
       acc[c].w = fmaf(wk, t.w, acc[c].w);
+    }
+  }
+  if (bpart != nullptr) {
+    // thread (h, c) of the H (2K - 1) bias cells adds, in row order and in
+    // float64, the block's weights w[r, k] of head h with pb(r) + k = c
+    // (spatial-first rows: head = row mod H; pb + k never needs clamping
+    // here, pb lies in [0, K - 1]); one partial per (cell, block)
+    constexpr int R0 = 2 * K - 1;
+    if (tid < A.H * R0) {
+      const int h = tid / R0, c = tid - h * R0;
+      const int row0 = (int)blockIdx.x * nthr;
+      const int h0 = row0 - (int)fdiv((uint32_t)row0, A.fH) * A.H;
+      double acc_b = 0.0;
+      for (int j = h >= h0 ? h - h0 : h - h0 + A.H; j < b.rows; j += A.H) {
+        const int k = c - spb[j];
+        if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
+      }
+      bpart[(int64_t)tid * gridDim.x + blockIdx.x] = acc_b;
     }
   }
   // the block's output rows are one contiguous range: write them through
@@ -1358,9 +1380,16 @@ bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
 }
 
 bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
-               float post, hipStream_t st) {
+               float post, hipStream_t st, double *bpart = nullptr) {
   const int rb = rpb_block(A);
-  const size_t lds = r1_lds(A, rb, false);
+  size_t lds = r1_lds(A, rb, false);
+  if (bpart != nullptr) {
+    // bias partials: spatial-first rows, one thread per bias cell, each
+    // row's first bias cell in LDS
+    if (lds == 0 || A.heads_first || A.H * A.R0 > rb) return false;
+    lds += (size_t)rb * sizeof(int);
+    if (lds > 65536) return false;
+  }
   if (lds == 0) {
     const size_t pl = ph_lds(A, false);
     if (pl == 0) return false;
@@ -1389,8 +1418,9 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
     return true;
   }
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
-#define R1G_(KK, NC) \
-  hipLaunchKernelGGL((k_r1_gather<KK, NC>), grid, dim3(rb), lds, st, A, w, y, out, post)
+#define R1G_(KK, NC)                                                              \
+  hipLaunchKernelGGL((k_r1_gather<KK, NC>), grid, dim3(rb), lds, st, A, w, y, out, post, \
+                     bpart)
   switch (A.D / 4) {
 #define NC_ 1
     case 1: R1_K(A.K0, R1G_) break;
@@ -1571,17 +1601,30 @@ size_t rpb_bias_workspace_bytes(const RpbProb &A) {
 void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
                 const float *dlogits, void *dq, void *dk, float *drpb,
                 void *workspace, hipStream_t st) {
+  int32_t chunk, n_chunks;
+  bias_chunking(A, &chunk, &n_chunks);
+  // fp32 rank 1 on the staged kernels: the dq pass also writes the bias
+  // gradient's partials, one per block (when they fit the workspace)
+  int32_t n_fused = 0;
+  if (drpb != nullptr && dq != nullptr && dtype == NA_F32 && A.n_rows > 0) {
+    const int32_t nblk = (A.n_rows + rpb_block(A) - 1) / rpb_block(A);
+    if (nblk <= n_chunks &&
+        r1_gather(A, dlogits, (const float *)key, (float *)dq, A.has_scale ? A.scale : 1.f,
+                  st, (double *)workspace))
+      n_fused = nblk;
+  }
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     if (A.n_rows == 0) return;
-    if (dq != nullptr)
+    if (dq != nullptr && n_fused == 0)
       launch_gather<T, T>(A, dlogits, key, dq, A.has_scale ? A.scale : 1.f,
                           st);
     if (dk != nullptr) launch_inverse<T, T>(A, dlogits, q, dk, A.has_scale, st);
   });
-  if (drpb != nullptr) {
-    int32_t chunk, n_chunks;
-    bias_chunking(A, &chunk, &n_chunks);
+  if (drpb != nullptr && n_fused > 0) {
+    hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)(A.H * A.R0 * A.R1)), dim3(64), 0,
+                       st, (const double *)workspace, n_fused, drpb);
+  } else if (drpb != nullptr) {
     const int32_t nb = A.H * A.R0 * A.R1;
     // per-(query, head) bin cells in LDS when they fit 32 KB
     const size_t sbytes = (size_t)chunk * nb * sizeof(float);
