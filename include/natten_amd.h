@@ -297,6 +297,33 @@ int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,
                   const void *dout, int32_t out_dtype, float *dattn,
                   void *dvalue, void *stream);
 
+/*
+ * Host-only diagnostic: the kernel family each allin1 pass of these
+ * parameters runs on, as the launchers choose it (no device work).  Rank-1
+ * float32 problems take the staged kernels (a block's windows in LDS) or,
+ * for large dilations, the phase-major ones; everything else the generic
+ * kernels.  qk assumes a bias table, dq a requested drpb (fused_bias: the dq
+ * pass also forms the bias gradient's partials).  The kernels' choice has
+ * no counterpart in the reference (its Metal kernels are chosen by K and
+ * head_dim, functional_metal.py:1921-2033).
+ */
+enum na_rpb_kernel_t {
+  NA_RPB_GENERIC = 0, /* k_rpb_dot / k_rpb_gather / k_rpb_inverse */
+  NA_RPB_STAGED = 1,  /* k_r1_dot / k_r1_gather / k_r1_inverse */
+  NA_RPB_PHASE = 2    /* k_r1p_dot / k_r1p_gather */
+};
+typedef struct na_rpb_plan {
+  int32_t qk;         /* na_rpb_qk_fwd */
+  int32_t av;         /* na_rpb_av_fwd */
+  int32_t dq;         /* na_rpb_qk_bwd, dq pass */
+  int32_t dk;         /* na_rpb_qk_bwd, dk pass */
+  int32_t dattn;      /* na_rpb_av_bwd, dattn pass */
+  int32_t dv;         /* na_rpb_av_bwd, dv pass */
+  int32_t fused_bias; /* 1: the dq pass forms the drpb partials */
+  int32_t block;      /* rows per block of the forward kernels */
+} na_rpb_plan;
+int na_rpb_kernel_plan(const na_rpb_params *p, na_rpb_plan *plan);
+
 /* ---- merge of attention outputs --------------------------------------- */
 
 #define NA_MERGE_MAX_PARTS 8

@@ -289,21 +289,38 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_of_current_device(void **out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+// The scratch of the device the kernels run on: that of `stream` (a null
+// stream runs on the current device).  The address is looked up with that
+// device current (each device holds its own copy of the array at its own
+// address); the caller's current device is restored afterwards.
+int scratch_of_stream_device(hipStream_t stream, void **out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess)
     return fail(NA_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = -1;
+    e = hipStreamGetDevice(stream, &sd);
+    if (e != hipSuccess)
+      return fail(NA_ERR_INVALID, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    dev = (int)sd;
+  }
   if (dev < 0 || dev >= kMaxDevices)
     return fail(NA_ERR_UNSUPPORTED, "device %d is beyond the %d devices na_bwd_noalloc serves",
                 dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(NA_ERR_LAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
     void *ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t er = dev != cur ? hipSetDevice(cur) : hipSuccess;
     if (e != hipSuccess || ptr == nullptr)
       return fail(NA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
                   hipGetErrorString(e));
+    if (er != hipSuccess)
+      return fail(NA_ERR_LAUNCH, "hipSetDevice(%d): %s", cur, hipGetErrorString(er));
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -512,7 +529,7 @@ int na_bwd_noalloc(const na_params *p, const void *q, const void *k,
                 "fixed maximum of %zu; use na_bwd with a caller workspace",
                 need, kScratchBytes);
   void *ws = nullptr;
-  const int src = scratch_of_current_device(&ws);
+  const int src = scratch_of_stream_device(as_stream(stream), &ws);
   if (src != NA_OK) return src;
   // every byte the kernels read from the workspace is written earlier in
   // the same call (delta rows; one partial per reduction segment), so the
@@ -659,6 +676,24 @@ int na_rpb_qk_bwd(const na_rpb_params *p, const void *q, const void *key,
   na::rpb_qk_bwd(A, p->dtype, q, key, dlogits, dq, dk, drpb, workspace,
                  as_stream(stream));
   return launch_status("na_rpb_qk_bwd");
+}
+
+int na_rpb_kernel_plan(const na_rpb_params *p, na_rpb_plan *plan) {
+  if (plan == nullptr) return fail(NA_ERR_INVALID, "plan is NULL");
+  na::RpbProb A;
+  const int rc = make_rpb(p, &A);
+  if (rc != NA_OK) return rc;
+  na::RpbPlanInfo o{};
+  na::rpb_plan(A, p->dtype, &o);
+  plan->qk = o.qk;
+  plan->av = o.av;
+  plan->dq = o.dq;
+  plan->dk = o.dk;
+  plan->dattn = o.dattn;
+  plan->dv = o.dv;
+  plan->fused_bias = o.fused_bias;
+  plan->block = o.block;
+  return NA_OK;
 }
 
 int na_rpb_av_bwd(const na_rpb_params *p, const float *attn, const void *value,

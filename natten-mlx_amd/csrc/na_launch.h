@@ -51,6 +51,12 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
 void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
                 const void *value, const void *dout, float *dattn, void *dvalue,
                 hipStream_t st);
+// Kernel family per allin1 pass (0 generic, 1 staged rank-1, 2 phase-major
+// rank-1) as the launchers choose it; host only.
+struct RpbPlanInfo {
+  int32_t qk, av, dq, dk, dattn, dv, fused_bias, block;
+};
+void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o);
 
 // Matrix-core kernels (na_mfma.hip): bf16/fp16, head_dim 32/64/128,
 // stride 1, odd kernel size on every non-causal axis.

@@ -1268,8 +1268,17 @@ size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes, int rb) {
 // three times the block's rows still beats them: config 5 K=7 d=4 qk / av
 // 9.08 / 10.5 -> 6.08 / 5.68 us).  With K d <= L every window lies inside
 // the sequence, so each slot row is in the staged range.
+// The staged and phase-major kernels index rows, slot rows and 16-byte units
+// with 32-bit integers: a row index times K or head_dim must stay below
+// 2^31 (larger problems take the generic kernels, whose row offsets are
+// 64-bit).
+bool r1_offsets_fit(const RpbProb &A) {
+  return (int64_t)A.n_rows * std::max(A.K0, A.D) < ((int64_t)1 << 31);
+}
+
 size_t r1_lds(const RpbProb &A, int rb, bool bias) {
   if (A.rank != 1 || A.D % 4 != 0 || A.D > 16) return 0;
+  if (!r1_offsets_fit(A)) return 0;
   if ((int64_t)A.K0 * A.d0 > A.L0) return 0;
   if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
   if (bias && A.H * A.R0 > rb) return 0;  // one bias entry per thread
@@ -1304,6 +1313,7 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias) {
 constexpr int kPhBlock = 256;
 size_t ph_lds(const RpbProb &A, bool bias) {
   if (A.heads_first || A.rank != 1 || A.d0 < 2 || (A.H * A.K0) % 4 != 0) return 0;
+  if (!r1_offsets_fit(A)) return 0;
   if (A.D % 4 != 0 || A.D > 16) return 0;
   if ((int64_t)A.K0 * A.d0 > A.L0) return 0;
   if (A.K0 < 3 || A.K0 > 13 || (A.K0 & 1) == 0 || A.R0 != 2 * A.K0 - 1) return 0;
@@ -1324,6 +1334,34 @@ void ph_maps(const RpbProb &A, PhMap *M, PhUnits *U) {
   U->rk = A.H * A.K0 / 4;
   U->fry = make_fastdiv((uint32_t)U->ry);
   U->frk = make_fastdiv((uint32_t)U->rk);
+}
+
+// Which rank-1 fp32 kernels apply (the launchers below and rpb_plan share
+// these): the staged contiguous ones, the phase-major ones, or neither.
+enum R1Kind { kR1None = 0, kR1Staged = 1, kR1Phase = 2 };
+R1Kind r1_kind(const RpbProb &A, bool bias) {
+  if (r1_lds(A, rpb_block(A), bias) != 0) return kR1Staged;
+  if (ph_lds(A, bias) != 0) return kR1Phase;
+  return kR1None;
+}
+// The staged gather that also forms the bias gradient's partials:
+// spatial-first rows, one thread per bias cell, each row's first bias cell
+// in LDS.
+size_t r1_bias_gather_lds(const RpbProb &A) {
+  const int rb = rpb_block(A);
+  const size_t lds = r1_lds(A, rb, false);
+  if (lds == 0 || A.heads_first || A.H * A.R0 > rb) return 0;
+  const size_t b = lds + (size_t)rb * sizeof(int);
+  return b <= 65536 ? b : 0;
+}
+// LDS of the staged inverse (dk / dv), or 0 where it does not apply.
+size_t r1_inverse_lds(const RpbProb &A) {
+  const int rb = rpb_block(A);
+  if (r1_lds(A, rb, false) == 0) return 0;
+  const int step = A.heads_first ? 1 : A.H;
+  const size_t cap = (size_t)rb + 2 * (size_t)r1_halo(A.K0, A.d0, step);
+  const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
+  return lds <= 65536 ? lds : 0;
 }
 
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
@@ -1384,11 +1422,8 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
   const int rb = rpb_block(A);
   size_t lds = r1_lds(A, rb, false);
   if (bpart != nullptr) {
-    // bias partials: spatial-first rows, one thread per bias cell, each
-    // row's first bias cell in LDS
-    if (lds == 0 || A.heads_first || A.H * A.R0 > rb) return false;
-    lds += (size_t)rb * sizeof(int);
-    if (lds > 65536) return false;
+    lds = r1_bias_gather_lds(A);
+    if (lds == 0) return false;
   }
   if (lds == 0) {
     const size_t pl = ph_lds(A, false);
@@ -1443,11 +1478,8 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
 bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
                 float post, hipStream_t st) {
   const int rb = rpb_block(A);
-  if (r1_lds(A, rb, false) == 0) return false;
-  const int step = A.heads_first ? 1 : A.H;
-  const size_t cap = (size_t)rb + 2 * (size_t)r1_halo(A.K0, A.d0, step);
-  const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
-  if (lds > 65536) return false;
+  const size_t lds = r1_inverse_lds(A);
+  if (lds == 0) return false;
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
 #define R1I_(KK, NC)                                                              \
   do {                                                                            \
@@ -1636,6 +1668,24 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)nb), dim3(64), 0, st,
                        (const double *)workspace, n_chunks, drpb);
   }
+}
+
+void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
+  // the rank-1 fp32 kernels take float inputs and outputs only
+  const bool f32 = dtype == NA_F32;
+  auto kind = [&](bool bias) { return f32 ? (int)r1_kind(A, bias) : 0; };
+  o->qk = kind(true);
+  o->av = kind(false);
+  o->dattn = kind(false);
+  o->dk = f32 && r1_inverse_lds(A) != 0 ? 1 : 0;
+  o->dv = o->dk;
+  int32_t chunk, n_chunks;
+  bias_chunking(A, &chunk, &n_chunks);
+  const int rb = rpb_block(A);
+  const int64_t nblk = ((int64_t)A.n_rows + rb - 1) / rb;
+  o->fused_bias = f32 && A.n_rows > 0 && nblk <= n_chunks && r1_bias_gather_lds(A) != 0;
+  o->dq = o->fused_bias ? 1 : kind(false);
+  o->block = o->qk == kR1Phase ? kPhBlock : rb;
 }
 
 void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,

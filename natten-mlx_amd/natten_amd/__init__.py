@@ -35,6 +35,18 @@ def has_hip() -> bool:
     return _hip.is_available()
 
 
+def has_metal() -> bool:
+    """The reference's Metal-tier probe (``natten_mlx/__init__.py:23-24``):
+    there is no Metal tier on this platform, so always False."""
+    return False
+
+
+def has_nanobind() -> bool:
+    """The reference's nanobind-tier probe (``natten_mlx/__init__.py:27-28``):
+    always False here (the native tier is the HIP library, see has_hip)."""
+    return False
+
+
 def get_backend() -> str:
     return ops.get_backend()
 
@@ -54,5 +66,5 @@ __all__ = [
     "__version__", "na1d", "na1d_varlen", "na1d_varlen_gqa", "na2d", "na2d_varlen", "na1d_qk",
     "na1d_av", "na2d_qk", "na2d_av", "na3d", "na3d_varlen", "na3d_qk", "na3d_av",
     "merge_attentions", "NeighborhoodAttention1D", "NeighborhoodAttention2D",
-    "NeighborhoodAttention3D", "has_hip", "get_backend", "set_backend", "get_support_matrix",
+    "NeighborhoodAttention3D", "has_hip", "has_metal", "has_nanobind", "get_backend", "set_backend", "get_support_matrix",
 ]

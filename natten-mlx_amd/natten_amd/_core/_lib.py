@@ -87,6 +87,24 @@ class NaPlan(ctypes.Structure):
     ]
 
 
+class NaRpbPlan(ctypes.Structure):
+    """Mirror of ``na_rpb_plan`` (include/natten_amd.h)."""
+
+    _fields_ = [
+        ("qk", ctypes.c_int32),
+        ("av", ctypes.c_int32),
+        ("dq", ctypes.c_int32),
+        ("dk", ctypes.c_int32),
+        ("dattn", ctypes.c_int32),
+        ("dv", ctypes.c_int32),
+        ("fused_bias", ctypes.c_int32),
+        ("block", ctypes.c_int32),
+    ]
+
+
+RPB_GENERIC, RPB_STAGED, RPB_PHASE = 0, 1, 2
+
+
 class NaMergeParams(ctypes.Structure):
     """Mirror of ``na_merge_params`` (include/natten_amd.h)."""
 
@@ -133,6 +151,7 @@ SIGNATURES = {
     "na_rpb_bwd_workspace_bytes": (ctypes.c_size_t, [_R]),
     "na_rpb_qk_bwd": (ctypes.c_int, [_R, _V, _V, _V, _V, _V, _V, _V, ctypes.c_size_t, _V]),
     "na_rpb_av_bwd": (ctypes.c_int, [_R, _V, _V, _V, _I, _V, _V, _V]),
+    "na_rpb_kernel_plan": (ctypes.c_int, [_R, ctypes.POINTER(NaRpbPlan)]),
     "na_merge_fwd": (ctypes.c_int, [_M, _PP, _PP, _V, _V, _V]),
     "na_merge_bwd": (ctypes.c_int, [_M, _PP, _PP, _V, _V, _PP, _PP, _V]),
 }

@@ -133,3 +133,13 @@ def test_backend_registry():
     natten_amd.set_backend("auto")
     with pytest.raises(ValueError, match="Unknown backend"):
         natten_amd.set_backend("pure")
+
+
+def test_reference_tier_probes_exist():
+    """natten_mlx's tier probes (``__init__.py:23-28``) exist and report
+    that neither the Metal nor the nanobind tier is present."""
+    import natten_amd
+
+    assert natten_amd.has_metal() is False
+    assert natten_amd.has_nanobind() is False
+    assert "has_metal" in natten_amd.__all__ and "has_nanobind" in natten_amd.__all__

@@ -99,8 +99,23 @@ def test_allin1_1d_partial_blocks(B, L, H, D, K, d):
 EDGE_1D = [(2, 86, 9, 12, 7), (3, 109, 7, 12, 5), (3, 29, 9, 8, 7)]
 
 
+def _plan(B, L, H, D, K, d):
+    import ctypes
+
+    from natten_amd._core import _lib
+
+    p = _lib.make_rpb_params(1, B, H, D, (L,), K, d, False, _lib.NA_F32, 0.288)
+    plan = _lib.NaRpbPlan()
+    assert _lib.load().na_rpb_kernel_plan(ctypes.byref(p), ctypes.byref(plan)) == 0
+    return plan
+
+
 @pytest.mark.parametrize("B,L,H,D,K", EDGE_1D)
 def test_allin1_1d_block_edges(B, L, H, D, K):
+    from natten_amd._core import _lib
+
+    pl = _plan(B, L, H, D, K, 1)  # the staged kernels and the fused bias partials run
+    assert (pl.qk, pl.av, pl.dq, pl.dk, pl.fused_bias) == (_lib.RPB_STAGED,) * 4 + (1,)
     _say(f"[case] allin1 1d block edges B={B} L={L} H={H} D={D} K={K}")
     q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (41, 42, 43))
     rpb = randn((H, 2 * K - 1), torch.float32, 44, std=0.02)
@@ -115,7 +130,10 @@ PHASE_1D = [(2, 203, 12, 12, 7, 8), (3, 150, 16, 8, 5, 8), (1, 333, 16, 4, 7, 7)
 
 @pytest.mark.parametrize("B,L,H,D,K,d", PHASE_1D)
 def test_allin1_1d_phase_major(B, L, H, D, K, d):
-    from natten_amd._core import hip  # noqa: F401  (the library is loaded)
+    from natten_amd._core import _lib
+
+    pl = _plan(B, L, H, D, K, d)  # the phase-major kernels run
+    assert (pl.qk, pl.av, pl.dq, pl.dattn) == (_lib.RPB_PHASE,) * 4
 
     _say(f"[case] allin1 1d phase-major B={B} L={L} H={H} D={D} K={K} d={d}")
     q, k, v = (randn((B, L, H, D), torch.float32, s) for s in (51, 52, 53))
@@ -217,3 +235,14 @@ def test_allin1_bias_gradient_deterministic():
         na2d_qk_rpb(q, k, r, 7, 2, scale=0.3).backward(g)
         res.append(r.grad.clone())
     assert torch.equal(res[0], res[1])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_allin1_1d_low_precision_dilated(dtype):
+    """bf16 / fp16 rank-1 at head_dim 12 with d >= 2: the generic kernels
+    with the block size the fp32 staged kernels' shapes select (384 rows)."""
+    B, L, H, D, K, d = 2, 203, 12, 12, 5, 2
+    _say(f"[case] allin1 1d {dtype} B={B} L={L} H={H} D={D} K={K} d={d}")
+    q, k, v = (randn((B, L, H, D), dtype, s) for s in (61, 62, 63))
+    rpb = randn((H, 2 * K - 1), torch.float32, 64, std=0.02)
+    _check_qk_av(q, k, v, rpb, K, d, 0.288, dtype, f"1d {dtype} K{K} d{d}")

@@ -175,9 +175,20 @@ def test_config4_full():
 def test_config5_full(K, d):
     from natten_amd.extras.allin1 import na1d_av_fused, na1d_qk_rpb
 
+    import ctypes
+
+    from natten_amd._core import _lib
+
     _say(f"[case] config 5 allin1 fp32 [8,2048,12,12] K={K} d={d}")
     f32 = torch.float32
     B, L, H, D = 8, 2048, 12, 12
+    # the kernels the bench times: staged rank-1 (phase-major at K >= 5,
+    # d = 8), and the dq pass forming the bias partials on the staged ones
+    pp = _lib.make_rpb_params(1, B, H, D, (L,), K, d, False, _lib.NA_F32, 0.288)
+    pl = _lib.NaRpbPlan()
+    assert _lib.load().na_rpb_kernel_plan(ctypes.byref(pp), ctypes.byref(pl)) == 0
+    want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
+    assert (pl.qk, pl.av, pl.dq) == (want,) * 3 and pl.fused_bias == (want == _lib.RPB_STAGED)
     q, k, v = (randn((B, L, H, D), f32, s) for s in (40, 41, 42))
     rpb = randn((H, 2 * K - 1), f32, 43, std=0.02)
     qd, kd = _dev(q, k)

@@ -152,3 +152,61 @@ def test_varlen_backward_box_covers_every_sample_length():
         need = max(max(_box_need(Lb, K, d, t, True), _box_need(Lb, K, d, t, False))
                    for Lb in range(d * K, L + 1, 7 if L > 1000 else 1))
         assert p["box"][2] >= need, (L, K, d, p, need)
+
+
+# ---- allin1 kernel families (na_rpb_kernel_plan, host only) ----
+
+def _rpb_plan(B, L, H, D, K, d, dtype=None, heads_first=False):
+    import ctypes
+
+    from natten_amd._core import _lib
+
+    lib = _lib.load()
+    p = _lib.make_rpb_params(1, B, H, D, (L,), K, d, heads_first,
+                             _lib.NA_F32 if dtype is None else dtype, 0.288)
+    plan = _lib.NaRpbPlan()
+    assert lib.na_rpb_kernel_plan(ctypes.byref(p), ctypes.byref(plan)) == 0
+    return {f: getattr(plan, f) for f, _ in plan._fields_}
+
+
+def test_config5_allin1_kernels():
+    """Config 5 ([8, 2048, 12, 12] fp32): the staged rank-1 kernels for
+    every K x d except K = 5 and 7 at d = 8, whose contiguous halos are too
+    wide and which run phase-major; the dq pass forms the bias partials
+    wherever the staged gather applies."""
+    from natten_amd._core import _lib
+
+    for K in (3, 5, 7):
+        for d in (1, 2, 4, 8):
+            pl = _rpb_plan(8, 2048, 12, 12, K, d)
+            want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
+            assert pl["qk"] == want and pl["av"] == want and pl["dattn"] == want, (K, d, pl)
+            assert pl["fused_bias"] == (want == _lib.RPB_STAGED), (K, d, pl)
+            assert pl["dq"] == want, (K, d, pl)
+    # staged dk / dv wherever their staged rows fit LDS
+    assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dk"] == _lib.RPB_STAGED
+    assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dv"] == _lib.RPB_STAGED
+
+
+def test_allin1_low_precision_takes_generic_kernels():
+    from natten_amd._core import _lib
+
+    for dt in (_lib.NA_BF16, _lib.NA_F16):
+        pl = _rpb_plan(2, 203, 12, 12, 5, 2, dtype=dt)
+        assert all(pl[f] == _lib.RPB_GENERIC for f in ("qk", "av", "dq", "dk", "dattn", "dv"))
+        assert pl["fused_bias"] == 0
+
+
+def test_allin1_32bit_offset_limit():
+    """The rank-1 kernels index with 32-bit integers: a problem whose rows
+    times max(K, head_dim) reach 2^31 takes the generic kernels (64-bit row
+    offsets); one just below keeps the staged kernels."""
+    from natten_amd._core import _lib
+
+    big = _rpb_plan(1, 15_000_000, 12, 12, 7, 1)        # 180M rows x 12 >= 2^31
+    assert all(big[f] == _lib.RPB_GENERIC for f in ("qk", "av", "dq", "dk", "dattn", "dv"))
+    assert big["fused_bias"] == 0
+    ok = _rpb_plan(1, 10_000_000, 12, 12, 7, 1)         # 120M rows x 12 < 2^31
+    assert ok["qk"] == _lib.RPB_STAGED and ok["dk"] == _lib.RPB_STAGED
+    # the phase-major kernels obey the same limit
+    assert _rpb_plan(1, 15_000_000, 12, 12, 7, 8)["qk"] == _lib.RPB_GENERIC

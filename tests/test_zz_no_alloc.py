@@ -34,11 +34,12 @@ def _problem(B, sp, H, Hkv, D, nx, dtype, ks, dil, seed):
     return p, (q, k, v, ek, ev, out, lse, do, dlse)
 
 
-def _grads(lib, p, t, noalloc):
+def _grads(lib, p, t, noalloc, stream=None):
     q, k, v, ek, ev, out, lse, do, dlse = t
     g = [torch.full_like(x, float("nan")) for x in (q, k, v)]
     gx = [torch.full_like(x, float("nan")) if x is not None else None for x in (ek, ev)]
-    stream = _lib.stream_of(q)
+    torch.cuda.synchronize()
+    stream = _lib.stream_of(q) if stream is None else stream
     common = [_p(q), _p(k), _p(v), _p(ek), _p(ev), _p(out), _p(lse), _p(do), _p(dlse),
               _p(g[0]), _p(g[1]), _p(g[2]), _p(gx[0]), _p(gx[1])]
     if noalloc:
@@ -82,6 +83,21 @@ def test_noalloc_matches_workspace_backward(name, probs):
         for a, b, n in zip(got, ref, ("dq", "dk", "dv", "dek", "dev")):
             assert not torch.isnan(a).any(), f"{name} call {i}: {n} not written"
             assert torch.equal(a, b), f"{name} call {i}: {n} differs from na_bwd"
+
+
+@pytest.mark.gpu
+def test_noalloc_on_a_side_stream():
+    """The scratch is the one of the stream's device: a call on a stream other
+    than torch's current one (same device here) matches na_bwd."""
+    lib = _lib.load()
+    kw = CASES[0][1][1]
+    print(f"[case] na_bwd_noalloc side stream: {kw}", flush=True)
+    p, t = _problem(seed=7, **kw)
+    ref = _grads(lib, p, t, noalloc=False)
+    side = torch.cuda.Stream()
+    got = _grads(lib, p, t, noalloc=True, stream=side.cuda_stream)
+    for a, b, n in zip(got, ref, ("dq", "dk", "dv", "dek", "dev")):
+        assert torch.equal(a, b), f"side stream: {n} differs from na_bwd"
 
 
 def test_noalloc_rejects_problems_beyond_the_scratch():
