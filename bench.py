@@ -50,6 +50,7 @@ BF16_PEAK_TFLOPS = 2516.6
 FP32_PEAK_TFLOPS = 157.3
 COPY_BYTES = 1 << 30      # calibration copy for --profile-calls (1 GiB each way)
 FLUSH_BYTES = 512 << 20   # written before a "mall_flushed" trial (> the 256 MB MALL)
+ROTATE_BYTES = 640 << 20  # buffers cycled through by the "cold" (rotating) figures
 WARMUP, TRIALS, DROP = 5, 20, 2   # final_perf_table.py:33-58
 
 
@@ -136,11 +137,44 @@ def protocol_ms(run, flush: bool = False) -> dict:
     return {"median": statistics.median(kept), "min": min(kept), "max": max(kept)}
 
 
-def call_timing(fn, reps: int = 20) -> dict:
+def rotating_ms(make_call, nbytes: int) -> dict:
+    """Cold-HBM device time (ms) per call: back-to-back calls, each on its own
+    set of input and output buffers, cycling through enough sets that they
+    hold more than ROTATE_BYTES together (2.5x the 256 MB Infinity Cache), so
+    no call finds its inputs in the MALL or an L2, while neighbouring calls
+    still overlap their launch ramps as in the warm figure.
+    ``make_call(i)`` returns a zero-argument call bound to set i (it copies
+    the inputs); ``nbytes`` is one call's algorithmic bytes.  A graph of the
+    n calls (outputs kept alive, so every call writes its own buffers) is
+    replayed under the protocol; the median over n."""
+    n = max(2, min(4096, -(-ROTATE_BYTES // max(nbytes, 1))))
+    calls = [make_call(i) for i in range(n)]
+    keep = []
+
+    def cycle():
+        keep.clear()
+        for c in calls:
+            keep.append(c())
+
+    cycle()
+    torch.cuda.synchronize()
+    g, _ = capture(cycle, 1)
+    run = (lambda: g.replay()) if g is not None else cycle
+    r = protocol_ms(run)
+    out = {"cold_ms": r["median"] / n, "sets": n, "bytes_cycled": n * nbytes}
+    del calls, keep, g
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def call_timing(fn, reps: int = 20, cold=None) -> dict:
     """Device time (ms) of one call of ``fn``: warm = median trial of a graph
     replay of ``reps`` back-to-back calls, divided by ``reps``; single = one
     call per trial (launch ramp and drain not hidden by a neighbour);
-    mall_flushed = one call per trial right after a MALL flush."""
+    mall_flushed = one call per trial right after a MALL flush; with
+    ``cold`` = (make_call, nbytes), cold = rotating_ms over distinct buffer
+    sets (inputs from HBM, launches overlapped)."""
     fn()
     torch.cuda.synchronize()
     g_many, _ = capture(fn, reps)
@@ -150,9 +184,17 @@ def call_timing(fn, reps: int = 20) -> dict:
     one = (lambda: g_one.replay()) if g_one is not None else fn
     warm = protocol_ms(many)
     single = protocol_ms(one)
-    cold = protocol_ms(one, flush=True)
-    return {"warm_ms": warm["median"] / reps, "single_ms": single["median"],
-            "flushed_ms": cold["median"]}
+    flushed = protocol_ms(one, flush=True)
+    res = {"warm_ms": warm["median"] / reps, "single_ms": single["median"],
+           "flushed_ms": flushed["median"]}
+    if cold is not None:
+        res.update(rotating_ms(*cold))
+    return res
+
+
+def clones(*ts):
+    """Copies of the tensors in fresh device memory (None stays None)."""
+    return tuple(None if t is None else t.detach().clone() for t in ts)
 
 
 def eager_call_ms(fn, reps: int = 20) -> float:
@@ -238,7 +280,19 @@ def _roof(call, nbytes, flops, timing, flop_peak, traffic=None):
                      "Cache between them; mall_flushed: one call after a 512 MB read",
             "mall_flushed": {"call_ms": round(timing["flushed_ms"], 5),
                              "achieved": round(cold, 2),
-                             "frac": round(cold / HBM_PEAK_GBS, 5)}}
+                             "frac": round(cold / HBM_PEAK_GBS, 5)},
+            **_cold_fields(nbytes, timing)}
+
+
+def _cold_fields(nbytes, timing):
+    """cold_ms / cold_frac: the rotating-buffer figure (inputs from HBM,
+    launches overlapped), when the timing has one."""
+    if timing.get("cold_ms") is None:
+        return {}
+    c = nbytes / (timing["cold_ms"] * 1e-3) / 1e9
+    return {"cold_ms": round(timing["cold_ms"], 5), "cold_achieved": round(c, 2),
+            "cold_frac": round(c / HBM_PEAK_GBS, 5),
+            "cold_sets": timing["sets"], "cold_bytes_cycled": timing["bytes_cycled"]}
 
 
 # ---------------------------------------------------------------------------
@@ -268,8 +322,19 @@ def cpu_median(fn, budget_s: float = 10.0, min_runs: int = 3, max_runs: int = 50
     return statistics.median(times), len(times), time.perf_counter() - t_start, threads
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _cpu_line(value, unit, threads, sample, runs, wall, per_step_s):
     return {"value": round(value, 6), "unit": unit, "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"{sample}; median of {runs} runs in {wall:.1f} s of CPU time",
             "ms_per_step": round(per_step_s * 1e3, 3)}
 
@@ -325,9 +390,21 @@ def run_gpu(args):
         qd, kd, vd = q.detach(), k.detach(), v.detach()
         ks, stt, dl, ca = (K, K), (1, 1), (dil, dil), (False, False)
         out, lse = hip.fused_forward(qd, kd, vd, ks, stt, dl, ca, None)
-        fwd = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, stt, dl, ca, None))
+        _, _, fwd_b, bwd_b = algorithmic(K * K)
+
+        def fwd_set(i):
+            a = clones(qd, kd, vd)
+            return lambda: hip.fused_forward(*a, ks, stt, dl, ca, None)
+
+        def bwd_set(i):
+            a = clones(qd, kd, vd, out, lse, do)
+            return lambda: hip.fused_backward(*a, None, ks, stt, dl, ca, None)
+
+        fwd = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, stt, dl, ca, None),
+                          cold=(fwd_set, fwd_b) if dil == 1 else None)
         bwd = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, stt,
-                                                     dl, ca, None))
+                                                     dl, ca, None),
+                          cold=(bwd_set, bwd_b) if dil == 1 else None)
         results[dil] = dict(st, fwd=fwd, bwd=bwd)
     return results
 
@@ -417,7 +494,9 @@ def main_line(args):
                 "fwd_call_single_ms": rnd(r["fwd"]["single_ms"]),
                 "bwd_call_single_ms": rnd(r["bwd"]["single_ms"]),
                 "fwd_call_flushed_ms": rnd(r["fwd"]["flushed_ms"]),
-                "bwd_call_flushed_ms": rnd(r["bwd"]["flushed_ms"])}
+                "bwd_call_flushed_ms": rnd(r["bwd"]["flushed_ms"]),
+                "fwd_call_cold_ms": rnd(r["fwd"].get("cold_ms")),
+                "bwd_call_cold_ms": rnd(r["bwd"].get("cold_ms"))}
 
     return {
         "metric": "na2d 56x56 k7 bf16 fwd+bwd ms & TFLOP/s; % MFMA/HBM roofline, 1 MI355X",
@@ -490,9 +569,15 @@ def wl_cfg1(args):
     q, k, v = (_gen((Bc, L, H, Dc), torch.float32, s) for s in range(3))
     a = ((Kc,), (1,), (1,), (False,), None)
     step_ms, st = _step_ms(lambda: natten_amd.na1d(q, k, v, Kc), args)
-    t = call_timing(lambda: hip.fused_forward(q, k, v, *a, want_lse=False))
     flops = Bc * L * H * 4 * Dc * Kc
     nbytes = 4 * Bc * L * H * Dc * 4
+
+    def fwd_set(i):
+        c = clones(q, k, v)
+        return lambda: hip.fused_forward(*c, *a, want_lse=False)
+
+    t = call_timing(lambda: hip.fused_forward(q, k, v, *a, want_lse=False),
+                    cold=(fwd_set, nbytes))
     roof = _roof("na_fwd", nbytes, flops, t, FP32_PEAK_TFLOPS)
     cpu = None
     if not args.no_cpu:
@@ -520,13 +605,34 @@ def wl_split(args):
     a = ((K, K), (1, 1), (1, 1), (False, False))
     logits = hip.qk_forward(q, k, *a, None)
     attn = torch.softmax(logits, -1)
-    tq = call_timing(lambda: hip.qk_forward(q, k, *a, None))
-    ta = call_timing(lambda: hip.av_forward(attn, v, *a))
-    dl = _gen(logits.shape, torch.bfloat16, 5)
-    tqb = call_timing(lambda: hip.qk_backward(q, k, dl, *a, None))
-    tab = call_timing(lambda: hip.av_backward(attn, v, do, *a))
     t = B * HH * WW * HEADS * D * 2
     lg = B * HH * WW * HEADS * K * K * 2
+
+    def qk_set(i):
+        c = clones(q, k)
+        return lambda: hip.qk_forward(*c, *a, None)
+
+    def av_set(i):
+        c = clones(attn, v)
+        return lambda: hip.av_forward(*c, *a)
+
+    tq = call_timing(lambda: hip.qk_forward(q, k, *a, None), cold=(qk_set, 2 * t + lg))
+    ta = call_timing(lambda: hip.av_forward(attn, v, *a), cold=(av_set, lg + 2 * t))
+    dl = _gen(logits.shape, torch.bfloat16, 5)
+
+    def qkb_set(i):
+        c = clones(q, k, dl)
+        return lambda: hip.qk_backward(*c, *a, None)
+
+    def avb_set(i):
+        c = clones(attn, v, do)
+        return lambda: hip.av_backward(*c, *a)
+
+    # backward: q, k, dlogits read, dq, dk written / attn, v, dout read,
+    # dattn, dv written
+    qkb_b, avb_b = 4 * t + lg, 2 * lg + 3 * t
+    tqb = call_timing(lambda: hip.qk_backward(q, k, dl, *a, None), cold=(qkb_set, qkb_b))
+    tab = call_timing(lambda: hip.av_backward(attn, v, do, *a), cold=(avb_set, avb_b))
     pairs = B * HEADS * _valid_pairs((HH, WW), (K, K), (1, 1), (False, False))
     qk_b, av_b = 2 * t + lg, lg + 2 * t
     fl = 2 * D * pairs
@@ -550,10 +656,9 @@ def wl_split(args):
                        "k=7 dilation=1", "global_batch": B}
     return _line("na2d split qk/av bf16 HBM GB/s, 1 MI355X", value, "GB/s", ms, "bf16", cfg,
                  rq if tq["warm_ms"] >= ta["warm_ms"] else ra, cpu,
-                 {"calls": {"qk": rq, "av": ra, "qk_bwd_ms": round(tqb["warm_ms"], 5),
-                            "av_bwd_ms": round(tab["warm_ms"], 5),
-                            "qk_bwd_flushed_ms": round(tqb["flushed_ms"], 5),
-                            "av_bwd_flushed_ms": round(tab["flushed_ms"], 5)}})
+                 {"calls": {"qk": rq, "av": ra,
+                            "qk_bwd": _roof("na_qk_bwd", qkb_b, 2 * fl, tqb, BF16_PEAK_TFLOPS),
+                            "av_bwd": _roof("na_av_bwd", avb_b, 2 * fl, tab, BF16_PEAK_TFLOPS)}})
 
 
 def wl_cfg3(args):
@@ -576,14 +681,24 @@ def wl_cfg3(args):
     step_ms, stt = _step_ms(step, args)
     qd, kd, vd = q.detach(), k.detach(), v.detach()
     out, lse = hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None)
-    tf = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None))
-    tb = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca,
-                                                None))
     pairs = 8 * _valid_pairs(shape[1:4], ks, dl, ca)
     tb_ = 16 * 32 * 32 * 8 * 64 * 2
     lse_b = 16 * 32 * 32 * 8 * 4
     fwd_f, bwd_f = 4 * 64 * pairs, 8 * 64 * pairs
     fwd_b, bwd_b = 4 * tb_ + lse_b, 8 * tb_ + lse_b
+
+    def fwd_set(i):
+        c = clones(qd, kd, vd)
+        return lambda: hip.fused_forward(*c, ks, st, dl, ca, None)
+
+    def bwd_set(i):
+        c = clones(qd, kd, vd, out, lse, do)
+        return lambda: hip.fused_backward(*c, None, ks, st, dl, ca, None)
+
+    tf = call_timing(lambda: hip.fused_forward(qd, kd, vd, ks, st, dl, ca, None),
+                     cold=(fwd_set, fwd_b))
+    tb = call_timing(lambda: hip.fused_backward(qd, kd, vd, out, lse, do, None, ks, st, dl, ca,
+                                                None), cold=(bwd_set, bwd_b))
     rf = _roof("na_fwd", fwd_b, fwd_f, tf, BF16_PEAK_TFLOPS, measured_traffic("na_fwd", "cfg3"))
     rb = _roof("na_bwd", bwd_b, bwd_f, tb, BF16_PEAK_TFLOPS, measured_traffic("na_bwd", "cfg3"))
     rf["mfma_busy"] = measured_mfma_busy("na_fwd", "cfg3")
@@ -643,17 +758,39 @@ def wl_cfg4(args):
     se = lens.to("cuda:0").reshape(Bc, 1).contiguous()
     kw = dict(extra_k=ak, extra_v=av, sample_extent=se, varlen_clamped=True)
     a = ((63,), (1,), (2,), (False,), None)
-    tf = call_timing(lambda: hip.fused_forward(q, k, v, *a, **kw))
-    # the backward (dq, dk, dv and the additional tokens' gradients), timed
-    # alongside; not part of `value`
-    out, lse = hip.fused_forward(q, k, v, *a, **kw)
-    do = _gen(out.shape, torch.float16, 6)
-    tb = call_timing(lambda: hip.fused_backward(q, k, v, out, lse, do, None, *a, **kw))
     tokens = int(lens.sum())
     flops = tokens * H * 4 * Dc * (63 + nx)
     nbytes = tokens * (H * Dc * 2 + 2 * Hkv * Dc * 2 + H * Dc * 2) + 2 * Bc * nx * Hkv * Dc * 2
     nbytes_pad = nbytes + (Bc * L - tokens) * H * Dc * 2  # padded rows written as zeros
+    # backward: q, out, dO, lse rows and k, v rows of the samples read; dq,
+    # dk, dv written over the whole tensors (zero rows outside the samples);
+    # the additional tokens read and their gradients written
+    qrow, kvrow = H * Dc * 2, Hkv * Dc * 2
+    bwd_b = (tokens * (3 * qrow + 2 * kvrow + H * 4) + Bc * L * (qrow + 2 * kvrow)
+             + 4 * Bc * nx * Hkv * Dc * 2)
+    bwd_f = tokens * H * 8 * Dc * (63 + nx)
+
+    def fwd_set(i):
+        c = clones(q, k, v, ak, av)
+        return lambda: hip.fused_forward(*c[:3], *a, extra_k=c[3], extra_v=c[4],
+                                         sample_extent=se, varlen_clamped=True)
+
+    tf = call_timing(lambda: hip.fused_forward(q, k, v, *a, **kw), cold=(fwd_set, nbytes_pad))
+    # the backward (dq, dk, dv and the additional tokens' gradients), timed
+    # alongside; not part of `value`
+    out, lse = hip.fused_forward(q, k, v, *a, **kw)
+    do = _gen(out.shape, torch.float16, 6)
+
+    def bwd_set(i):
+        c = clones(q, k, v, out, lse, do, ak, av)
+        return lambda: hip.fused_backward(*c[:6], None, *a, extra_k=c[6], extra_v=c[7],
+                                          sample_extent=se, varlen_clamped=True)
+
+    tb = call_timing(lambda: hip.fused_backward(q, k, v, out, lse, do, None, *a, **kw),
+                     cold=(bwd_set, bwd_b))
     rf = _roof("na_fwd", nbytes_pad, flops, tf, BF16_PEAK_TFLOPS)
+    rb = _roof("na_bwd", bwd_b, bwd_f, tb, BF16_PEAK_TFLOPS, measured_traffic("na_bwd", "cfg4"))
+    rb["mfma_busy"] = measured_mfma_busy("na_bwd", "cfg4")
     cpu = None
     if not args.no_cpu:
         rows = 1024
@@ -678,7 +815,8 @@ def wl_cfg4(args):
                  {"timing": dict(stt, fwd_call_ms=round(tf["warm_ms"], 5),
                                  call_tflops=round(flops / (tf["warm_ms"] * 1e-3) / 1e12, 3),
                                  bwd_call_ms=round(tb["warm_ms"], 5),
-                                 bwd_call_flushed_ms=round(tb["flushed_ms"], 5))})
+                                 bwd_call_flushed_ms=round(tb["flushed_ms"], 5)),
+                  "calls": {"fwd": rf, "bwd": rb}})
 
 
 def wl_cfg5(args):
@@ -699,18 +837,45 @@ def wl_cfg5(args):
         for d in (1, 2, 4, 8):
             logits = hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288)
             attn = torch.softmax(logits, -1)
-            tq = call_timing(lambda: hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288))
-            ta = call_timing(lambda: hip.rpb_av_forward(attn, v, Kx, d))
-            tqb = call_timing(lambda: hip.rpb_qk_backward(q, k, attn, Kx, d, 0.288))
-            tab = call_timing(lambda: hip.rpb_av_backward(attn, v, v, Kx, d))
             lg = rows * Kx * 4
             qk_b, av_b = 2 * t + lg, lg + 2 * t
+            # backward: q, k, dlogits read, dq, dk written (+ the bias
+            # gradient); attn, v, dout read, dattn, dv written
+            qkb_b, avb_b = 4 * t + lg + H * (2 * Kx - 1) * 4, 2 * lg + 3 * t
+            head = (Kx, d) == (7, 1)
+
+            def qk_set(i, Kx=Kx, d=d, rpb=rpb):
+                c = clones(q, k, rpb)
+                return lambda: hip.rpb_qk_forward(*c, Kx, d, 0.288)
+
+            def av_set(i, Kx=Kx, d=d, attn=attn):
+                c = clones(attn, v)
+                return lambda: hip.rpb_av_forward(*c, Kx, d)
+
+            def qkb_set(i, Kx=Kx, d=d, attn=attn):
+                c = clones(q, k, attn)
+                return lambda: hip.rpb_qk_backward(*c, Kx, d, 0.288)
+
+            def avb_set(i, Kx=Kx, d=d, attn=attn):
+                c = clones(attn, v, v)
+                return lambda: hip.rpb_av_backward(*c, Kx, d)
+
+            tq = call_timing(lambda: hip.rpb_qk_forward(q, k, rpb, Kx, d, 0.288),
+                             cold=(qk_set, qk_b) if head else None)
+            ta = call_timing(lambda: hip.rpb_av_forward(attn, v, Kx, d),
+                             cold=(av_set, av_b) if head else None)
+            tqb = call_timing(lambda: hip.rpb_qk_backward(q, k, attn, Kx, d, 0.288),
+                              cold=(qkb_set, qkb_b) if head else None)
+            tab = call_timing(lambda: hip.rpb_av_backward(attn, v, v, Kx, d),
+                              cold=(avb_set, avb_b) if head else None)
             rq = _roof("na_rpb_qk_fwd", qk_b, (2 * Dc * Kx + Kx) * rows, tq, FP32_PEAK_TFLOPS,
                        measured_traffic("na_rpb_qk_fwd", "cfg5") if (Kx, d) == (7, 1) else None)
             ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, ta, FP32_PEAK_TFLOPS,
                        measured_traffic("na_rpb_av_fwd", "cfg5") if (Kx, d) == (7, 1) else None)
-            table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd_ms": round(tqb["warm_ms"], 5),
-                                    "av_bwd_ms": round(tab["warm_ms"], 5)}
+            rqb = _roof("na_rpb_qk_bwd", qkb_b, (4 * Dc * Kx + Kx) * rows, tqb,
+                        FP32_PEAK_TFLOPS)
+            rab = _roof("na_rpb_av_bwd", avb_b, 4 * Dc * Kx * rows, tab, FP32_PEAK_TFLOPS)
+            table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd": rqb, "av_bwd": rab}
             if Kx == 7 and d == 1:
                 ms = tq["warm_ms"] + ta["warm_ms"]
                 best = (rq, ra, ms, (qk_b + av_b) / (ms * 1e-3) / 1e9, qk_b + av_b, rpb)
@@ -778,9 +943,22 @@ def wl_merge(args):
             part = rows * Dm * 2 + rows * 4
             fwd_b = (n + 1) * part
             bwd_b = (2 * n + 1) * part
-            tf = call_timing(lambda: hip.merge_forward(outs, lses))
+            head = name == "cfg3" and n == 2
+
+            def mf_set(i, outs=outs, lses=lses):
+                o, l = list(clones(*outs)), list(clones(*lses))
+                return lambda: hip.merge_forward(o, l)
+
+            def mb_set(i, outs=outs, lses=lses, n=n):
+                o, l = list(clones(*outs)), list(clones(*lses))
+                do_, dl_ = clones(dout, dlse)
+                return lambda: hip.merge_backward(o, l, do_, dl_, [True] * n, [True] * n)
+
+            tf = call_timing(lambda: hip.merge_forward(outs, lses),
+                             cold=(mf_set, fwd_b) if head else None)
             tb = call_timing(lambda: hip.merge_backward(outs, lses, dout, dlse, [True] * n,
-                                                        [True] * n))
+                                                        [True] * n),
+                             cold=(mb_set, bwd_b) if head else None)
             tt = call_timing(lambda: torch_merge(outs, lses))
             rf = _roof("na_merge_fwd", fwd_b, 2 * n * rows * Dm, tf, FP32_PEAK_TFLOPS)
             rb = _roof("na_merge_bwd", bwd_b, 4 * n * rows * Dm, tb, FP32_PEAK_TFLOPS)
