@@ -512,6 +512,47 @@ __device__ __forceinline__ void stage_box(const LProb &P, const LTile &t,
   zero_slack<T, D>(P, xs, tid, nthr);
 }
 
+// A slab of the box of two tensors staged in two steps, so its loads can be
+// in flight while the previous slab is computed: load() issues every unit
+// of the lane (two rounds of four, the units of stage_box) into registers,
+// store() writes them to LDS.  Used where a box is staged in several slabs
+// and two rounds cover a slab (ebox * D / 8 <= 8 * nthr).
+template <typename T, int D, int R>
+struct SlabPrefetch {
+  typedef typename L16<T>::v8 v8;
+  static constexpr int OCT = D / 8;
+  static constexpr int RSE = lds_row(D);
+  v8 x[2][4], y[2][4];
+  int la[2][4];
+  __device__ __forceinline__ void load(const LProb &P, const LTile &t,
+                                       const T *__restrict__ xg,
+                                       const T *__restrict__ yg, int tid, int nthr,
+                                       int s0) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      int g[4];
+      // a round past the layout clamps to its last row (real rows,
+      // rewritten with the same values)
+      unit_walk<R, OCT, RSE>(P, t, r * 4 * nthr, tid, nthr, s0, g, la[r]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[r][j] = ld8(xg, g[j]);
+        y[r][j] = ld8(yg, g[j]);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(typename L16<T>::e *xs,
+                                        typename L16<T>::e *ys) const {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<v8 *>(xs + la[r][j]) = x[r][j];
+        *reinterpret_cast<v8 *>(ys + la[r][j]) = y[r][j];
+      }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Host side.
 

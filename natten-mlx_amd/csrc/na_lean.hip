@@ -119,12 +119,19 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
 // and/or additional tokens (P.nx rows per sample of ek / ev, staged in LDS
 // before the box and attended after it); query rows of the tensor outside
 // their sample's extent get zero output and lse 0.
-template <typename T, int D, int R, bool CPR1, bool VX>
+// CA: some axis is causal; without one the window rules are the clamped
+// rule alone (the causal fields are known zero at compile time, so the
+// setup's selects between the two rules fold away).
+// PFS: the box is staged in several slabs and each slab's loads are issued
+// while the previous slab is computed (SlabPrefetch).
+template <typename T, int D, int R, bool CPR1, bool VX, bool CA, bool PFS>
 __global__ void __launch_bounds__(512)
-    k_wfwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
+    k_wfwd(LProb Pin, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, T *__restrict__ out,
            float *__restrict__ lse) {
+  LProb P = Pin;
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -260,11 +267,21 @@ __global__ void __launch_bounds__(512)
   // additional-token chunks, run after the last slab's box chunks; their
   // rows sit before the box (LDS rows -nxr .. -1 from ks)
   const int nxc = VX ? nxr >> 4 : 0;
+  SlabPrefetch<T, D, R> pf;
+  if constexpr (PFS) {  // one query head (no hl): the first slab's loads
+    pf.load(P, t, k, v, tid, nthr, 0);
+    zero_slack<T, D>(P, ks, tid, nthr);
+  }
   for (int si = 0; si < nsl; ++si) {
     const int s0 = si * P.sl;
     if (hr == 0) {  // with hl the whole box is one slab, staged once
       if (si > 0) __syncthreads();  // the previous slab's reads are done
-      stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+      if constexpr (PFS) {
+        pf.store(ks, vs);
+        if (si + 1 < nsl) pf.load(P, t, k, v, tid, nthr, s0 + P.sl);
+      } else {
+        stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+      }
       __syncthreads();
     }
     if (!ws.any) continue;
@@ -287,13 +304,14 @@ __global__ void __launch_bounds__(512)
         const bool ext = VX && !box && c < nch;
         bool ok = box;
         // closed forms: one box row (rank 1) or one chunk per row (rank 2,
-        // CPR1); otherwise the cursor
-        const int e1 = R == 2 && CPR1 ? ws.ws[1] + c : cc.e1;
+        // CPR1; rank 3, CPR1, whose slabs are one layer a0); otherwise the
+        // cursor
+        const int e1 = R >= 2 && CPR1 ? ws.ws[1] + c : cc.e1;
         const int cs = R == 1 ? c : CPR1 ? 0 : cc.cs;
         if (R > 1) ok = ok && (unsigned)(e1 - wl[1]) < (unsigned)ww[1];
-        if (R == 3) ok = ok && (unsigned)(cc.e0 - wl[0]) < (unsigned)ww[0];
+        if (R == 3) ok = ok && (unsigned)((CPR1 ? a0 : cc.e0) - wl[0]) < (unsigned)ww[0];
         const int krow = R == 1 ? key0 + 16 * c
-                         : R == 2 && CPR1 ? key0 + (c << P.lgP2)
+                         : CPR1 ? key0 + (c << P.lgP2)
                          : (((cc.e0 - s0) * Em1 + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs;
         float cb[4];
         if (CPR1 && !VX) {
@@ -309,7 +327,7 @@ __global__ void __launch_bounds__(512)
           ok = ok || ext;
         }
         sv[j] = mask_init(ok, cb);
-        if (R == 3 || (R == 2 && !CPR1)) advance(cc, ws);
+        if (R >= 2 && !CPR1) advance(cc, ws);
       }
       fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, lacc, ones, sl2, ka_off, tr_off);
     };
@@ -483,15 +501,17 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
 // box of the tile's keys (Q, dO, lse, delta) is staged and each wave
 // accumulates dK and dV of its 16 keys.  One workgroup per tile keeps the
 // whole launch resident at once.
-template <typename T, int D, int R, bool CPR1, bool VX>
+template <typename T, int D, int R, bool CPR1, bool VX, bool CA>
 __global__ void __launch_bounds__(512)
     __attribute__((amdgpu_waves_per_eu(D == 64 && R == 1 ? 4 : 1)))
-    k_wbwd(LProb P, const T *__restrict__ q, const T *__restrict__ k,
+    k_wbwd(LProb Pin, const T *__restrict__ q, const T *__restrict__ k,
            const T *__restrict__ v, const T *__restrict__ ek,
            const T *__restrict__ ev, const T *__restrict__ out,
            const float *__restrict__ lse, const T *__restrict__ dout,
            const float *__restrict__ dlse, T *__restrict__ dq,
            T *__restrict__ dk, T *__restrict__ dv, float *__restrict__ dlt) {
+  LProb P = Pin;
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -627,8 +647,9 @@ __global__ void __launch_bounds__(512)
       const int nchb = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
       const int nch = nchb + (si == nsl - 1 ? nxc : 0);
       const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
-      // a slab of one layer (rank 3): its chunks are the rows of layer a0
-      const bool layer = R == 3 && P.sl == 1;
+      // a slab of one layer (rank 3, CPR1: launched only with one-layer
+      // slabs): its chunks are the rows of layer a0
+      constexpr bool layer = R == 3 && CPR1;
       const bool l0ok = (unsigned)(a0 - wl[0]) < (unsigned)ww[0];
       Cursor cc{a0, ws.ws[1], 0};
       for (int c0 = 0; c0 < nch; c0 += 2) {
@@ -784,7 +805,7 @@ __global__ void __launch_bounds__(512)
     const int b0 = R == 3 ? min(ws.we[0], s0 + P.sl) : 1;
     const int nch = b0 > a0 ? (b0 - a0) * rows1 * ws.cpr : 0;
     const int key0 = (((a0 - s0) * Em1 + ws.ws[1]) << P.lgP2) + ws.ws[2];
-    const bool layer = R == 3 && P.sl == 1;
+    constexpr bool layer = R == 3 && CPR1;
     const bool l0ok = (unsigned)(a0 - wl[0]) < (unsigned)ww[0];
     Cursor cc{a0, ws.ws[1], 0};
     for (int c0 = 0; c0 < nch; c0 += 2) {
@@ -880,6 +901,16 @@ __global__ void __launch_bounds__(512)
 
 }  // namespace
 
+// NATTEN_AMD_NO_PFS=1 stages every slab after the previous one is computed
+// (A/B checks of the slab prefetch).
+bool slab_prefetch_off() {
+  static const bool off = [] {
+    const char *e = std::getenv("NATTEN_AMD_NO_PFS");
+    return e != nullptr && e[0] != '\0' && e[0] != '0';
+  }();
+  return off;
+}
+
 bool lean_eligible(const Prob &P, int dtype) {
   if (!lean_shape_ok(P, dtype)) return false;
   if (P.dense) return false;
@@ -956,12 +987,32 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
   const LProb L = lean_fwd_lprob(P, C);
   if (L.n_tiles == 0) return;
   const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
+  const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
+  // rank 3 staged in several slabs, one query head per box: each slab's
+  // loads fly while the previous slab is computed (two rounds of four
+  // units per lane must cover a slab)
+  // The prefetched units take up to ~250 VGPRs (two waves per SIMD), so only
+  // where the LDS already holds the launch to two workgroups per CU.
+  const size_t lds_f = lean_lds_bytes(P, kLFwd, L.ebox, C.W);
+  const bool pfs = P.rank == 3 && !vx && (C.Em[0] + C.sl - 1) / C.sl > 1 && !L.hl &&
+                   (int64_t)L.ebox * (P.D / 8) <= (int64_t)8 * 64 * C.W &&
+                   3 * lds_f > (size_t)160 * 1024 && C.W <= 4 && !slab_prefetch_off();
   const size_t lds = lean_lds_bytes(P, kLFwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
-#define LF_LAUNCH1(TT, DD, RR, CC, VV)                                          \
-  hipLaunchKernelGGL((k_wfwd<TT, DD, RR, CC, VV>), grid, block, lds, st, L,     \
+#define LF_LAUNCH2(TT, DD, RR, CC, VV, AA, PP)                                  \
+  hipLaunchKernelGGL((k_wfwd<TT, DD, RR, CC, VV, AA, PP>), grid, block, lds, st, L, \
                      (const TT *)q, (const TT *)k, (const TT *)v,              \
                      (const TT *)ek, (const TT *)ev, (TT *)out, lse)
+#define LF_LAUNCH1(TT, DD, RR, CC, VV)                                          \
+  do {                                                                        \
+    if (RR == 3 && !VV && pfs) {                                              \
+      if (ca) LF_LAUNCH2(TT, DD, RR, CC, VV, true, (RR == 3 && !VV));         \
+      else LF_LAUNCH2(TT, DD, RR, CC, VV, false, (RR == 3 && !VV));           \
+    } else {                                                                  \
+      if (ca) LF_LAUNCH2(TT, DD, RR, CC, VV, true, false);                    \
+      else LF_LAUNCH2(TT, DD, RR, CC, VV, false, false);                      \
+    }                                                                         \
+  } while (0)
 #define LF_LAUNCH(TT, DD, RR, CC)                                              \
   do {                                                                        \
     if (vx) LF_LAUNCH1(TT, DD, RR, CC, true);                                 \
@@ -973,7 +1024,7 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
     else if (P.rank == 2) {                                                   \
       if (C.cpr1) LF_LAUNCH(TT, DD, 2, true); else LF_LAUNCH(TT, DD, 2, false); \
     } else {                                                                  \
-      if (C.cpr1) LF_LAUNCH(TT, DD, 3, true); else LF_LAUNCH(TT, DD, 3, false); \
+      if (C.cpr1 && C.sl == 1) LF_LAUNCH(TT, DD, 3, true); else LF_LAUNCH(TT, DD, 3, false); \
     }                                                                         \
   } while (0)
 #define LF_D(DD)                          \
@@ -986,6 +1037,7 @@ void lean_fwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef LF_R
 #undef LF_LAUNCH
 #undef LF_LAUNCH1
+#undef LF_LAUNCH2
 }
 
 void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
@@ -999,11 +1051,20 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
   const size_t lds = lean_lds_bytes(P, kLBwd, L.ebox, C.W);
   const dim3 grid(L.n_launch), block(64 * C.W);
   const bool vx = P.sample_extent != nullptr || P.n_extra > 0;
+  const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
 #define LB_LAUNCH1(TT, DD, RR, CC, VV)                                          \
-  hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV>), grid, block, lds, st, L,    \
-                     (const TT *)q, (const TT *)k, (const TT *)v,              \
-                     (const TT *)ek, (const TT *)ev, (const TT *)out, lse,     \
-                     (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out)
+  do {                                                                        \
+    if (ca)                                                                   \
+      hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV, true>), grid, block, lds, st, L, \
+                         (const TT *)q, (const TT *)k, (const TT *)v,          \
+                         (const TT *)ek, (const TT *)ev, (const TT *)out, lse, \
+                         (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out); \
+    else                                                                      \
+      hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV, false>), grid, block, lds, st, L, \
+                         (const TT *)q, (const TT *)k, (const TT *)v,          \
+                         (const TT *)ek, (const TT *)ev, (const TT *)out, lse, \
+                         (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out); \
+  } while (0)
 #define LB_LAUNCH(TT, DD, RR, CC)                                             \
   do {                                                                        \
     if (vx) LB_LAUNCH1(TT, DD, RR, CC, true);                                 \
@@ -1015,7 +1076,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
     else if (P.rank == 2) {                                                   \
       if (C.cpr1) LB_LAUNCH(TT, DD, 2, true); else LB_LAUNCH(TT, DD, 2, false); \
     } else {                                                                  \
-      if (C.cpr1) LB_LAUNCH(TT, DD, 3, true); else LB_LAUNCH(TT, DD, 3, false); \
+      if (C.cpr1 && C.sl == 1) LB_LAUNCH(TT, DD, 3, true); else LB_LAUNCH(TT, DD, 3, false); \
     }                                                                         \
   } while (0)
 #define LB_D(DD)                          \
