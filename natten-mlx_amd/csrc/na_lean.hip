@@ -501,7 +501,9 @@ __device__ __forceinline__ void pair_rows(const WSub &ws, Cursor &cc, int c0,
 // box of the tile's keys (Q, dO, lse, delta) is staged and each wave
 // accumulates dK and dV of its 16 keys.  One workgroup per tile keeps the
 // whole launch resident at once.
-template <typename T, int D, int R, bool CPR1, bool VX, bool CA>
+// PFS: the dQ half's K / V box is staged in several slabs, each slab's loads
+// issued while the previous slab is computed (SlabPrefetch).
+template <typename T, int D, int R, bool CPR1, bool VX, bool CA, bool PFS>
 __global__ void __launch_bounds__(512)
     __attribute__((amdgpu_waves_per_eu(D == 64 && R == 1 ? 4 : 1)))
     k_wbwd(LProb Pin, const T *__restrict__ q, const T *__restrict__ k,
@@ -603,6 +605,11 @@ __global__ void __launch_bounds__(512)
     // slab is staged once for every query head of the group
     const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
     const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+    SlabPrefetch<T, D, R> pf;
+    if constexpr (PFS) {
+      pf.load(P, t, k, v, tid, nthr, 0);
+      zero_slack<T, D>(P, ks, tid, nthr);
+    }
     for (int hr = 0; hr < P.rep; ++hr) {
       const int hq = t.hk * P.rep + hr;
       bool qv;
@@ -637,7 +644,16 @@ __global__ void __launch_bounds__(512)
       const int s0 = si * P.sl;
       if (nsl > 1 || hr == 0) {
         if (hr > 0 || si > 0) __syncthreads();  // the previous slab's reads are done
-        stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+        if constexpr (PFS) {
+          pf.store(ks, vs);
+          // the next slab: of this head, else the first of the next head
+          if (si + 1 < nsl)
+            pf.load(P, t, k, v, tid, nthr, s0 + P.sl);
+          else if (hr + 1 < P.rep)
+            pf.load(P, t, k, v, tid, nthr, 0);
+        } else {
+          stage_box<T, D, R>(P, t, k, v, ks, vs, tid, nthr, s0);
+        }
         __syncthreads();
       }
       if (!ws.any) continue;
@@ -1052,18 +1068,24 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
   const dim3 grid(L.n_launch), block(64 * C.W);
   const bool vx = P.sample_extent != nullptr || P.n_extra > 0;
   const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
+  // the dQ half's K / V slabs prefetched (as in lean_fwd)
+  const bool pfs = P.rank == 3 && !vx && (C.Em[0] + C.sl - 1) / C.sl > 1 &&
+                   (int64_t)L.ebox * (P.D / 8) <= (int64_t)8 * 64 * C.W &&
+                   3 * lds > (size_t)160 * 1024 && C.W <= 4 && !slab_prefetch_off();
+#define LB_LAUNCH2(TT, DD, RR, CC, VV, AA, PP)                                  \
+  hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV, AA, PP>), grid, block, lds, st, L, \
+                     (const TT *)q, (const TT *)k, (const TT *)v,              \
+                     (const TT *)ek, (const TT *)ev, (const TT *)out, lse,     \
+                     (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out)
 #define LB_LAUNCH1(TT, DD, RR, CC, VV)                                          \
   do {                                                                        \
-    if (ca)                                                                   \
-      hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV, true>), grid, block, lds, st, L, \
-                         (const TT *)q, (const TT *)k, (const TT *)v,          \
-                         (const TT *)ek, (const TT *)ev, (const TT *)out, lse, \
-                         (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out); \
-    else                                                                      \
-      hipLaunchKernelGGL((k_wbwd<TT, DD, RR, CC, VV, false>), grid, block, lds, st, L, \
-                         (const TT *)q, (const TT *)k, (const TT *)v,          \
-                         (const TT *)ek, (const TT *)ev, (const TT *)out, lse, \
-                         (const TT *)dout, dlse, (TT *)dq, (TT *)dk, (TT *)dv, delta_out); \
+    if (RR == 3 && !VV && pfs) {                                              \
+      if (ca) LB_LAUNCH2(TT, DD, RR, CC, VV, true, (RR == 3 && !VV));         \
+      else LB_LAUNCH2(TT, DD, RR, CC, VV, false, (RR == 3 && !VV));           \
+    } else {                                                                  \
+      if (ca) LB_LAUNCH2(TT, DD, RR, CC, VV, true, false);                    \
+      else LB_LAUNCH2(TT, DD, RR, CC, VV, false, false);                      \
+    }                                                                         \
   } while (0)
 #define LB_LAUNCH(TT, DD, RR, CC)                                             \
   do {                                                                        \
@@ -1089,6 +1111,7 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
 #undef LB_R
 #undef LB_LAUNCH
 #undef LB_LAUNCH1
+#undef LB_LAUNCH2
 }
 
 }  // namespace na
