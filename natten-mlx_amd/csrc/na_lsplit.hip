@@ -131,7 +131,8 @@ struct ChunkPos {
 // Chunk ci of the walk; closed forms where the walk is one box row (rank 1)
 // or one chunk per row (rank 2, CPR1), otherwise the cursor (chunks in
 // order).
-template <int R, bool CPR1>
+// LAYER3: the caller stages rank-3 boxes one layer (s0) per slab.
+template <int R, bool CPR1, bool LAYER3 = false>
 __device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
                                               Cursor &cc, int ci, int nch,
                                               int s0, int key0, const int wl[3],
@@ -144,11 +145,14 @@ __device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
     c.e0 = 0;
     c.e1 = 0;
     c.col = ws.ws[2] + 16 * ci;
-  } else if (R == 2 && CPR1) {
+  } else if (CPR1 && (R == 2 || LAYER3)) {
+    // rank 2, or rank 3 whose slabs are one layer s0 (CPR1 rank-3 launches
+    // use one-layer slabs only)
     c.kb = key0 + (real ? ci << P.lgP2 : 0);
-    c.e0 = 0;
+    c.e0 = R == 3 ? s0 : 0;
     c.e1 = ws.ws[1] + ci;
     c.rok = real && (unsigned)(c.e1 - wl[1]) < (unsigned)ww[1];
+    if (R == 3) c.rok = c.rok && (unsigned)(c.e0 - wl[0]) < (unsigned)ww[0];
     c.col = ws.ws[2];
   } else {
     c.kb = real ? (((cc.e0 - s0) * P.ax[1].Em + cc.e1) << P.lgP2) + ws.ws[2] + 16 * cc.cs
@@ -171,10 +175,12 @@ __device__ __forceinline__ ChunkPos chunk_pos(const LProb &P, const WSub &ws,
 // 4 (l / 16) + r), each in-window score to its slot of the query's row in
 // LDS; then the rows to HBM.  FILL: some slots lie outside every window
 // (a causal axis) and start as `fill`.
-template <typename T, int D, int R, bool CPR1>
+template <typename T, int D, int R, bool CPR1, bool CA>
 __global__ void __launch_bounds__(512)
-    k_lqk(LProb P, const T *__restrict__ x, const T *__restrict__ y,
+    k_lqk(LProb Pin, const T *__restrict__ x, const T *__restrict__ y,
           T *__restrict__ out, float scale, float fill, int prefill) {
+  LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::e E;
@@ -226,7 +232,7 @@ __global__ void __launch_bounds__(512)
       ChunkPos cp[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
+        cp[j] = chunk_pos<R, CPR1, true>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
       v8 ka[NB][NT];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
@@ -275,11 +281,13 @@ __global__ void __launch_bounds__(512)
 // sub-box, so nothing is shared through LDS and no barrier precedes the
 // products); scores go to the LDS row buffer branch-free (out-of-window
 // lanes write a per-lane spare slot past the rows).
-template <typename T, int D, int R, bool CPR1, int VW>
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
 __global__ void __launch_bounds__(1024)
-    k_lqh(LProb P, const T *__restrict__ x, const T *__restrict__ y,
+    k_lqh(LProb Pin, const T *__restrict__ x, const T *__restrict__ y,
           T *__restrict__ out, float scale, float fill, int prefill,
           FastDiv fups) {
+  LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::e E;
@@ -408,10 +416,12 @@ __global__ void __launch_bounds__(1024)
 // stages the Y rows of its own chunks (a group at a time) in a private LDS
 // area for the transposing read, so only the compact rows pass a
 // workgroup barrier.
-template <typename T, int D, int R, bool CPR1, int VW>
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
 __global__ void __launch_bounds__(1024)
-    k_lah(LProb P, const T *__restrict__ a, const T *__restrict__ y,
+    k_lah(LProb Pin, const T *__restrict__ a, const T *__restrict__ y,
           T *__restrict__ out, float scale, FastDiv fups) {
+  LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -556,10 +566,12 @@ __global__ void __launch_bounds__(1024)
 // operand (query n, keys 4 (l / 16) + r of each chunk) is gathered from them
 // by slot (zero outside the window) and O^T += Y^T . A^T with Y^T through
 // the transposing LDS read.
-template <typename T, int D, int R, bool CPR1>
+template <typename T, int D, int R, bool CPR1, bool CA>
 __global__ void __launch_bounds__(512)
-    k_lav(LProb P, const T *__restrict__ a, const T *__restrict__ y,
+    k_lav(LProb Pin, const T *__restrict__ a, const T *__restrict__ y,
           T *__restrict__ out, float scale) {
+  LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -627,7 +639,7 @@ __global__ void __launch_bounds__(512)
       ChunkPos cp[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
+        cp[j] = chunk_pos<R, CPR1, true>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
       v8 bp[NB / 2];
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
@@ -671,10 +683,12 @@ __global__ void __launch_bounds__(512)
 // key, S(q) = sum_a s_a(q) st_a), and Z^T += X^T . A with X^T through the
 // transposing LDS read.  The gathers of a group of chunk pairs are issued
 // together; every compact-row element is read by exactly one key.
-template <typename T, int D, int R, bool CPR1>
+template <typename T, int D, int R, bool CPR1, bool CA>
 __global__ void __launch_bounds__(512)
-    k_linv(LProb P, const T *__restrict__ a, const T *__restrict__ x,
+    k_linv(LProb Pin, const T *__restrict__ a, const T *__restrict__ x,
            T *__restrict__ z, float scale) {
+  LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
+  if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -736,7 +750,7 @@ __global__ void __launch_bounds__(512)
         v8 bp[NP];
 #pragma unroll
         for (int j = 0; j < 2 * NP; ++j) {
-          cp[j] = chunk_pos<R, CPR1>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
+          cp[j] = chunk_pos<R, CPR1, true>(P, ws, cc, c0 + j, nch, s0, key0, wl, ww);
           // the chunk's row: slot-base and token parts of axes 0 and 1
           int sb01 = 0, tok01 = t.b * P.Ltot + t.r[2];
           if (R == 3) {
@@ -812,8 +826,12 @@ bool lsplit_eligible(const Prob &P, int dtype) {
       typedef decltype(tt) TT;                                                  \
       constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;         \
       constexpr bool CC = decltype(cc)::value;                                  \
-      hipLaunchKernelGGL((KERNEL<TT, DD, RR, CC>), grid, block, lds, st, L,     \
-                         ARGS);                                                 \
+      if (ca)                                                                   \
+        hipLaunchKernelGGL((KERNEL<TT, DD, RR, CC, true>), grid, block, lds, st, L, \
+                           ARGS);                                               \
+      else                                                                      \
+        hipLaunchKernelGGL((KERNEL<TT, DD, RR, CC, false>), grid, block, lds, st, L, \
+                           ARGS);                                               \
     };                                                                          \
     auto by_r = [&](auto tt, auto dd) {                                         \
       if (P.rank == 1)                                                          \
@@ -822,7 +840,7 @@ bool lsplit_eligible(const Prob &P, int dtype) {
         if (C.cpr1) go(tt, dd, std::integral_constant<int, 2>(), std::true_type()); \
         else go(tt, dd, std::integral_constant<int, 2>(), std::false_type());   \
       } else {                                                                  \
-        if (C.cpr1) go(tt, dd, std::integral_constant<int, 3>(), std::true_type()); \
+        if (C.cpr1 && C.sl == 1) go(tt, dd, std::integral_constant<int, 3>(), std::true_type()); \
         else go(tt, dd, std::integral_constant<int, 3>(), std::false_type());   \
       }                                                                         \
     };                                                                          \
@@ -853,6 +871,7 @@ bool lqh_plan(const Prob &P, LqhPlan *pl) {
 
 void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
                void *out, float scale, float fill, hipStream_t st) {
+  const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
   const LChoice C = lean_choice(P, kLQK);
   int prefill = 0;
   for (int a = 0; a < 3; ++a) prefill |= P.ax[a].causal;
@@ -872,9 +891,14 @@ void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
       constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;
       constexpr bool CC = decltype(cc)::value;
       constexpr int VV = decltype(vv)::value;
-      hipLaunchKernelGGL((k_lqh<TT, DD, RR, CC, VV>), grid, block, lds, st, L,
-                         (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill,
-                         fups);
+      if (ca)
+        hipLaunchKernelGGL((k_lqh<TT, DD, RR, CC, VV, true>), grid, block, lds, st, L,
+                           (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill,
+                           fups);
+      else
+        hipLaunchKernelGGL((k_lqh<TT, DD, RR, CC, VV, false>), grid, block, lds, st, L,
+                           (const TT *)x, (const TT *)y, (TT *)out, scale, fill, prefill,
+                           fups);
     };
     auto by_v = [&](auto tt, auto dd, auto rr, auto cc) {
       if (pl.vw == 8) go(tt, dd, rr, cc, std::integral_constant<int, 8>());
@@ -889,7 +913,7 @@ void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
         if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 2>(), std::true_type());
         else by_v(tt, dd, std::integral_constant<int, 2>(), std::false_type());
       } else {
-        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
+        if (C.cpr1 && C.sl == 1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
         else by_v(tt, dd, std::integral_constant<int, 3>(), std::false_type());
       }
     };
@@ -913,6 +937,7 @@ void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
 
 void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
                void *out, float scale, hipStream_t st) {
+  const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
   const LChoice C = lean_choice(P, kLQK);
   LqhPlan pl;
   // k_lah's LDS: the tile's compact rows and, per wave, NB chunks of 16 rows
@@ -933,8 +958,12 @@ void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
       constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;
       constexpr bool CC = decltype(cc)::value;
       constexpr int VV = decltype(vv)::value;
-      hipLaunchKernelGGL((k_lah<TT, DD, RR, CC, VV>), grid, block, lah_lds, st, L,
-                         (const TT *)a, (const TT *)y, (TT *)out, scale, fups);
+      if (ca)
+        hipLaunchKernelGGL((k_lah<TT, DD, RR, CC, VV, true>), grid, block, lah_lds, st, L,
+                           (const TT *)a, (const TT *)y, (TT *)out, scale, fups);
+      else
+        hipLaunchKernelGGL((k_lah<TT, DD, RR, CC, VV, false>), grid, block, lah_lds, st, L,
+                           (const TT *)a, (const TT *)y, (TT *)out, scale, fups);
     };
     auto by_v = [&](auto tt, auto dd, auto rr, auto cc) {
       if (pl.vw == 8) go(tt, dd, rr, cc, std::integral_constant<int, 8>());
@@ -949,7 +978,7 @@ void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
         if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 2>(), std::true_type());
         else by_v(tt, dd, std::integral_constant<int, 2>(), std::false_type());
       } else {
-        if (C.cpr1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
+        if (C.cpr1 && C.sl == 1) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
         else by_v(tt, dd, std::integral_constant<int, 3>(), std::false_type());
       }
     };
@@ -973,6 +1002,7 @@ void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
 
 void lsplit_inv(const Prob &P, int dtype, const void *a, const void *x,
                 void *z, float scale, hipStream_t st) {
+  const bool ca = P.ax[0].causal || P.ax[1].causal || P.ax[2].causal;
   const LChoice C = lean_choice(P, kLInv);
   LProb L = make_lprob(P, C);
   L.n_tiles = P.B * P.Hkv * (int)L.fGrid.d;
