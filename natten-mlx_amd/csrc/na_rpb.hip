@@ -446,10 +446,10 @@ __host__ __device__ __forceinline__ int r1_halo(int K, int d, int step) {
 // layout (a row of a lower position may carry a higher head).  Otherwise
 // the rows widened by (K - 1) d positions per side (same head).
 template <int K>
-__device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step) {
+__device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step, int bid) {
   R1Rows o;
   const int nthr = (int)blockDim.x;
-  const int row0 = (int)blockIdx.x * nthr;
+  const int row0 = bid * nthr;
   o.rows = min(nthr, A.n_rows - row0);
   o.r = row0 + min((int)threadIdx.x, o.rows - 1);
   if (A.d0 == 1) {
@@ -491,14 +491,15 @@ struct R1Copy {
 // logits / dattn: out[r, k] = <x'[r], y[nbr(r, k)]> (+ bias); every slot is
 // inside its window here, so no slot takes the `fill` value.
 template <int K, int NC>
-__global__ void __launch_bounds__(512)
-    k_r1_dot(RpbProb A, const float *__restrict__ x, const float *__restrict__ y,
-             const float *__restrict__ rpb, float *__restrict__ out,
-             int scale_x) {
+__device__ __forceinline__ void r1_dot_body(int bid, const RpbProb &A,
+                                            const float *__restrict__ x,
+                                            const float *__restrict__ y,
+                                            const float *__restrict__ rpb,
+                                            float *__restrict__ out, int scale_x) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int step = A.heads_first ? 1 : A.H;
-  const R1Rows b = r1_rows<K>(A, step);
+  const R1Rows b = r1_rows<K>(A, step, bid);
   float *so = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   constexpr int R0 = 2 * K - 1;
@@ -551,19 +552,29 @@ __global__ void __launch_bounds__(512)
     sr[k] = acc;
   }
   __syncthreads();
-  block_copy_f32<true>(out + (int64_t)blockIdx.x * nthr * K, so, (int64_t)b.rows * K);
+  block_copy_f32<true>(out + (int64_t)bid * nthr * K, so, (int64_t)b.rows * K);
+}
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1_dot(RpbProb A, const float *__restrict__ x, const float *__restrict__ y,
+             const float *__restrict__ rpb, float *__restrict__ out,
+             int scale_x) {
+  r1_dot_body<K, NC>((int)blockIdx.x, A, x, y, rpb, out, scale_x);
 }
 
 // AV / dq: out[r] = post * sum_k w[r, k] * y[nbr(r, k)] over valid slots.
+// nblk: blocks of this pass (the bias partials' stride).
 template <int K, int NC>
-__global__ void __launch_bounds__(512)
-    k_r1_gather(RpbProb A, const float *__restrict__ wgt,
-                const float *__restrict__ y, float *__restrict__ out,
-                float post, double *__restrict__ bpart) {
+__device__ __forceinline__ void r1_gather_body(int bid, int nblk, const RpbProb &A,
+                                               const float *__restrict__ wgt,
+                                               const float *__restrict__ y,
+                                               float *__restrict__ out, float post,
+                                               double *__restrict__ bpart) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int step = A.heads_first ? 1 : A.H;
-  const R1Rows b = r1_rows<K>(A, step);
+  const R1Rows b = r1_rows<K>(A, step, bid);
   float *sw = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   // every load of the prologue is issued before any is waited on: the
@@ -571,7 +582,7 @@ __global__ void __launch_bounds__(512)
   // units plus a tail of floats, and the window's first units
   constexpr int JW = (K + 3) / 4;  // weight units per thread (rows <= nthr)
   const int nwf = b.rows * K, nw4 = nwf >> 2;
-  const float *wg = wgt + (int64_t)blockIdx.x * nthr * K;
+  const float *wg = wgt + (int64_t)bid * nthr * K;
   const uint4 *ysrc = reinterpret_cast<const uint4 *>(y) + (int64_t)b.lo * NC;
   const int nwin = (b.hi - b.lo) * NC;
   // without a whole weight unit the unit loads read the window instead and
@@ -623,14 +634,14 @@ __global__ void __launch_bounds__(512)
     constexpr int R0 = 2 * K - 1;
     if (tid < A.H * R0) {
       const int h = tid / R0, c = tid - h * R0;
-      const int row0 = (int)blockIdx.x * nthr;
+      const int row0 = bid * nthr;
       const int h0 = row0 - (int)fdiv((uint32_t)row0, A.fH) * A.H;
       double acc_b = 0.0;
       for (int j = h >= h0 ? h - h0 : h - h0 + A.H; j < b.rows; j += A.H) {
         const int k = c - spb[j];
         if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
       }
-      bpart[(int64_t)tid * gridDim.x + blockIdx.x] = acc_b;
+      bpart[(int64_t)tid * nblk + bid] = acc_b;
     }
   }
   // the block's output rows are one contiguous range: write them through
@@ -647,8 +658,16 @@ __global__ void __launch_bounds__(512)
     sm4[tid * NC + c] = o;
   }
   __syncthreads();
-  block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)blockIdx.x * nthr * NC,
+  block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)bid * nthr * NC,
                reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
+}
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1_gather(RpbProb A, const float *__restrict__ wgt,
+                const float *__restrict__ y, float *__restrict__ out,
+                float post, double *__restrict__ bpart) {
+  r1_gather_body<K, NC>((int)blockIdx.x, (int)gridDim.x, A, wgt, y, out, post, bpart);
 }
 
 // ---- rank 1, spatial-first, dilation d > 1: rows in phase-major order ----
@@ -866,13 +885,14 @@ __global__ void __launch_bounds__(512)
 // window rule, and writes its output rows through LDS as consecutive
 // 16-byte units (streaming stores).
 template <int K, int NC, bool D1>
-__global__ void __launch_bounds__(512)
-    k_r1_inverse(RpbProb A, const float *__restrict__ w,
-                 const float *__restrict__ x, float *__restrict__ out, float post) {
+__device__ __forceinline__ void r1_inverse_body(int bid, const RpbProb &A,
+                                                const float *__restrict__ w,
+                                                const float *__restrict__ x,
+                                                float *__restrict__ out, float post) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int step = A.heads_first ? 1 : A.H;
-  const int row0 = (int)blockIdx.x * nthr;
+  const int row0 = bid * nthr;
   const int rows = min(nthr, A.n_rows - row0);
   const int r = row0 + min(tid, rows - 1);
   const int reach = (K - 1) * A.d0 * step;
@@ -915,6 +935,33 @@ __global__ void __launch_bounds__(512)
   float4 acc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto add = [&](float wk, const float4 *xr) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 v = xr[c];
+      acc[c].x = fmaf(wk, v.x, acc[c].x);
+      acc[c].y = fmaf(wk, v.y, acc[c].y);
+      acc[c].z = fmaf(wk, v.z, acc[c].z);
+      acc[c].w = fmaf(wk, v.w, acc[c].w);
+    }
+  };
+  // d = 1, every key of the block at a position j in [K, L - K - 1] of one
+  // sequence (block-uniform): the queries holding j are exactly j - K/2 ..
+  // j + K/2, each with j at slot K/2 - (i - j) (their windows are unclamped),
+  // so the K candidates need no window test
+  bool interior = false;
+  if (D1) {
+    const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)(row0 + rows - 1));
+    interior = pf.b == pl.b && pf.h == (A.heads_first ? pl.h : pf.h) && pf.i0 >= K &&
+               pl.i0 <= A.L0 - K - 1;
+  }
+  if (interior) {
+#pragma unroll
+    for (int t = -(K / 2); t <= K / 2; ++t) {
+      const int sr = r - lo + t * step;
+      add(ws[wrow0 + sr * K + (K / 2 - t)], xs + sr * NC);
+    }
+  } else {
   // four candidates per step keep the loads in flight without holding all
   // 2K - 1 candidates' rows in registers
 #pragma unroll 4
@@ -934,15 +981,8 @@ __global__ void __launch_bounds__(512)
     }
     const int sr = r - lo + t * A.d0 * step;  // the candidate's staged row
     const float wk = ok ? ws[wrow0 + sr * K + k] : 0.f;
-    const float4 *xr = xs + (ok ? sr : r - lo) * NC;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float4 v = xr[c];
-      acc[c].x = fmaf(wk, v.x, acc[c].x);
-      acc[c].y = fmaf(wk, v.y, acc[c].y);
-      acc[c].z = fmaf(wk, v.z, acc[c].z);
-      acc[c].w = fmaf(wk, v.w, acc[c].w);
-    }
+    add(wk, xs + (ok ? sr : r - lo) * NC);
+  }
   }
   __syncthreads();
 #pragma unroll
@@ -957,6 +997,42 @@ __global__ void __launch_bounds__(512)
   __syncthreads();
   block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)row0 * NC,
                      reinterpret_cast<const uint4 *>(sm4), (int64_t)rows * NC);
+}
+
+template <int K, int NC, bool D1>
+__global__ void __launch_bounds__(512)
+    k_r1_inverse(RpbProb A, const float *__restrict__ w,
+                 const float *__restrict__ x, float *__restrict__ out, float post) {
+  r1_inverse_body<K, NC, D1>((int)blockIdx.x, A, w, x, out, post);
+}
+
+// The two passes of a backward in one launch (they are independent): blocks
+// [0, n0) run the first pass, the others the inverse (dk or dv).  QK
+// backward: dq by the gather over dlogits (with the bias partials when bpart
+// is set) and dk; AV backward: dattn by the dot of dout with the values and
+// dv.
+template <int K, int NC, bool D1>
+__global__ void __launch_bounds__(512)
+    k_r1_qkb(RpbProb A, const float *__restrict__ dl, const float *__restrict__ q,
+             const float *__restrict__ key, float *__restrict__ dq,
+             float *__restrict__ dk, float post, double *__restrict__ bpart, int n0) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    r1_gather_body<K, NC>(bid, n0, A, dl, key, dq, post, bpart);
+  else
+    r1_inverse_body<K, NC, D1>(bid - n0, A, dl, q, dk, post);
+}
+
+template <int K, int NC, bool D1>
+__global__ void __launch_bounds__(512)
+    k_r1_avb(RpbProb A, const float *__restrict__ attn, const float *__restrict__ v,
+             const float *__restrict__ dout, float *__restrict__ dattn,
+             float *__restrict__ dv, int n0) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    r1_dot_body<K, NC>(bid, A, dout, v, nullptr, dattn, 0);
+  else
+    r1_inverse_body<K, NC, D1>(bid - n0, A, attn, dout, dv, 1.f);
 }
 
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
@@ -1272,6 +1348,16 @@ size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes, int rb) {
 // with 32-bit integers: a row index times K or head_dim must stay below
 // 2^31 (larger problems take the generic kernels, whose row offsets are
 // 64-bit).
+// NATTEN_AMD_RPB_PAIR=0 keeps the backward's two passes in two launches
+// (A/B checks of k_r1_qkb / k_r1_avb).
+bool pair_launch_off() {
+  static const bool off = [] {
+    const char *e = std::getenv("NATTEN_AMD_RPB_PAIR");
+    return e != nullptr && e[0] == '0';
+  }();
+  return off;
+}
+
 bool r1_offsets_fit(const RpbProb &A) {
   return (int64_t)A.n_rows * std::max(A.K0, A.D) < ((int64_t)1 << 31);
 }
@@ -1354,14 +1440,17 @@ size_t r1_bias_gather_lds(const RpbProb &A) {
   const size_t b = lds + (size_t)rb * sizeof(int);
   return b <= 65536 ? b : 0;
 }
-// LDS of the staged inverse (dk / dv), or 0 where it does not apply.
+// LDS of the staged inverse (dk / dv), or 0 where it does not apply.  Up
+// to 80 KB (two blocks per CU): the candidate queries' rows of dilated
+// windows (K = 7 at d = 4 takes 73 KB for 384 keys).
+constexpr size_t kR1InvLds = 80 * 1024;
 size_t r1_inverse_lds(const RpbProb &A) {
   const int rb = rpb_block(A);
   if (r1_lds(A, rb, false) == 0) return 0;
   const int step = A.heads_first ? 1 : A.H;
   const size_t cap = (size_t)rb + 2 * (size_t)r1_halo(A.K0, A.d0, step);
   const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
-  return lds <= 65536 ? lds : 0;
+  return lds <= kR1InvLds ? lds : 0;
 }
 
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
@@ -1509,6 +1598,86 @@ bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
 }
 #undef R1_K
 
+// The QK / AV backward's two passes in one launch (k_r1_qkb / k_r1_avb)
+// where both run on the staged rank-1 fp32 kernels; false otherwise.
+#define R1_KD(KK_, BODY)                 \
+  switch (KK_) {                         \
+    case 3: BODY(3); break;              \
+    case 5: BODY(5); break;              \
+    case 7: BODY(7); break;              \
+    case 9: BODY(9); break;              \
+    case 11: BODY(11); break;            \
+    default: BODY(13); break;            \
+  }
+bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const float *key,
+                     float *dq, float *dk, double *bpart, hipStream_t st) {
+  if (pair_launch_off()) return false;
+  const size_t lg = bpart != nullptr ? r1_bias_gather_lds(A) : r1_lds(A, rpb_block(A), false);
+  const size_t li = r1_inverse_lds(A);
+  // the pair shares one LDS size: an inverse above 64 KB would hold the
+  // gather's blocks to two per CU too (K = 7, d = 4: 26.4 us as two
+  // launches, 29.9 us as one)
+  if (lg == 0 || li == 0 || li > 65536) return false;
+  const int rb = rpb_block(A);
+  const int n0 = (A.n_rows + rb - 1) / rb;
+  const dim3 grid((unsigned)(2 * n0)), block(rb);
+  const size_t lds = std::max(lg, li);
+  const float post = A.has_scale ? A.scale : 1.f;
+#define QKB_(KK, NC)                                                                   \
+  do {                                                                                 \
+    if (A.d0 == 1)                                                                     \
+      hipLaunchKernelGGL((k_r1_qkb<KK, NC, true>), grid, block, lds, st, A, dl, q, key, \
+                         dq, dk, post, bpart, n0);                                     \
+    else                                                                               \
+      hipLaunchKernelGGL((k_r1_qkb<KK, NC, false>), grid, block, lds, st, A, dl, q, key, \
+                         dq, dk, post, bpart, n0);                                     \
+  } while (0)
+#define QKB_NC(KK)                                  \
+  do {                                              \
+    if (A.D == 4) QKB_(KK, 1);                      \
+    else if (A.D == 8) QKB_(KK, 2);                 \
+    else if (A.D == 12) QKB_(KK, 3);                \
+    else QKB_(KK, 4);                               \
+  } while (0)
+  R1_KD(A.K0, QKB_NC);
+#undef QKB_NC
+#undef QKB_
+  return true;
+}
+
+bool r1_av_bwd_fused(const RpbProb &A, const float *attn, const float *v, const float *dout,
+                     float *dattn, float *dv, hipStream_t st) {
+  if (pair_launch_off()) return false;
+  const int rb = rpb_block(A);
+  const size_t ld = r1_lds(A, rb, false);
+  const size_t li = r1_inverse_lds(A);
+  if (ld == 0 || li == 0) return false;
+  const int n0 = (A.n_rows + rb - 1) / rb;
+  const dim3 grid((unsigned)(2 * n0)), block(rb);
+  const size_t lds = std::max(ld, li);
+#define AVB_(KK, NC)                                                                   \
+  do {                                                                                 \
+    if (A.d0 == 1)                                                                     \
+      hipLaunchKernelGGL((k_r1_avb<KK, NC, true>), grid, block, lds, st, A, attn, v,    \
+                         dout, dattn, dv, n0);                                         \
+    else                                                                               \
+      hipLaunchKernelGGL((k_r1_avb<KK, NC, false>), grid, block, lds, st, A, attn, v,   \
+                         dout, dattn, dv, n0);                                         \
+  } while (0)
+#define AVB_NC(KK)                                  \
+  do {                                              \
+    if (A.D == 4) AVB_(KK, 1);                      \
+    else if (A.D == 8) AVB_(KK, 2);                 \
+    else if (A.D == 12) AVB_(KK, 3);                \
+    else AVB_(KK, 4);                               \
+  } while (0)
+  R1_KD(A.K0, AVB_NC);
+#undef AVB_NC
+#undef AVB_
+  return true;
+}
+#undef R1_KD
+
 template <typename TX, typename TY>
 void launch_dot(const RpbProb &A, const void *x, const void *y,
                 const float *rpb, float *out, int scale_x, float fill,
@@ -1638,7 +1807,18 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
   // fp32 rank 1 on the staged kernels: the dq pass also writes the bias
   // gradient's partials, one per block (when they fit the workspace)
   int32_t n_fused = 0;
-  if (drpb != nullptr && dq != nullptr && dtype == NA_F32 && A.n_rows > 0) {
+  bool pair = false;  // dq and dk in one launch
+  if (dq != nullptr && dk != nullptr && dtype == NA_F32 && A.n_rows > 0) {
+    const int32_t nblk = (A.n_rows + rpb_block(A) - 1) / rpb_block(A);
+    const bool bias = drpb != nullptr && nblk <= n_chunks;
+    if ((drpb == nullptr || bias) &&
+        r1_qk_bwd_fused(A, dlogits, (const float *)q, (const float *)key, (float *)dq,
+                        (float *)dk, bias ? (double *)workspace : nullptr, st)) {
+      pair = true;
+      if (bias) n_fused = nblk;
+    }
+  }
+  if (!pair && drpb != nullptr && dq != nullptr && dtype == NA_F32 && A.n_rows > 0) {
     const int32_t nblk = (A.n_rows + rpb_block(A) - 1) / rpb_block(A);
     if (nblk <= n_chunks &&
         r1_gather(A, dlogits, (const float *)key, (float *)dq, A.has_scale ? A.scale : 1.f,
@@ -1647,7 +1827,7 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
   }
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (A.n_rows == 0) return;
+    if (A.n_rows == 0 || pair) return;
     if (dq != nullptr && n_fused == 0)
       launch_gather<T, T>(A, dlogits, key, dq, A.has_scale ? A.scale : 1.f,
                           st);
@@ -1691,6 +1871,11 @@ void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
 void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
                 const void *value, const void *dout, float *dattn, void *dvalue,
                 hipStream_t st) {
+  // fp32 (dout fp32 whatever out_dtype): dattn and dv in one launch
+  if (dtype == NA_F32 && dattn != nullptr && dvalue != nullptr && A.n_rows > 0 &&
+      r1_av_bwd_fused(A, attn, (const float *)value, (const float *)dout, dattn,
+                      (float *)dvalue, st))
+    return;
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     if (out_dtype == NA_F32) {
