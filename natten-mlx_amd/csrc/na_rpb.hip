@@ -945,20 +945,24 @@ __device__ __forceinline__ void r1_inverse_body(int bid, const RpbProb &A,
       acc[c].w = fmaf(wk, v.w, acc[c].w);
     }
   };
-  // d = 1, every key of the block at a position j in [K, L - K - 1] of one
-  // sequence (block-uniform): the queries holding j are exactly j - K/2 ..
-  // j + K/2, each with j at slot K/2 - (i - j) (their windows are unclamped),
-  // so the K candidates need no window test
-  bool interior = false;
-  if (D1) {
+  // every key of the block at a position j in [K d, L - 1 - K d] of one
+  // sequence (block-uniform): j's phase index m and the phase indices m + t,
+  // |t| <= K/2, of the queries j + t d lie at least K from both ends of the
+  // phase, so those queries' windows are unclamped ([m + t - K/2, m + t +
+  // K/2], holding j at slot K/2 - t) and every other query's window (of the
+  // same phase: unclamped and more than K/2 away, or clamped to the first
+  // or last K indices) misses j; the K candidates need no window test
+  bool interior;
+  {
     const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)(row0 + rows - 1));
-    interior = pf.b == pl.b && pf.h == (A.heads_first ? pl.h : pf.h) && pf.i0 >= K &&
-               pl.i0 <= A.L0 - K - 1;
+    const int kd = K * A.d0;
+    interior = pf.b == pl.b && pf.h == (A.heads_first ? pl.h : pf.h) && pf.i0 >= kd &&
+               pl.i0 <= A.L0 - 1 - kd;
   }
   if (interior) {
 #pragma unroll
     for (int t = -(K / 2); t <= K / 2; ++t) {
-      const int sr = r - lo + t * step;
+      const int sr = r - lo + t * A.d0 * step;
       add(ws[wrow0 + sr * K + (K / 2 - t)], xs + sr * NC);
     }
   } else {

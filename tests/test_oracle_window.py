@@ -145,3 +145,21 @@ def test_inverse_range_closed_form():
                         qlo = 0 if j <= K - 1 else j - K // 2
                         qhi = Lr - 1 if j >= Lr - K else j + K // 2
                         assert inv == list(range(qlo, qhi + 1)), (L, K, d, r, j)
+
+
+def test_allin1_interior_keys():
+    """The allin1 staged inverse's fast path: with K*d <= L (odd K), a key
+    at position j in [K*d, L - 1 - K*d] lies in the partition window of
+    exactly the queries j + t*d, |t| <= K//2, at slot K//2 - t (checked
+    against every query's window, not derived from the claim)."""
+    for L in range(1, 72):
+        for K in range(1, L + 1, 2):
+            for d in range(1, L // K + 1):
+                held = {}
+                for i in range(L):
+                    s = W.window_start_partition(i, L, K, K // 2, d)
+                    for slot in range(K):
+                        held.setdefault(s + slot * d, []).append((i, slot))
+                for j in range(K * d, L - K * d):
+                    want = sorted((j + t * d, K // 2 - t) for t in range(-(K // 2), K // 2 + 1))
+                    assert sorted(held.get(j, [])) == want, (L, K, d, j)
