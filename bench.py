@@ -323,13 +323,21 @@ def cpu_median(fn, budget_s: float = 10.0, min_runs: int = 3, max_runs: int = 50
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, then family /
+    model / stepping, which a virtualised name like "AMD EPYC" leaves out)
+    and the logical CPUs the host shows."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block is enough
+            k, _, v = line.partition(":")
+            fields.setdefault(k.strip(), v.strip())
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids}; {os.cpu_count()} logical CPUs on the host)" if ids else name
 
 
 def _cpu_line(value, unit, threads, sample, runs, wall, per_step_s):
@@ -426,15 +434,22 @@ PROFILE_SUMMARIES = {
     "cfg2": [os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_hbm_traffic.md"),
              os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_lean_fwd_bwd.md")],
     "cfg3": [os.path.join(ROOT, "profiles", "na3d_16x32x32_k377_causal_bf16_lean_fwd_bwd.md")],
+    "cfg4": [os.path.join(ROOT, "profiles", "na1d_varlen_gqa_cfg4_fp16_fwd_bwd.md")],
     "cfg5": [os.path.join(ROOT, "profiles", "allin1_1d_2048x12_k7_f32_rpb.md")],
+    "split": [os.path.join(ROOT, "profiles", "na2d_56x56_k7_bf16_split_lean.md")],
 }
 CALL_KERNEL = {"na_fwd": "k_wfwd", "na_bwd": "k_wbwd", "na_rpb_qk_fwd": "k_r1_dot",
-               "na_rpb_av_fwd": "k_r1_gather"}
+               "na_rpb_av_fwd": "k_r1_gather", "na_qk_fwd": "k_lqh", "na_av_fwd": "k_lah",
+               "na_rpb_qk_bwd": "k_r1_qkb", "na_rpb_av_bwd": "k_r1_avb"}
 
 
-def _profile_figure(key: str, call: str, workload: str, kind):
-    """A per-kernel figure (``<key> <kernel> <value>`` lines) from the
-    committed rocprofv3 counter summaries of the workload, or None."""
+def _profile_figure(key: str, call_key: str, call: str, workload: str, kind):
+    """A figure of the call from the committed rocprofv3 counter summaries of
+    the workload, or None: a ``<call_key> <call> <value>`` line (calls of
+    several kernels: the figure over all of them), else a ``<key> <kernel>
+    <value>`` line of the call's one kernel."""
+    want = [(call_key, call), (key, CALL_KERNEL.get(call))]
+    found = {}
     for path in PROFILE_SUMMARIES.get(workload, []):
         try:
             text = open(path).read()
@@ -442,21 +457,25 @@ def _profile_figure(key: str, call: str, workload: str, kind):
             continue
         for line in text.splitlines():
             parts = line.split()
-            if len(parts) == 3 and parts[0] == key and parts[1] == CALL_KERNEL.get(call):
-                return kind(parts[2])
+            if len(parts) == 3 and (parts[0], parts[1]) in want:
+                found.setdefault((parts[0], parts[1]), kind(parts[2]))
+    for w in want:
+        if w in found:
+            return found[w]
     return None
 
 
 def measured_traffic(call: str, workload: str = "cfg2"):
-    """HBM bytes per launch of the call's kernel (FETCH_SIZE / WRITE_SIZE
-    counter runs, copy-calibrated), or None."""
-    return _profile_figure("traffic_bytes_per_launch", call, workload, int)
+    """HBM bytes per call (its one kernel, or the sum over its kernels) from
+    the FETCH_SIZE / WRITE_SIZE counter runs, copy-calibrated, or None."""
+    return _profile_figure("traffic_bytes_per_launch", "traffic_bytes_per_call", call,
+                           workload, int)
 
 
 def measured_mfma_busy(call: str, workload: str = "cfg2"):
-    """Matrix-core busy fraction of the call's kernel (SQ_VALU_MFMA_BUSY_CYCLES
-    over 1024 SIMDs x launch duration x 2.4 GHz), or None."""
-    return _profile_figure("mfma_busy_frac", call, workload, float)
+    """Matrix-core busy fraction of the call (SQ_VALU_MFMA_BUSY_CYCLES summed
+    over its kernels, over 1024 SIMDs x call duration x 2.4 GHz), or None."""
+    return _profile_figure("mfma_busy_frac", "mfma_busy_frac_per_call", call, workload, float)
 
 
 def main_line(args):
@@ -636,8 +655,8 @@ def wl_split(args):
     pairs = B * HEADS * _valid_pairs((HH, WW), (K, K), (1, 1), (False, False))
     qk_b, av_b = 2 * t + lg, lg + 2 * t
     fl = 2 * D * pairs
-    rq = _roof("na_qk_fwd", qk_b, fl, tq, BF16_PEAK_TFLOPS)
-    ra = _roof("na_av_fwd", av_b, fl, ta, BF16_PEAK_TFLOPS)
+    rq = _roof("na_qk_fwd", qk_b, fl, tq, BF16_PEAK_TFLOPS, measured_traffic("na_qk_fwd", "split"))
+    ra = _roof("na_av_fwd", av_b, fl, ta, BF16_PEAK_TFLOPS, measured_traffic("na_av_fwd", "split"))
     ms = tq["warm_ms"] + ta["warm_ms"]
     value = (qk_b + av_b) / (ms * 1e-3) / 1e9
     cpu = None
@@ -788,7 +807,8 @@ def wl_cfg4(args):
 
     tb = call_timing(lambda: hip.fused_backward(q, k, v, out, lse, do, None, *a, **kw),
                      cold=(bwd_set, bwd_b))
-    rf = _roof("na_fwd", nbytes_pad, flops, tf, BF16_PEAK_TFLOPS)
+    rf = _roof("na_fwd", nbytes_pad, flops, tf, BF16_PEAK_TFLOPS, measured_traffic("na_fwd", "cfg4"))
+    rf["mfma_busy"] = measured_mfma_busy("na_fwd", "cfg4")
     rb = _roof("na_bwd", bwd_b, bwd_f, tb, BF16_PEAK_TFLOPS, measured_traffic("na_bwd", "cfg4"))
     rb["mfma_busy"] = measured_mfma_busy("na_bwd", "cfg4")
     cpu = None
@@ -873,8 +893,10 @@ def wl_cfg5(args):
             ra = _roof("na_rpb_av_fwd", av_b, 2 * Dc * Kx * rows, ta, FP32_PEAK_TFLOPS,
                        measured_traffic("na_rpb_av_fwd", "cfg5") if (Kx, d) == (7, 1) else None)
             rqb = _roof("na_rpb_qk_bwd", qkb_b, (4 * Dc * Kx + Kx) * rows, tqb,
-                        FP32_PEAK_TFLOPS)
-            rab = _roof("na_rpb_av_bwd", avb_b, 4 * Dc * Kx * rows, tab, FP32_PEAK_TFLOPS)
+                        FP32_PEAK_TFLOPS,
+                        measured_traffic("na_rpb_qk_bwd", "cfg5") if (Kx, d) == (7, 1) else None)
+            rab = _roof("na_rpb_av_bwd", avb_b, 4 * Dc * Kx * rows, tab, FP32_PEAK_TFLOPS,
+                        measured_traffic("na_rpb_av_bwd", "cfg5") if (Kx, d) == (7, 1) else None)
             table[f"K{Kx}_d{d}"] = {"qk": rq, "av": ra, "qk_bwd": rqb, "av_bwd": rab}
             if Kx == 7 and d == 1:
                 ms = tq["warm_ms"] + ta["warm_ms"]
@@ -1076,10 +1098,18 @@ WORKLOADS = {"cfg1": wl_cfg1, "split": wl_split, "cfg3": wl_cfg3, "cfg4": wl_cfg
 
 def profile_calls(n: int, workload: str = "cfg2") -> None:
     """Run n calls of each library entry point of a workload (for rocprofv3
-    counter passes); cfg2 and cfg3 also run a calibration copy of
-    COPY_BYTES each time."""
+    counter passes), each workload with n calibration copies of COPY_BYTES
+    (interleaved with the calls for cfg2 and cfg3, before them otherwise)."""
     from natten_amd._core import hip
 
+    # calibration for the HBM byte counters: a plain device copy of a known
+    # size (COPY_BYTES read + COPY_BYTES written), far larger than the caches
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0").uniform_()
+    dst = torch.empty_like(src)
+    if workload != "cfg2" and workload != "cfg3":
+        for _ in range(n):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     if workload == "split":
         q, k, v, do = make_inputs(torch.device("cuda:0"))
         a = ((K, K), (1, 1), (1, 1), (False, False))
@@ -1153,10 +1183,6 @@ def profile_calls(n: int, workload: str = "cfg2") -> None:
         q, k, v, do = make_inputs(torch.device("cuda:0"))
         a = ((K, K), (1, 1), (1, 1), (False, False), None)
     out, lse = hip.fused_forward(q, k, v, *a)
-    # calibration for the HBM byte counters: a plain device copy of a known
-    # size (COPY_BYTES read + COPY_BYTES written), far larger than the caches
-    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=q.device).uniform_()
-    dst = torch.empty_like(src)
     for _ in range(n):
         dst.copy_(src)
         hip.fused_forward(q, k, v, *a)
