@@ -17,6 +17,9 @@ import torch
 
 LIB_NAME = "libnatten_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
+# The fused op as a torch custom operator (csrc/na_torch.cpp): its autograd
+# node runs in C++ over this library
+OP_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libnatten_amd_torch.so")
 
 NA_F32, NA_F16, NA_BF16 = 0, 1, 2
 NA_FLAG_DENSE = 1
@@ -159,6 +162,7 @@ SIGNATURES = {
 _lib = None
 _lock = threading.Lock()
 _load_error: str | None = None
+_fused_op = None
 
 
 def load():
@@ -180,8 +184,29 @@ def load():
             fn.argtypes = args
         if lib.na_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_NAME} ABI {lib.na_abi_version()} != {ABI_VERSION}")
+        _load_fused_op()
         _lib = lib
         return lib
+
+
+def _load_fused_op() -> None:
+    """Register natten_amd::na_fused from libnatten_amd_torch.so (built
+    beside the library; it links this library, which the loader then shares
+    with the ctypes handle)."""
+    global _fused_op
+    if not os.path.exists(OP_LIB_PATH):
+        return
+    torch.ops.load_library(OP_LIB_PATH)
+    _fused_op = torch.ops.natten_amd.na_fused
+
+
+def fused_op():
+    """torch.ops.natten_amd.na_fused, or None where the operator library is
+    not built (the fused op then runs through the Python autograd Function
+    over the same kernels)."""
+    if _lib is None:
+        load()
+    return _fused_op
 
 
 def available() -> bool:

@@ -1,19 +1,44 @@
 """Autograd for the fused op (reference ``autograd/na{1,2,3}d.py``).
 
-One Function covers every rank, GQA, additional tokens, varlen and the
-dense (FMHA) mode.  Its forward returns ``(out, lse)``; the backward takes
+One op covers every rank, GQA, additional tokens, varlen and the dense
+(FMHA) mode.  Its forward returns ``(out, lse)``; the backward takes
 gradients for both (the LSE gradient enters as ``delta - dlse``), so a loss
 that uses the returned LSE differentiates correctly
 (reference ``tests/test_new_features.py:1177-1192``).
+
+With the built-in ``hip`` backend the op is ``torch.ops.natten_amd.na_fused``
+(``csrc/na_torch.cpp``): its autograd node runs in C++ over the C ABI, so
+neither direction passes through Python or ctypes per call.  ``_FusedNA``
+below is the same op as a Python ``autograd.Function`` over the backend
+module's hooks; it runs for other registered backends, where the operator
+library is not built, and under ``python_autograd()`` /
+``NATTEN_AMD_PY_AUTOGRAD=1`` (A/B checks: both launch the same kernels).
 """
 
 from __future__ import annotations
 
+import contextlib
+import os
 from typing import NamedTuple, Optional
 
 import torch
 
-from .._core import ops
+from .._core import _lib, ops
+from .._core import hip as _hip
+
+_py_autograd = os.environ.get("NATTEN_AMD_PY_AUTOGRAD", "0") == "1"
+
+
+@contextlib.contextmanager
+def python_autograd(enabled: bool = True):
+    """Temporarily run the fused op through the Python autograd Function."""
+    global _py_autograd
+    prev = _py_autograd
+    _py_autograd = enabled
+    try:
+        yield
+    finally:
+        _py_autograd = prev
 
 
 class FusedSpec(NamedTuple):
@@ -55,9 +80,24 @@ class _FusedNA(torch.autograd.Function):
         return dq, dk, dv, dek, dev, None, None
 
 
+def _op_flags(spec: FusedSpec, sample_extent) -> int:
+    return ((_lib.NA_FLAG_DENSE if spec.dense else 0)
+            | (_lib.NA_FLAG_GENERIC if _hip._force_generic else 0)
+            | (_lib.NA_FLAG_NO_LEAN if _hip._no_lean else 0)
+            | (_lib.NA_FLAG_VARLEN_CLAMPED if spec.varlen_clamped and sample_extent is not None
+               else 0))
+
+
 def na_fused_with_grad(q, k, v, spec: FusedSpec, extra_k=None, extra_v=None,
                        sample_extent=None):
     """Differentiable fused op; returns ``(out, lse_float32)``."""
+    if not _py_autograd and q.is_cuda:
+        op = _lib.fused_op()
+        if op is not None and ops.backend_module() is _hip:
+            scale = q.shape[-1] ** -0.5 if spec.scale is None else float(spec.scale)
+            return op(q, k, v, extra_k, extra_v, sample_extent, spec.kernel_size, spec.stride,
+                      spec.dilation, [int(c) for c in spec.is_causal], scale,
+                      _op_flags(spec, sample_extent), _lib.stream_of(q))
     return _FusedNA.apply(q, k, v, extra_k, extra_v, sample_extent, spec)
 
 

@@ -110,10 +110,19 @@ def _is_full_attention(kernel_size: tuple, spatial_shape: tuple) -> bool:
     return all(ks >= s for ks, s in zip(kernel_size, spatial_shape))
 
 
-def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
-        additional_keys, additional_values):
+# Validated specs by call signature (shapes, dtypes and the arguments as
+# passed): a training loop calls with the same few signatures every step,
+# and the checks and tuple normalisation cost more host time than the rest
+# of the call.  Only successful validations are stored; unhashable arguments
+# (lists) are validated on every call.
+_spec_cache: dict = {}
+_SPEC_MAX = 512
+
+
+def _fused_spec(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale,
+                additional_keys, additional_values) -> FusedSpec:
     _validate_qkv(query, key, value, rank)
-    add_k, add_v = _validate_additional_kv(query, key, additional_keys, additional_values)
+    _validate_additional_kv(query, key, additional_keys, additional_values)
     spatial_shape = tuple(query.shape[1:-2])
     head_dim = query.shape[-1]
 
@@ -127,15 +136,42 @@ def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale
     check_dilation_kernel_vs_input(dil, ks, spatial_shape)
 
     scale_value = head_dim ** -0.5 if scale is None else float(scale)
+    dense = (_is_full_attention(ks, spatial_shape) and all(s == 1 for s in st)
+             and not any(caus))
+    return FusedSpec(tuple(ks), tuple(st), tuple(dil), tuple(bool(c) for c in caus), scale_value,
+                     dense)
+
+
+def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+        additional_keys, additional_values):
+    add = additional_keys is not None or additional_values is not None
+    try:
+        ck = (rank, query.shape, key.shape, value.shape, query.dtype, key.dtype, value.dtype,
+              kernel_size, stride, dilation, is_causal, scale,
+              (None if additional_keys is None else (additional_keys.shape, additional_keys.dtype),
+               None if additional_values is None
+               else (additional_values.shape, additional_values.dtype)) if add else None)
+        spec = _spec_cache.get(ck)
+    except TypeError:  # an unhashable argument
+        ck = spec = None
+    if spec is None:
+        spec = _fused_spec(rank, query, key, value, kernel_size, stride, dilation, is_causal,
+                           scale, additional_keys, additional_values)
+        if ck is not None:
+            if len(_spec_cache) >= _SPEC_MAX:
+                _spec_cache.clear()
+            _spec_cache[ck] = spec
+    add_k, add_v = additional_keys, additional_values
+    if add:
+        if add_k.dtype != query.dtype:
+            add_k = add_k.to(query.dtype)
+        if add_v.dtype != query.dtype:
+            add_v = add_v.to(query.dtype)
     if key.dtype != query.dtype:
         key = key.to(query.dtype)
     if value.dtype != query.dtype:
         value = value.to(query.dtype)
-
-    dense = (_is_full_attention(ks, spatial_shape) and all(s == 1 for s in st)
-             and not any(caus))
-    spec = FusedSpec(tuple(ks), tuple(st), tuple(dil), tuple(bool(c) for c in caus), scale_value,
-                     dense)
+    dense = spec.dense
     out, lse = na_fused_with_grad(query, key, value, spec, add_k, add_v)
     if not return_lse:
         return out

@@ -143,3 +143,16 @@ def test_reference_tier_probes_exist():
     assert natten_amd.has_metal() is False
     assert natten_amd.has_nanobind() is False
     assert "has_metal" in natten_amd.__all__ and "has_nanobind" in natten_amd.__all__
+
+
+def test_fused_operator_registered():
+    """libnatten_amd_torch.so registers natten_amd::na_fused (the fused op's
+    C++ autograd node); with host tensors it raises like the rest of the
+    package (no CPU implementation)."""
+    from natten_amd._core import _lib
+
+    op = _lib.fused_op()
+    assert op is not None
+    q = torch.randn(1, 16, 2, 8, requires_grad=True)
+    with pytest.raises(RuntimeError, match="HIP"):
+        op(q, q, q, None, None, None, [3], [1], [1], [0], 0.3, 0, 0)
