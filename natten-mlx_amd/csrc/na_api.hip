@@ -587,8 +587,7 @@ int na_qk_bwd(const na_params *p, const void *q, const void *k,
       dk == nullptr)
     return fail(NA_ERR_INVALID, "q/k/dlogits/dq/dk must be non-NULL");
   if (use_lsplit(p, P)) {
-    na::lsplit_av(P, p->dtype, dlogits, k, dq, P.scale, as_stream(stream));
-    na::lsplit_inv(P, p->dtype, dlogits, q, dk, P.scale, as_stream(stream));
+    na::lsplit_qk_bwd(P, p->dtype, q, k, dlogits, dq, dk, as_stream(stream));
   } else if (use_msplit(p, P)) {
     na::msplit_av(P, p->dtype, dlogits, k, dq, P.scale, as_stream(stream));
     na::msplit_inv(P, p->dtype, dlogits, q, dk, P.scale, as_stream(stream));
@@ -609,8 +608,7 @@ int na_av_bwd(const na_params *p, const void *attn, const void *v,
       dv == nullptr)
     return fail(NA_ERR_INVALID, "attn/v/dout/dattn/dv must be non-NULL");
   if (use_lsplit(p, P)) {
-    na::lsplit_qk(P, p->dtype, dout, v, dattn, 1.f, 0.f, as_stream(stream));
-    na::lsplit_inv(P, p->dtype, attn, dout, dv, 1.f, as_stream(stream));
+    na::lsplit_av_bwd(P, p->dtype, attn, v, dout, dattn, dv, as_stream(stream));
   } else if (use_msplit(p, P)) {
     na::msplit_qk(P, p->dtype, dout, v, dattn, 1.f, 0.f, as_stream(stream));
     na::msplit_inv(P, p->dtype, attn, dout, dv, 1.f, as_stream(stream));

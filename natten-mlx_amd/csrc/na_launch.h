@@ -128,6 +128,14 @@ void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,
                void *out, float scale, hipStream_t st);
 void lsplit_inv(const Prob &P, int dtype, const void *a, const void *x,
                 void *z, float scale, hipStream_t st);
+// The split backward calls: dq (lsplit_av over dlogits and the keys) and
+// dk (lsplit_inv over dlogits and the queries); dattn (lsplit_qk over dout
+// and the values) and dv (lsplit_inv over attn and dout) — each pair in one
+// launch where that applies.
+void lsplit_qk_bwd(const Prob &P, int dtype, const void *q, const void *k,
+                   const void *dlogits, void *dq, void *dk, hipStream_t st);
+void lsplit_av_bwd(const Prob &P, int dtype, const void *attn, const void *v,
+                   const void *dout, void *dattn, void *dv, hipStream_t st);
 
 // Matrix-core split ops (na_msplit.hip): the MFMA-eligible problems with
 // d*K <= L on every non-causal axis and at most 512 kernel slots.

@@ -282,10 +282,9 @@ __global__ void __launch_bounds__(512)
 // products); scores go to the LDS row buffer branch-free (out-of-window
 // lanes write a per-lane spare slot past the rows).
 template <typename T, int D, int R, bool CPR1, int VW, bool CA>
-__global__ void __launch_bounds__(1024)
-    k_lqh(LProb Pin, const T *__restrict__ x, const T *__restrict__ y,
-          T *__restrict__ out, float scale, float fill, int prefill,
-          FastDiv fups) {
+__device__ __forceinline__ void lqh_body(int bid, const LProb &Pin, const T *__restrict__ x,
+                                         const T *__restrict__ y, T *__restrict__ out,
+                                         float scale, float fill, int prefill, FastDiv fups) {
   LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
   if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
@@ -296,7 +295,7 @@ __global__ void __launch_bounds__(1024)
   extern __shared__ __align__(16) char smem[];
 
   // tile: (sample, spatial tile of 16 queries); wave w: query head w
-  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const int tile = xcd_tile(bid, P.n_launch);
   const uint32_t bq = fdiv((uint32_t)tile, P.fGrid);
   const uint32_t sp = (uint32_t)tile - bq * P.fGrid.d;
   const int tid = threadIdx.x, nthr = blockDim.x;
@@ -417,9 +416,9 @@ __global__ void __launch_bounds__(1024)
 // area for the transposing read, so only the compact rows pass a
 // workgroup barrier.
 template <typename T, int D, int R, bool CPR1, int VW, bool CA>
-__global__ void __launch_bounds__(1024)
-    k_lah(LProb Pin, const T *__restrict__ a, const T *__restrict__ y,
-          T *__restrict__ out, float scale, FastDiv fups) {
+__device__ __forceinline__ void lah_body(int bid, const LProb &Pin, const T *__restrict__ a,
+                                         const T *__restrict__ y, T *__restrict__ out,
+                                         float scale, FastDiv fups) {
   LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
   if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
@@ -432,7 +431,7 @@ __global__ void __launch_bounds__(1024)
   constexpr int RS = lds_y(D);
   extern __shared__ __align__(16) char smem[];
 
-  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const int tile = xcd_tile(bid, P.n_launch);
   const uint32_t bq = fdiv((uint32_t)tile, P.fGrid);
   const uint32_t sp = (uint32_t)tile - bq * P.fGrid.d;
   const int tid = threadIdx.x, nthr = blockDim.x;
@@ -684,9 +683,9 @@ __global__ void __launch_bounds__(512)
 // transposing LDS read.  The gathers of a group of chunk pairs are issued
 // together; every compact-row element is read by exactly one key.
 template <typename T, int D, int R, bool CPR1, bool CA>
-__global__ void __launch_bounds__(512)
-    k_linv(LProb Pin, const T *__restrict__ a, const T *__restrict__ x,
-           T *__restrict__ z, float scale) {
+__device__ __forceinline__ void linv_body(int bid, const LProb &Pin, const T *__restrict__ a,
+                                          const T *__restrict__ x, T *__restrict__ z,
+                                          float scale) {
   LProb P = Pin;  // without a causal axis the window rules fold to the clamped rule
   if constexpr (!CA) P.ax[0].causal = P.ax[1].causal = P.ax[2].causal = 0;
   typedef L16<T> M;
@@ -699,7 +698,7 @@ __global__ void __launch_bounds__(512)
   extern __shared__ __align__(16) char smem[];
 
   // tile: (batch, key/value head, spatial tile)
-  const int tile = xcd_tile(blockIdx.x, P.n_launch);
+  const int tile = xcd_tile(bid, P.n_launch);
   const uint32_t rest = fdiv((uint32_t)tile, P.fGrid);
   const uint32_t sp = (uint32_t)tile - rest * P.fGrid.d;
   const uint32_t bq = fdiv(rest, P.fHkv);
@@ -794,6 +793,56 @@ __global__ void __launch_bounds__(512)
     for (int r = 0; r < 4; ++r) wv[r] = (E)(acc[db][r] * scale);
     *reinterpret_cast<v4 *>(z + krow * D + 16 * db + 4 * gq) = wv;
   }
+}
+
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
+__global__ void __launch_bounds__(1024)
+    k_lqh(LProb P, const T *__restrict__ x, const T *__restrict__ y, T *__restrict__ out,
+          float scale, float fill, int prefill, FastDiv fups) {
+  lqh_body<T, D, R, CPR1, VW, CA>((int)blockIdx.x, P, x, y, out, scale, fill, prefill, fups);
+}
+
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
+__global__ void __launch_bounds__(1024)
+    k_lah(LProb P, const T *__restrict__ a, const T *__restrict__ y, T *__restrict__ out,
+          float scale, FastDiv fups) {
+  lah_body<T, D, R, CPR1, VW, CA>((int)blockIdx.x, P, a, y, out, scale, fups);
+}
+
+template <typename T, int D, int R, bool CPR1, bool CA>
+__global__ void __launch_bounds__(512)
+    k_linv(LProb P, const T *__restrict__ a, const T *__restrict__ x, T *__restrict__ z,
+           float scale) {
+  linv_body<T, D, R, CPR1, CA>((int)blockIdx.x, P, a, x, z, scale);
+}
+
+// A backward's two passes in one launch (they are independent and their
+// workgroups have the same size): blocks [0, n0) the all-heads pass (dq by
+// k_lah over dlogits and the keys, or dattn by k_lqh over dout and the
+// values), the rest the inverse pass (dk from dlogits and the queries, or
+// dv from attn and dout) on their own problem description.
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
+__global__ void __launch_bounds__(1024)
+    k_lqkb(LProb Pa, LProb Pi, const T *__restrict__ dl, const T *__restrict__ key,
+           const T *__restrict__ q, T *__restrict__ dq, T *__restrict__ dk, float scale,
+           FastDiv fups, int n0) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    lah_body<T, D, R, CPR1, VW, CA>(bid, Pa, dl, key, dq, scale, fups);
+  else
+    linv_body<T, D, R, CPR1, CA>(bid - n0, Pi, dl, q, dk, scale);
+}
+
+template <typename T, int D, int R, bool CPR1, int VW, bool CA>
+__global__ void __launch_bounds__(1024)
+    k_lavb(LProb Pa, LProb Pi, const T *__restrict__ attn, const T *__restrict__ v,
+           const T *__restrict__ dout, T *__restrict__ dattn, T *__restrict__ dv, int prefill,
+           FastDiv fups, int n0) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    lqh_body<T, D, R, CPR1, VW, CA>(bid, Pa, dout, v, dattn, 1.f, 0.f, prefill, fups);
+  else
+    linv_body<T, D, R, CPR1, CA>(bid - n0, Pi, attn, dout, dv, 1.f);
 }
 
 }  // namespace
@@ -1013,6 +1062,118 @@ void lsplit_inv(const Prob &P, int dtype, const void *a, const void *x,
 #define LS_ARGS_INV(TT) (const TT *)a, (const TT *)x, (TT *)z, scale
   LS_DISPATCH(k_linv, LS_ARGS_INV(TT));
 #undef LS_ARGS_INV
+}
+
+// NATTEN_AMD_SPLIT_PAIR=0 launches a split backward's two passes separately
+// (A/B checks of the paired launch; read on every call, so a test can switch
+// it within one process).
+static bool split_pair_on() {
+  const char *e = std::getenv("NATTEN_AMD_SPLIT_PAIR");
+  return e == nullptr || e[0] != '0';
+}
+
+// A split backward's two passes in one launch (k_lqkb: dq + dk, k_lavb:
+// dattn + dv) where the all-heads pass applies, its workgroups have the
+// inverse pass's size and both take the same chunk walk; false otherwise
+// (nothing launched).
+static bool lsplit_pair(const Prob &P, int dtype, bool qk, const void *w, const void *y,
+                        const void *xi, void *out_a, void *out_i, float scale,
+                        hipStream_t st) {
+  if (!split_pair_on()) return false;
+  const LChoice C = lean_choice(P, kLQK);
+  const LChoice Ci = lean_choice(P, kLInv);
+  LqhPlan pl;
+  if (!lqh_plan(P, &pl)) return false;
+  const int nb = P.D == 128 ? 2 : 4;
+  const size_t lah_lds = (size_t)align16(16 * P.H * P.kprod) * 2 +
+                         (size_t)P.H * nb * 16 * lds_y(P.D) * 2;
+  if (qk && lah_lds > 65536) return false;
+  if (Ci.W != P.H) return false;
+  const bool cp = P.rank == 3 ? C.cpr1 && C.sl == 1 : C.cpr1;
+  const bool cpi = P.rank == 3 ? Ci.cpr1 && Ci.sl == 1 : Ci.cpr1;
+  if (P.rank > 1 && cp != cpi) return false;
+  LChoice C1 = C;  // one wave tile per workgroup (waves are heads)
+  C1.W = 1;
+  LProb La = make_lprob(P, C1);
+  La.n_tiles = P.B * (int)La.fGrid.d;
+  La.n_launch = (La.n_tiles + 7) & ~7;
+  LProb Li = make_lprob(P, Ci);
+  Li.n_tiles = P.B * P.Hkv * (int)Li.fGrid.d;
+  Li.n_launch = (Li.n_tiles + 7) & ~7;
+  if (La.n_tiles == 0 || Li.n_tiles == 0) return false;
+  const size_t lds = std::max(qk ? lah_lds : pl.lds, lean_lds_bytes(P, kLInv, Li.ebox, Ci.W));
+  int prefill = 0;
+  for (int a = 0; a < 3; ++a) prefill |= P.ax[a].causal;
+  const bool ca = prefill != 0;
+  const FastDiv fups = make_fastdiv((uint32_t)(P.H * P.kprod / pl.vw));
+  const int n0 = La.n_launch;
+  const dim3 grid(La.n_launch + Li.n_launch), block(64 * P.H);
+  auto go = [&](auto tt, auto dd, auto rr, auto cc, auto vv) {
+    typedef decltype(tt) TT;
+    constexpr int DD = decltype(dd)::value, RR = decltype(rr)::value;
+    constexpr bool CC = decltype(cc)::value;
+    constexpr int VV = decltype(vv)::value;
+    if (qk) {
+      // w = dlogits, y = keys, xi = queries; out_a = dq, out_i = dk
+      if (ca)
+        hipLaunchKernelGGL((k_lqkb<TT, DD, RR, CC, VV, true>), grid, block, lds, st, La, Li,
+                           (const TT *)w, (const TT *)y, (const TT *)xi, (TT *)out_a,
+                           (TT *)out_i, scale, fups, n0);
+      else
+        hipLaunchKernelGGL((k_lqkb<TT, DD, RR, CC, VV, false>), grid, block, lds, st, La, Li,
+                           (const TT *)w, (const TT *)y, (const TT *)xi, (TT *)out_a,
+                           (TT *)out_i, scale, fups, n0);
+    } else {
+      // w = attn, y = values, xi = dout; out_a = dattn, out_i = dv
+      if (ca)
+        hipLaunchKernelGGL((k_lavb<TT, DD, RR, CC, VV, true>), grid, block, lds, st, La, Li,
+                           (const TT *)w, (const TT *)y, (const TT *)xi, (TT *)out_a,
+                           (TT *)out_i, prefill, fups, n0);
+      else
+        hipLaunchKernelGGL((k_lavb<TT, DD, RR, CC, VV, false>), grid, block, lds, st, La, Li,
+                           (const TT *)w, (const TT *)y, (const TT *)xi, (TT *)out_a,
+                           (TT *)out_i, prefill, fups, n0);
+    }
+  };
+  auto by_v = [&](auto tt, auto dd, auto rr, auto cc) {
+    if (pl.vw == 8) go(tt, dd, rr, cc, std::integral_constant<int, 8>());
+    else if (pl.vw == 4) go(tt, dd, rr, cc, std::integral_constant<int, 4>());
+    else if (pl.vw == 2) go(tt, dd, rr, cc, std::integral_constant<int, 2>());
+    else go(tt, dd, rr, cc, std::integral_constant<int, 1>());
+  };
+  auto by_r = [&](auto tt, auto dd) {
+    if (P.rank == 1)
+      by_v(tt, dd, std::integral_constant<int, 1>(), std::false_type());
+    else if (P.rank == 2) {
+      if (cp) by_v(tt, dd, std::integral_constant<int, 2>(), std::true_type());
+      else by_v(tt, dd, std::integral_constant<int, 2>(), std::false_type());
+    } else {
+      if (cp) by_v(tt, dd, std::integral_constant<int, 3>(), std::true_type());
+      else by_v(tt, dd, std::integral_constant<int, 3>(), std::false_type());
+    }
+  };
+  auto by_d = [&](auto tt) {
+    if (P.D == 32) by_r(tt, std::integral_constant<int, 32>());
+    else if (P.D == 64) by_r(tt, std::integral_constant<int, 64>());
+    else by_r(tt, std::integral_constant<int, 128>());
+  };
+  if (dtype == NA_BF16) by_d(bf16_t());
+  else by_d(f16_t());
+  return true;
+}
+
+void lsplit_qk_bwd(const Prob &P, int dtype, const void *q, const void *k,
+                   const void *dlogits, void *dq, void *dk, hipStream_t st) {
+  if (lsplit_pair(P, dtype, true, dlogits, k, q, dq, dk, P.scale, st)) return;
+  lsplit_av(P, dtype, dlogits, k, dq, P.scale, st);
+  lsplit_inv(P, dtype, dlogits, q, dk, P.scale, st);
+}
+
+void lsplit_av_bwd(const Prob &P, int dtype, const void *attn, const void *v,
+                   const void *dout, void *dattn, void *dv, hipStream_t st) {
+  if (lsplit_pair(P, dtype, false, attn, v, dout, dattn, dv, 1.f, st)) return;
+  lsplit_qk(P, dtype, dout, v, dattn, 1.f, 0.f, st);
+  lsplit_inv(P, dtype, attn, dout, dv, 1.f, st);
 }
 
 #undef LS_DISPATCH

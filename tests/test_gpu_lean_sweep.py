@@ -284,3 +284,43 @@ def test_lean_grouped_heads_forward(case, monkeypatch):
                                      extra_k=ek, extra_v=ev, sample_extent=se,
                                      varlen_clamped=True))
     assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+
+
+PAIR_CASES = [
+    ((2, 24, 20), 4, 4, 32, 7, 1, torch.bfloat16),   # config-2-like: the pairs apply
+    ((2, 30, 18), 4, 2, 64, 5, 2, torch.float16),    # GQA, dilation
+    ((3, 70), 4, 4, 32, 9, 3, torch.bfloat16),       # rank 1
+]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES, ids=[f"p{i}" for i in range(len(PAIR_CASES))])
+def test_split_backward_pair_matches_separate_launches(case, monkeypatch):
+    """The split backward's paired launch (dq + dk, dattn + dv in one
+    launch) against the two passes launched separately, bit for bit."""
+    from natten_amd._core import hip
+
+    bs, H, Hkv, D, K, d, dtype = case
+    _say(f"[case] split pair {case}")
+    rank = len(bs) - 1
+    sp = bs[1:]
+    ks, dil, st, ca = (K,) * rank, (d,) * rank, (1,) * rank, (False,) * rank
+    q = randn((bs[0], *sp, H, D), dtype, 81).to(DEV)
+    k = randn((bs[0], *sp, Hkv, D), dtype, 82).to(DEV)
+    v = randn((bs[0], *sp, Hkv, D), dtype, 83).to(DEV)
+    assert hip.kernel_path(q, k, ks, st, dil, ca, split=True) == "lean"
+    kp = K ** rank
+    dl = randn((bs[0], *sp, H, kp), dtype, 84).to(DEV)
+    attn = torch.softmax(randn((bs[0], *sp, H, kp), torch.float32, 85), -1).to(dtype).to(DEV)
+    do = randn((bs[0], *sp, H, D), dtype, 86).to(DEV)
+
+    def run():
+        a = hip.qk_backward(q, k, dl, ks, st, dil, ca, 0.3)
+        b = hip.av_backward(attn, v, do, ks, st, dil, ca)
+        torch.cuda.synchronize()
+        return [*a, *b]
+
+    paired = run()
+    monkeypatch.setenv("NATTEN_AMD_SPLIT_PAIR", "0")
+    separate = run()
+    for a, b in zip(paired, separate):
+        assert torch.equal(a, b)
