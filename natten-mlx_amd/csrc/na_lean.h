@@ -185,7 +185,7 @@ __device__ __forceinline__ bool tile_origin(const LProb &P, uint32_t sp,
     }
     const int rr = (int)fdiv((uint32_t)g[a], x.fnt);
     t.r[a] = rr;
-    t.i0[a] = (g[a] - rr * x.nt) << x.lgTW;
+    t.i0[a] = (g[a] - rr * x.nt) * x.TW;  // TW: any wave count times T
     t.Lr[a] = x.Lq + (rr < x.Lrem ? 1 : 0);
     t.nvt[a] = min(t.Lr[a] - t.i0[a], x.TW);
     if (VX && P.se != nullptr) {
@@ -578,15 +578,23 @@ size_t lds_budget() {
 // (measured: eight-wave workgroups halve the workgroup count, and at
 // config 2 size the CUs holding two of them set a longer tail than the 16
 // CUs holding a fourth four-wave workgroup; on the 1-D config 4 they are
-// faster).  NATTEN_AMD_LEAN_WAVES overrides it (tuning).
-int lean_max_waves(int rank) {
+// faster).  NATTEN_AMD_LEAN_WAVES (1 to 8) overrides it (tuning).
+int lean_waves_env() {
   static const int w = [] {
     const char *e = std::getenv("NATTEN_AMD_LEAN_WAVES");
     const int v = e != nullptr ? std::atoi(e) : 0;
-    return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
+    return v >= 1 && v <= 8 ? v : 0;
   }();
+  return w;
+}
+bool lean_waves_forced() { return lean_waves_env() > 0; }
+int lean_max_waves(int rank) {
+  const int w = lean_waves_env();
   return w > 0 ? w : rank == 1 ? 8 : 4;
 }
+
+// Compute units of the gfx950 parts this library targets (MI350X, MI355X).
+constexpr int kLeanCUs = 256;
 
 struct LChoice {
   int T[3];      // wave tile (product 16 over the active axes)
@@ -716,8 +724,15 @@ LChoice lean_choice(const Prob &P, LMode mode) {
       }
     }
   double best_per_wave = 1e300;
-  for (int W = lean_max_waves(R); W >= 1; W >>= 1)
+  // the largest wave count, then the powers of two below it
+  int Ws[5], nW = 0;
+  const int wmax = lean_max_waves(R);
+  Ws[nW++] = wmax;
+  for (int W = 8; W >= 1; W >>= 1)
+    if (W < wmax) Ws[nW++] = W;
+  for (int wi = 0; wi < nW; ++wi)
     for (int sa = lead; sa < 3; ++sa) {
+      const int W = Ws[wi];
       const Axis &x = P.ax[sa];
       // every wave tile of a workgroup must start inside the phase
       if (W > 1 && best.T[sa] * (W - 1) >= (x.L + x.d - 1) / x.d) continue;
@@ -743,6 +758,49 @@ LChoice lean_choice(const Prob &P, LMode mode) {
         best.ok = true;
       }
     }
+  // The rank-2 backward: a workgroup of 5 to 7 waves where its tile divides
+  // every dilation phase exactly and fewer waves land on the busiest CU.
+  // Every workgroup of such a launch is resident at once and the backward
+  // is issue-bound, so the CU holding the most waves sets the time: at
+  // 56 x 56 (config 2) 448 seven-wave workgroups put at most 14 waves on a
+  // CU where 784 four-wave ones put 16 (13.9 vs 14.3 us; the forward,
+  // lighter per wave, is not faster with them).  NATTEN_AMD_LEAN_WAVES
+  // turns this off.
+  if (best.ok && mode == kLBwd && R == 2 && !lean_waves_forced()) {
+    auto tiles_of = [&](int W, int sa) {
+      int64_t n = (int64_t)P.B * P.Hkv;
+      for (int a = lead; a < 3; ++a) {
+        const Axis &x = P.ax[a];
+        const int tw = best.T[a] * (a == sa ? W : 1);
+        n *= (int64_t)x.d * (((x.L + x.d - 1) / x.d + tw - 1) / tw);
+      }
+      return n;
+    };
+    auto busiest = [&](int W, int sa) {
+      return (tiles_of(W, sa) + kLeanCUs - 1) / kLeanCUs * W;
+    };
+    int64_t cur = busiest(best.W, best.sa);
+    for (int W = 7; W >= 5; --W)
+      for (int sa = lead; sa < 3; ++sa) {
+        const Axis &x = P.ax[sa];
+        const int tw = best.T[sa] * W;
+        if (x.L % x.d != 0 || (x.L / x.d) % tw != 0) continue;
+        int Em[3];
+        for (int a = 0; a < 3; ++a) Em[a] = ext(a, best.T[a] * (a == sa ? W : 1));
+        const int ebox = lds_rows(R, Em);
+        // resident two to a CU, no more staged rows per wave
+        if (2 * lean_lds_bytes(P, mode, ebox, W) > (size_t)160 * 1024) continue;
+        if ((double)ebox / W > best_per_wave) continue;
+        const int64_t b = busiest(W, sa);
+        if (b < cur) {
+          cur = b;
+          best.W = W;
+          best.sa = sa;
+          best.sl = Em[0];
+          for (int a = 0; a < 3; ++a) best.Em[a] = Em[a];
+        }
+      }
+  }
   return best;
 }
 

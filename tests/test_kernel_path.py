@@ -105,6 +105,9 @@ def test_plans_of_the_benchmarked_configs():
         assert p3["lds_bytes"] <= 160 * 1024
         p2 = _plan((4, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False), backward=bwd)
         assert p2["path"] == "lean" and p2["slabs"] == 1 and not p2["grouped_heads"], p2
+        # the backward in seven-wave workgroups (14 x 8 queries: 448 of them,
+        # at most 14 waves on a CU), the forward in four-wave ones (784)
+        assert (p2["waves"], p2["workgroups"]) == ((7, 448) if bwd else (4, 784)), p2
     ext = torch.full((8, 1), 1024, dtype=torch.int32)
     kw = dict(n_extra=16, sample_extent=ext, dtype=torch.float16, varlen_clamped=True)
     f4 = _plan((8, 4096, 16, 64), 4, (63,), (2,), (False,), **kw)
