@@ -676,8 +676,10 @@ def wl_split(args):
     return _line("na2d split qk/av bf16 HBM GB/s, 1 MI355X", value, "GB/s", ms, "bf16", cfg,
                  rq if tq["warm_ms"] >= ta["warm_ms"] else ra, cpu,
                  {"calls": {"qk": rq, "av": ra,
-                            "qk_bwd": _roof("na_qk_bwd", qkb_b, 2 * fl, tqb, BF16_PEAK_TFLOPS),
-                            "av_bwd": _roof("na_av_bwd", avb_b, 2 * fl, tab, BF16_PEAK_TFLOPS)}})
+                            "qk_bwd": _roof("na_qk_bwd", qkb_b, 2 * fl, tqb, BF16_PEAK_TFLOPS,
+                                            measured_traffic("na_qk_bwd", "split")),
+                            "av_bwd": _roof("na_av_bwd", avb_b, 2 * fl, tab, BF16_PEAK_TFLOPS,
+                                            measured_traffic("na_av_bwd", "split"))}})
 
 
 def wl_cfg3(args):
