@@ -156,8 +156,9 @@ typedef struct na_plan {
   int32_t box[3];          /* largest staged key box (backward: also the
                               query box of a key tile) */
   int32_t slabs;           /* pieces along axis 0 the box is staged in */
-  int32_t grouped_heads;   /* forward: a workgroup runs every query head of
-                              its key/value head over one staged box */
+  int32_t grouped_heads;   /* forward: query heads a workgroup runs over one
+                              staged box of their key/value head (0: one
+                              head per workgroup) */
   int32_t workgroups;      /* workgroups launched */
   int32_t lds_bytes;       /* LDS per workgroup */
   int32_t extra_reduction; /* backward with additional tokens: their

@@ -91,8 +91,10 @@ struct LProb {
   int32_t nxr;        // their LDS rows (nx rounded up to 16), before the box
   int32_t kp;         // kernel slots per query (K0 K1 K2), split ops
   int32_t kst0, kst1; // slot strides of axes 0 and 1 (K1 K2, K2)
-  int32_t hl;         // forward (VX): a workgroup runs every query head of
-                      // its key/value head over one staged box
+  int32_t hl;         // forward (VX): query heads a workgroup runs over one
+                      // staged box (a divisor of rep; 0: one head per
+                      // workgroup, decoded per query head)
+  FastDiv fHg;        // rep / hl: head groups per key/value head
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -223,16 +225,19 @@ __device__ __forceinline__ void tile_box(const LProb &P, LTile &t, int head,
   t.kbase = (tok0 * heads + head) * P.D;
 }
 
-// Tile of (sample, key/value head): t.head is the group's first query head.
+// Tile of (sample, key/value head, group of P.hl query heads): t.head is
+// the group's first query head.
 template <int R>
 __device__ __forceinline__ bool decode_tile_group(const LProb &P, int tile,
                                                   LTile &t) {
   const uint32_t rest = fdiv((uint32_t)tile, P.fGrid);
   const uint32_t sp = (uint32_t)tile - rest * P.fGrid.d;
-  const uint32_t bq = fdiv(rest, P.fHkv);
-  t.hk = (int)(rest - bq * P.fHkv.d);
+  const uint32_t r2 = fdiv(rest, P.fHg);
+  const int sub = (int)(rest - r2 * P.fHg.d);
+  const uint32_t bq = fdiv(r2, P.fHkv);
+  t.hk = (int)(r2 - bq * P.fHkv.d);
   t.b = (int)bq;
-  t.head = t.hk * P.rep;
+  t.head = t.hk * P.rep + sub * P.hl;
   const bool any = tile_origin<R, true>(P, sp, t);
   tile_box<R, false>(P, t, t.hk, P.Hkv);
   return any & (t.b < P.B);
@@ -842,6 +847,7 @@ LProb make_lprob(const Prob &P, const LChoice &C) {
   L.ebox = lds_rows(P.rank, C.Em) / C.Em[0] * C.sl;
   L.sl = C.sl;
   L.hl = 0;
+  L.fHg = make_fastdiv(1u);
   L.lgP2 = P.rank == 1 ? 0 : ilog2c(C.Em[2]);
   L.fGrid = make_fastdiv((uint32_t)grid);
   L.n_tiles = P.B * P.H * grid;

@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(512)
   } else {
     tile_any = decode_tile<R, VX>(P, xcd_tile(blockIdx.x, P.n_launch), t);
   }
-  const int nhl = hl ? P.rep : 1;
+  const int nhl = hl ? P.hl : 1;
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int n = lane & 15, gq = lane >> 4;
@@ -953,10 +953,13 @@ bool lean_bwd_eligible(const Prob &P, int dtype) {
     }                    \
   } while (0)
 
-// The forward's launch: grouped query heads (one staged box for the group)
-// for varlen / additional-token problems where the box is one slab and the
-// grouped launch still gives at least 4 workgroups per CU;
-// NATTEN_AMD_HL=0 / 1 turns the grouping off / on wherever it applies.
+// The forward's launch: grouped query heads (one staged box for a group
+// of query heads of one key/value head) for varlen / additional-token
+// problems where the box is one slab and the grouped launch still gives at
+// least 4 workgroups per CU; NATTEN_AMD_HL=0 / 1 turns the grouping off /
+// on wherever it applies, NATTEN_AMD_HL_HEADS=h (a divisor of the group)
+// runs h query heads per workgroup instead of all of them (both read per
+// call).
 LProb lean_fwd_lprob(const Prob &P, const LChoice &C) {
   LProb L = make_lprob(P, C);
   const bool vx = P.n_extra > 0 || P.sample_extent != nullptr;
@@ -964,8 +967,13 @@ LProb lean_fwd_lprob(const Prob &P, const LChoice &C) {
   const bool hl_auto = L.n_tiles / P.rep >= 1024;
   const bool hl_want = hl_env != nullptr ? hl_env[0] == '1' : hl_auto;
   if (vx && P.rep > 1 && (P.rank < 3 || L.sl >= L.ax[0].Em) && hl_want) {
-    L.hl = 1;
-    L.n_tiles /= P.rep;
+    int hpw = P.rep;
+    const char *hh = std::getenv("NATTEN_AMD_HL_HEADS");
+    const int h = hh != nullptr ? std::atoi(hh) : 0;
+    if (h >= 1 && h < P.rep && P.rep % h == 0) hpw = h;
+    L.hl = hpw;
+    L.fHg = make_fastdiv((uint32_t)(P.rep / hpw));
+    L.n_tiles /= hpw;
     L.n_launch = (L.n_tiles + 7) & ~7;
   }
   return L;

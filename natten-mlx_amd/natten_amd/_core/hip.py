@@ -174,7 +174,8 @@ def kernel_plan(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_ex
     """How na_fwd (or na_bwd) launches for this problem (a diagnostic;
     launches nothing): a dict with the kernel family and, on the lean
     kernels, the wave tile, waves per workgroup, staged box, axis-0 slabs,
-    grouped query heads, workgroups, LDS bytes; with additional tokens in
+    grouped query heads (and how many per workgroup), workgroups, LDS bytes;
+    with additional tokens in
     the backward, which unit reduces their gradients."""
     lib = _lib.load()
     p = _params(q, k, kernel_size, stride, dilation, is_causal, scale, n_extra, dense,
@@ -183,7 +184,8 @@ def kernel_plan(q, k, kernel_size, stride, dilation, is_causal, scale=None, n_ex
     _lib.check(lib.na_kernel_plan(p, 1 if backward else 0, plan), "na_kernel_plan")
     return {"path": KERNEL_PATHS[plan.path], "tile": tuple(plan.tile), "waves": plan.waves,
             "box": tuple(plan.box), "slabs": plan.slabs,
-            "grouped_heads": bool(plan.grouped_heads), "workgroups": plan.workgroups,
+            "grouped_heads": bool(plan.grouped_heads),
+            "heads_per_workgroup": max(int(plan.grouped_heads), 1), "workgroups": plan.workgroups,
             "lds_bytes": plan.lds_bytes,
             "extra_reduction": {0: None, 1: "valu", 2: "matrix"}[plan.extra_reduction]}
 

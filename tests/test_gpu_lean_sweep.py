@@ -278,12 +278,20 @@ def test_lean_grouped_heads_forward(case, monkeypatch):
     ev = randn((B, nx, Hkv, D), dtype, 65).to(DEV) if nx else None
     se = torch.tensor(sizes, dtype=torch.int32).to(DEV)
     res = []
-    for flag in ("0", "1"):
+    rep = H // Hkv
+    # per-head launch, every head of the group per workgroup, and (rep 4) two
+    flags = [("0", None), ("1", None)] + ([("1", "2")] if rep % 2 == 0 and rep > 2 else [])
+    for flag, heads in flags:
         monkeypatch.setenv("NATTEN_AMD_HL", flag)
+        if heads is None:
+            monkeypatch.delenv("NATTEN_AMD_HL_HEADS", raising=False)
+        else:
+            monkeypatch.setenv("NATTEN_AMD_HL_HEADS", heads)
         res.append(hip.fused_forward(q, k, v, ks, (1,) * rank, dil, (False,) * rank, None,
                                      extra_k=ek, extra_v=ev, sample_extent=se,
                                      varlen_clamped=True))
-    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    for r in res[1:]:
+        assert torch.equal(res[0][0], r[0]) and torch.equal(res[0][1], r[1])
 
 
 PAIR_CASES = [
