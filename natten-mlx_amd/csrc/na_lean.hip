@@ -51,7 +51,8 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
                                           const typename L16<T>::v8 (&qf)[D / 32],
                                           f32x4 (&o)[D / 16], float &m, f32x4 &lacc,
                                           const typename L16<T>::v8 &ones,
-                                          float sl2, int ka_off, int tr_off) {
+                                          float sl2, int ka_off, int tr_off,
+                                          bool fresh) {
   typedef L16<T> M;
   typedef typename M::v8 v8;
   typedef typename M::v4 v4;
@@ -78,8 +79,11 @@ __device__ __forceinline__ void fwd_group(const typename L16<T>::e *ks,
   mx = quad_max(mx) * sl2;
   // The reference point m may trail the running max by up to 8 (a factor
   // 2^8 in P): exact after the final division by l, and it spares the O
-  // rescale on groups that do not raise any query's max by more.
-  if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+  // rescale on groups that do not raise any query's max by more.  The first
+  // group of a query head finds O and l zero: it only sets m.
+  if (fresh) {
+    m = mx;
+  } else if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
     const float mn = fmaxf(m, mx);
     const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
     lacc *= alpha;
@@ -205,7 +209,7 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
           *reinterpret_cast<v4 *>(out + zo + 16 * db + 4 * gq) = z;
-        if (lse != nullptr && gq == 0) lse[zo / D] = 0.f;
+        if (lse != nullptr && gq == 0) lse[(uint32_t)zo / D] = 0.f;
       }
     }
     return;
@@ -252,6 +256,7 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
   for (int j = 0; j < NDB; ++j) o[j] = zero4();
   float m = -INFINITY;
+  bool fresh = true;  // no softmax group of this query head run yet
   f32x4 lacc = zero4();
   v8 ones;
 #pragma unroll
@@ -329,7 +334,8 @@ __global__ void __launch_bounds__(512)
         sv[j] = mask_init(ok, cb);
         if (R >= 2 && !CPR1) advance(cc, ws);
       }
-      fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, lacc, ones, sl2, ka_off, tr_off);
+      fwd_group<T, D, G>(ks, vs, kb, sv, qf, o, m, lacc, ones, sl2, ka_off, tr_off, fresh);
+      fresh = false;
     };
     if constexpr (NB >= 4) {
       int c0 = 0;
@@ -353,7 +359,7 @@ __global__ void __launch_bounds__(512)
       *reinterpret_cast<v4 *>(out + qoff + 16 * db + 4 * gq) = wv;
     }
     if (lse != nullptr && gq == 0)
-      lse[qoff / D] = !qv ? 0.f : l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
+      lse[(uint32_t)qoff / D] = !qv ? 0.f : l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
   }
   }  // query heads
 }
@@ -390,7 +396,8 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
     unit_walk<R, OCT, RSE, NU, false>(P, t, u0, tid, nthr, s0, g, la);
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
-      const int row = (g[j] - 8 * o) / D;
+      // element offsets are non-negative: an unsigned division is a shift
+      const int row = (int)((uint32_t)(g[j] - 8 * o) / D);
       qr[j] = ld8(q, g[j]);
       dr[j] = ld8(dout, g[j]);
       orr[j] = ld8(out, g[j]);
@@ -632,8 +639,9 @@ __global__ void __launch_bounds__(512)
           dsum = M::dot2(a2, b2, dsum);
         }
       }
-      const float lse2 = ldf(lse, qoff / D) * kLog2e;
-      const float dl = dlse != nullptr ? ldf(dlse, qoff / D) : 0.f;
+      const int qrow = (int)((uint32_t)qoff / D);
+      const float lse2 = ldf(lse, qrow) * kLog2e;
+      const float dl = dlse != nullptr ? ldf(dlse, qrow) : 0.f;
       float delta = 0.f;
       float cb0[4];
       col_bias(ws.ws[2] + 4 * gq - wl[2], ww[2], cb0);
@@ -753,7 +761,7 @@ __global__ void __launch_bounds__(512)
           *reinterpret_cast<v4 *>(dq + qoff + 16 * db + 4 * gq) = wv;
         }
         // VX: the row's delta, for the additional tokens' gradient pass
-        if (VX && dlt != nullptr && gq == 0) dlt[qoff / D] = delta;
+        if (VX && dlt != nullptr && gq == 0) dlt[(uint32_t)qoff / D] = delta;
       }
     }
   }
