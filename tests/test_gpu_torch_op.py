@@ -149,3 +149,43 @@ def test_operator_library_loaded():
     from natten_amd._core import _lib
 
     assert _lib.fused_op() is not None
+
+
+def test_op_edge_cases():
+    """Non-contiguous inputs, gradients for some inputs only, a loss on the
+    LSE alone (no gradient reaches out) and an empty batch, each through the
+    operator against the Python Function."""
+    import natten_amd
+    import natten_amd.autograd.fused as F
+
+    base = randn((2, 18, 16, 4, 32), torch.bfloat16, 1).to(DEV)
+    # a permuted view: [B, X, Y, H, D] seen through a transpose of X and Y
+    q = base.transpose(1, 2)
+    k = randn((2, 16, 18, 4, 32), torch.bfloat16, 2).to(DEV)
+    v = randn((2, 16, 18, 4, 32), torch.bfloat16, 3).to(DEV)
+    assert not q.is_contiguous()
+
+    def run(which, lse_only):
+        ts = [t.detach().clone() for t in (q, k, v)]
+        ts[0] = q.detach()  # keep the non-contiguous view
+        for i in which:
+            ts[i].requires_grad_(True)
+        out, lse = natten_amd.na2d(*ts, 5, dilation=2, return_lse=True)
+        loss = lse.float().sum() if lse_only else (out.float() ** 2).sum() + lse.float().sum()
+        return (out.detach(), lse.detach(),
+                *torch.autograd.grad(loss, [ts[i] for i in which]))
+
+    for which in ((0,), (1, 2), (0, 1, 2)):
+        for lse_only in (False, True):
+            r1 = run(which, lse_only)
+            with F.python_autograd():
+                r2 = run(which, lse_only)
+            for a, b in zip(r1, r2):
+                assert torch.equal(a, b), (which, lse_only)
+
+    # an empty batch: empty outputs and gradients
+    e = torch.empty((0, 10, 10, 2, 32), dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    out = natten_amd.na2d(e, e, e, 3)
+    assert out.shape == e.shape
+    (g,) = torch.autograd.grad(out.float().sum(), (e,))
+    assert g.shape == e.shape
