@@ -709,7 +709,7 @@ __device__ __forceinline__ PhPos ph_pos(const RpbProb &A, const PhMap &M, int po
 // Copy n 16-byte units of the virtual range starting at unit g0 (ru units per
 // position) between memory and LDS, four per thread in flight.  LOAD: memory
 // to LDS; else LDS to memory with streaming stores.
-template <bool LOAD>
+template <bool LOAD, bool NT = true>
 __device__ __forceinline__ void ph_copy(const RpbProb &A, const PhMap &M, int ru,
                                         FastDiv fru, const uint4 *gsrc, uint4 *gdst,
                                         uint4 *lds, int g0, int n) {
@@ -733,8 +733,10 @@ __device__ __forceinline__ void ph_copy(const RpbProb &A, const PhMap &M, int ru
     for (int j = 0; j < kB; ++j) {
       if (LOAD)
         reinterpret_cast<u32x4 *>(lds)[ix[j]] = r[j];
-      else
+      else if (NT)
         __builtin_nontemporal_store(r[j], reinterpret_cast<u32x4 *>(gdst) + mu[j]);
+      else
+        reinterpret_cast<u32x4 *>(gdst)[mu[j]] = r[j];
     }
   }
 }
@@ -875,6 +877,87 @@ __global__ void __launch_bounds__(512)
   __syncthreads();
   ph_copy<false>(A, M, U.ry, U.fry, nullptr, reinterpret_cast<uint4 *>(out),
                  reinterpret_cast<uint4 *>(sm4), R.row0 * NC, R.rows * NC);
+}
+
+// dk / dv on the phase-major rows (d > 1): one thread per key row in the
+// order (sample, phase, index m, head).  In phase units the queries whose
+// windows hold key m are [m <= K-1 ? 0 : m - K/2, m >= plen-K ? plen-1 :
+// m + K/2] (K d <= L), at slot m - clamp(mq - K/2, 0, plen - K); the
+// block stages the query rows and weight rows of the virtual positions from
+// its first key's first query to its last key's last query (at most K - 1
+// positions of halo per side, where the contiguous inverse needs (K - 1) d).
+// Where every key of the block lies at a phase index in [K, plen - K - 1]
+// of one phase the K candidates m + t, |t| <= K/2, take slot K/2 - t with no
+// window test (the interior rule of the contiguous inverse in phase units).
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_inverse(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ w,
+                  const float *__restrict__ x, float *__restrict__ out, float post,
+                  int cap) {
+  extern __shared__ __align__(16) float4 sm4[];
+  const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+  const int row0 = (int)blockIdx.x * nthr;
+  const int rows = min(nthr, A.n_rows - row0);
+  const PhPos f = ph_pos(A, M, (int)fdiv((uint32_t)row0, A.fH));
+  const PhPos l = ph_pos(A, M, (int)fdiv((uint32_t)(row0 + rows - 1), A.fH));
+  const int lo = f.b * A.L0 + f.pstart + (f.m <= K - 1 ? 0 : f.m - K / 2);
+  const int hi = l.b * A.L0 + l.pstart + (l.m >= l.plen - K ? l.plen - 1 : l.m + K / 2) + 1;
+  float4 *xs = sm4;                                     // cap rows of NC units
+  float *ws = reinterpret_cast<float *>(sm4 + cap * NC);  // cap rows of K floats
+  ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(x), nullptr,
+                reinterpret_cast<uint4 *>(xs), lo * U.ry, (hi - lo) * U.ry);
+  ph_copy<true>(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(w), nullptr,
+                reinterpret_cast<uint4 *>(ws), lo * U.rk, (hi - lo) * U.rk);
+  const int v = row0 + min(tid, rows - 1);
+  const int vpos = (int)fdiv((uint32_t)v, A.fH);
+  const int h = v - vpos * A.H;
+  const PhPos o = ph_pos(A, M, vpos);
+  // staged row of the phase's index 0, head h
+  const int rb0 = (o.b * A.L0 + o.pstart - lo) * A.H + h;
+  __syncthreads();
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto add = [&](float wk, int sr) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 t = xs[sr * NC + c];
+      acc[c].x = fmaf(wk, t.x, acc[c].x);
+      acc[c].y = fmaf(wk, t.y, acc[c].y);
+      acc[c].z = fmaf(wk, t.z, acc[c].z);
+      acc[c].w = fmaf(wk, t.w, acc[c].w);
+    }
+  };
+  const bool interior = f.b == l.b && f.r == l.r && f.m >= K && l.m <= l.plen - K - 1;
+  if (interior) {
+#pragma unroll
+    for (int t = -(K / 2); t <= K / 2; ++t) {
+      const int sr = rb0 + (o.m + t) * A.H;
+      add(ws[sr * K + (K / 2 - t)], sr);
+    }
+  } else {
+#pragma unroll 4
+    for (int t = -(K - 1); t <= K - 1; ++t) {
+      const int mq = o.m + t;
+      const int sl = o.m - min(max(mq - K / 2, 0), o.plen - K);
+      const bool ok = mq >= 0 && mq < o.plen && sl >= 0 && sl < K;
+      const int sr = ok ? rb0 + mq * A.H : rb0 + o.m * A.H;
+      add(ok ? ws[sr * K + sl] : 0.f, sr);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float4 r = acc[c];
+    r.x *= post;
+    r.y *= post;
+    r.z *= post;
+    r.w *= post;
+    sm4[tid * NC + c] = r;
+  }
+  __syncthreads();
+  ph_copy<false, false>(A, M, U.ry, U.fry, nullptr, reinterpret_cast<uint4 *>(out),
+                        reinterpret_cast<uint4 *>(sm4), row0 * NC, rows * NC);
 }
 
 // dk / dv: out[j] = post * sum over the queries i whose window holds key j
@@ -1362,6 +1445,21 @@ bool pair_launch_off() {
   return off;
 }
 
+// Whether dk (qk: the QK backward) or dv takes the phase-major inverse
+// before the contiguous staged inverse and its paired launch, where both
+// apply (d > 1).  The QK backward's dk does where the contiguous inverse's
+// halo is wide, (K - 1) d >= 12 with K >= 5 (config 5: K=7 d=2 23.7 -> 21.1
+// us, K=7 d=4 25.5 -> 22.0, K=5 d=4 20.5 -> 19.9, though its dq then runs
+// as a launch of its own); the AV backward keeps its pair (K=7 d=2 11.0 us
+// paired, 12.9 phase-major) and K = 3 both.  NATTEN_AMD_RPB_PHINV=1 / 0
+// forces / forbids it (A/B checks; read per call).
+bool phase_inverse_first(const RpbProb &A, bool qk) {
+  if (A.d0 < 2) return false;
+  const char *e = std::getenv("NATTEN_AMD_RPB_PHINV");
+  if (e != nullptr && (e[0] == '1' || e[0] == '0')) return e[0] == '1';
+  return qk && A.K0 >= 5 && (A.K0 - 1) * A.d0 >= 12;
+}
+
 bool r1_offsets_fit(const RpbProb &A) {
   return (int64_t)A.n_rows * std::max(A.K0, A.D) < ((int64_t)1 << 31);
 }
@@ -1424,6 +1522,17 @@ void ph_maps(const RpbProb &A, PhMap *M, PhUnits *U) {
   U->rk = A.H * A.K0 / 4;
   U->fry = make_fastdiv((uint32_t)U->ry);
   U->frk = make_fastdiv((uint32_t)U->rk);
+}
+
+// LDS of the phase-major inverse (rows of the staged query positions: x
+// rows and weight rows), or 0 where it does not apply; *cap: its rows.
+size_t ph_inverse_lds(const RpbProb &A, int *cap) {
+  if (ph_lds(A, false) == 0) return 0;
+  const int64_t pos = kPhBlock / A.H + 2 + 2 * (int64_t)(A.K0 - 1);
+  const int64_t rows = pos * A.H;
+  const size_t b = (size_t)rows * (A.D / 4) * 16 + (size_t)rows * A.K0 * 4;
+  if (cap != nullptr) *cap = (int)rows;
+  return b <= 65536 ? b : 0;
 }
 
 // Which rank-1 fp32 kernels apply (the launchers below and rpb_plan share
@@ -1568,6 +1677,36 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
 }
 
 // The rank-1 fp32 inverse (dk / dv) where the staged dot / gather apply.
+bool r1p_inverse(const RpbProb &A, const float *w, const float *x, float *out,
+                 float post, hipStream_t st) {
+  int cap = 0;
+  const size_t lds = ph_inverse_lds(A, &cap);
+  if (lds == 0) return false;
+  PhMap M;
+  PhUnits U;
+  ph_maps(A, &M, &U);
+  const dim3 pg((unsigned)((A.n_rows + kPhBlock - 1) / kPhBlock));
+#define R1PI_(KK, NC)                                                                  \
+  hipLaunchKernelGGL((k_r1p_inverse<KK, NC>), pg, dim3(kPhBlock), lds, st, A, M, U, w, \
+                     x, out, post, cap)
+  switch (A.D / 4) {
+#define NC_ 1
+    case 1: R1_K(A.K0, R1PI_) break;
+#undef NC_
+#define NC_ 2
+    case 2: R1_K(A.K0, R1PI_) break;
+#undef NC_
+#define NC_ 3
+    case 3: R1_K(A.K0, R1PI_) break;
+#undef NC_
+#define NC_ 4
+    default: R1_K(A.K0, R1PI_) break;
+#undef NC_
+  }
+#undef R1PI_
+  return true;
+}
+
 bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
                 float post, hipStream_t st) {
   const int rb = rpb_block(A);
@@ -1613,9 +1752,12 @@ bool r1_inverse(const RpbProb &A, const float *w, const float *x, float *out,
     case 11: BODY(11); break;            \
     default: BODY(13); break;            \
   }
+size_t ph_inverse_lds(const RpbProb &A, int *cap);
+
 bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const float *key,
                      float *dq, float *dk, double *bpart, hipStream_t st) {
   if (pair_launch_off()) return false;
+  if (phase_inverse_first(A, true) && ph_inverse_lds(A, nullptr) != 0) return false;
   const size_t lg = bpart != nullptr ? r1_bias_gather_lds(A) : r1_lds(A, rpb_block(A), false);
   const size_t li = r1_inverse_lds(A);
   // the pair shares one LDS size: an inverse above 64 KB would hold the
@@ -1651,6 +1793,7 @@ bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const fl
 
 bool r1_av_bwd_fused(const RpbProb &A, const float *attn, const float *v, const float *dout,
                      float *dattn, float *dv, hipStream_t st) {
+  if (phase_inverse_first(A, false) && ph_inverse_lds(A, nullptr) != 0) return false;
   if (pair_launch_off()) return false;
   const int rb = rpb_block(A);
   const size_t ld = r1_lds(A, rb, false);
@@ -1738,12 +1881,15 @@ void launch_gather(const RpbProb &A, const float *w, const void *y, void *out,
 
 template <typename TX, typename TO>
 void launch_inverse(const RpbProb &A, const float *w, const void *x, void *out,
-                    int scale_x, hipStream_t st) {
+                    int scale_x, hipStream_t st, bool qk) {
   if constexpr (sizeof(TX) == 4 && sizeof(TO) == 4) {
     // fp32 x: x scale is exact up to rounding, so the scale is applied to
     // the sums instead
-    if (r1_inverse(A, w, (const float *)x, (float *)out, scale_x ? A.scale : 1.f, st))
+    const float post = scale_x ? A.scale : 1.f;
+    if (phase_inverse_first(A, qk) && r1p_inverse(A, w, (const float *)x, (float *)out, post, st))
       return;
+    if (r1_inverse(A, w, (const float *)x, (float *)out, post, st)) return;
+    if (r1p_inverse(A, w, (const float *)x, (float *)out, post, st)) return;
   }
   constexpr int V = vmax_of<TX, TO>();
   const RShape s = rshape(A.D, V);
@@ -1835,7 +1981,7 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     if (dq != nullptr && n_fused == 0)
       launch_gather<T, T>(A, dlogits, key, dq, A.has_scale ? A.scale : 1.f,
                           st);
-    if (dk != nullptr) launch_inverse<T, T>(A, dlogits, q, dk, A.has_scale, st);
+    if (dk != nullptr) launch_inverse<T, T>(A, dlogits, q, dk, A.has_scale, st, true);
   });
   if (drpb != nullptr && n_fused > 0) {
     hipLaunchKernelGGL(k_rpb_bias_reduce, dim3((unsigned)(A.H * A.R0 * A.R1)), dim3(64), 0,
@@ -1861,8 +2007,15 @@ void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
   o->qk = kind(true);
   o->av = kind(false);
   o->dattn = kind(false);
-  o->dk = f32 && r1_inverse_lds(A) != 0 ? 1 : 0;
-  o->dv = o->dk;
+  const bool phinv = f32 && ph_inverse_lds(A, nullptr) != 0;
+  auto inv_kind = [&](bool qk) {
+    return phinv && phase_inverse_first(A, qk) ? (int)kR1Phase
+           : f32 && r1_inverse_lds(A) != 0     ? (int)kR1Staged
+           : phinv                             ? (int)kR1Phase
+                                               : 0;
+  };
+  o->dk = inv_kind(true);
+  o->dv = inv_kind(false);
   int32_t chunk, n_chunks;
   bias_chunking(A, &chunk, &n_chunks);
   const int rb = rpb_block(A);
@@ -1886,11 +2039,11 @@ void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
       if (dattn != nullptr)
         launch_dot<float, T>(A, dout, value, nullptr, dattn, 0, 0.f, st);
       if (dvalue != nullptr)
-        launch_inverse<float, T>(A, attn, dout, dvalue, 0, st);
+        launch_inverse<float, T>(A, attn, dout, dvalue, 0, st, false);
     } else {
       if (dattn != nullptr)
         launch_dot<T, T>(A, dout, value, nullptr, dattn, 0, 0.f, st);
-      if (dvalue != nullptr) launch_inverse<T, T>(A, attn, dout, dvalue, 0, st);
+      if (dvalue != nullptr) launch_inverse<T, T>(A, attn, dout, dvalue, 0, st, false);
     }
   });
 }

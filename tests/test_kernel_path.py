@@ -186,9 +186,18 @@ def test_config5_allin1_kernels():
             assert pl["qk"] == want and pl["av"] == want and pl["dattn"] == want, (K, d, pl)
             assert pl["fused_bias"] == (want == _lib.RPB_STAGED), (K, d, pl)
             assert pl["dq"] == want, (K, d, pl)
-    # staged dk / dv wherever their staged rows fit LDS
+    # staged dk / dv wherever their staged rows fit LDS, else phase-major
     assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dk"] == _lib.RPB_STAGED
     assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dv"] == _lib.RPB_STAGED
+    for K in (5, 7):
+        pl = _rpb_plan(8, 2048, 12, 12, K, 8)
+        assert pl["dk"] == _lib.RPB_PHASE and pl["dv"] == _lib.RPB_PHASE, (K, pl)
+    # the QK backward's dk on the phase-major inverse where the contiguous
+    # halo is wide ((K - 1) d >= 12, K >= 5); dv keeps the staged pair
+    for K, d, dk in ((7, 2, _lib.RPB_PHASE), (7, 4, _lib.RPB_PHASE), (5, 4, _lib.RPB_PHASE),
+                     (5, 2, _lib.RPB_STAGED), (3, 8, _lib.RPB_STAGED)):
+        pl = _rpb_plan(8, 2048, 12, 12, K, d)
+        assert pl["dk"] == dk and pl["dv"] == _lib.RPB_STAGED, (K, d, pl)
 
 
 def test_allin1_low_precision_takes_generic_kernels():
