@@ -831,19 +831,27 @@ __global__ void __launch_bounds__(512)
                  reinterpret_cast<uint4 *>(so), R.row0 * K / 4, R.rows * K / 4);
 }
 
+// bpart (the QK backward's dq pass): also the bias gradient's float64
+// partials, one per (cell, block), as the contiguous staged gather forms
+// them (the block's rows are (position, head) rows, heads innermost, in
+// phase-major order; the reduction adds blocks in order).
 template <int K, int NC>
 __global__ void __launch_bounds__(512)
     k_r1p_gather(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ wgt,
-                 const float *__restrict__ y, float *__restrict__ out, float post) {
+                 const float *__restrict__ y, float *__restrict__ out, float post,
+                 double *__restrict__ bpart) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
   const PhRows R = ph_rows<K>(A, M);
   float *sw = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
+  int *spb = reinterpret_cast<int *>(win + (nthr + 2 * r1_halo(K, 1, A.H)) * NC);
   ph_copy<true>(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(wgt), nullptr,
                 reinterpret_cast<uint4 *>(sw), R.row0 * K / 4, R.rows * K / 4);
   ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(y), nullptr,
                 reinterpret_cast<uint4 *>(win), R.lo * U.ry, (R.hi - R.lo) * U.ry);
+  if (bpart != nullptr)
+    spb[tid] = rwin_axis(K, A.d0, A.fd0, R.o.r + A.d0 * R.o.m, A.L0).pb;
   __syncthreads();
   const float4 *yb =
       win + ((R.o.b * A.L0 + R.o.pstart + R.wsm - R.lo) * A.H + R.h) * NC;
@@ -862,6 +870,21 @@ __global__ void __launch_bounds__(512)
       acc[c].y = fmaf(wk, t.y, acc[c].y);
       acc[c].z = fmaf(wk, t.z, acc[c].z);
       acc[c].w = fmaf(wk, t.w, acc[c].w);
+    }
+  }
+  if (bpart != nullptr) {
+    // thread (h, c) of the H (2K - 1) bias cells adds, in row order and in
+    // float64, the block's weights w[r, k] of head h with pb(r) + k = c
+    constexpr int R0 = 2 * K - 1;
+    if (tid < A.H * R0) {
+      const int h = tid / R0, c = tid - h * R0;
+      const int h0 = R.row0 - (int)fdiv((uint32_t)R.row0, A.fH) * A.H;
+      double acc_b = 0.0;
+      for (int j = h >= h0 ? h - h0 : h - h0 + A.H; j < R.rows; j += A.H) {
+        const int k = c - spb[j];
+        if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
+      }
+      bpart[(int64_t)tid * gridDim.x + blockIdx.x] = acc_b;
     }
   }
   __syncthreads();
@@ -1513,6 +1536,15 @@ size_t ph_lds(const RpbProb &A, bool bias) {
   return b <= 65536 ? b : 0;
 }
 
+// The phase-major gather that also forms the bias partials: one bias cell
+// per thread, each row's first cell in LDS after the window.
+size_t ph_bias_gather_lds(const RpbProb &A) {
+  const size_t l = ph_lds(A, false);
+  if (l == 0 || A.H * A.R0 > kPhBlock) return 0;
+  const size_t b = l + (size_t)kPhBlock * sizeof(int);
+  return b <= 65536 ? b : 0;
+}
+
 void ph_maps(const RpbProb &A, PhMap *M, PhUnits *U) {
   M->q = A.L0 / A.d0;
   M->rem = A.L0 % A.d0;
@@ -1619,24 +1651,25 @@ bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
   return true;
 }
 
+// The rank-1 fp32 gather: the staged contiguous kernel, else the
+// phase-major one; with bpart also the bias gradient's partials (*nblk: the
+// blocks, one partial each).  False where neither applies.
 bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
-               float post, hipStream_t st, double *bpart = nullptr) {
+               float post, hipStream_t st, double *bpart = nullptr, int *nblk = nullptr) {
   const int rb = rpb_block(A);
   size_t lds = r1_lds(A, rb, false);
-  if (bpart != nullptr) {
-    lds = r1_bias_gather_lds(A);
-    if (lds == 0) return false;
-  }
+  if (bpart != nullptr) lds = r1_bias_gather_lds(A);
   if (lds == 0) {
-    const size_t pl = ph_lds(A, false);
+    const size_t pl = bpart != nullptr ? ph_bias_gather_lds(A) : ph_lds(A, false);
     if (pl == 0) return false;
     PhMap M;
     PhUnits U;
     ph_maps(A, &M, &U);
     const dim3 pg((unsigned)((A.n_rows + kPhBlock - 1) / kPhBlock));
+    if (nblk != nullptr) *nblk = (int)pg.x;
 #define R1PG_(KK, NC)                                                                \
   hipLaunchKernelGGL((k_r1p_gather<KK, NC>), pg, dim3(kPhBlock), pl, st, A, M, U, w, \
-                     y, out, post)
+                     y, out, post, bpart)
     switch (A.D / 4) {
 #define NC_ 1
       case 1: R1_K(A.K0, R1PG_) break;
@@ -1655,6 +1688,7 @@ bool r1_gather(const RpbProb &A, const float *w, const float *y, float *out,
     return true;
   }
   const dim3 grid((unsigned)((A.n_rows + rb - 1) / rb));
+  if (nblk != nullptr) *nblk = (int)grid.x;
 #define R1G_(KK, NC)                                                              \
   hipLaunchKernelGGL((k_r1_gather<KK, NC>), grid, dim3(rb), lds, st, A, w, y, out, post, \
                      bpart)
@@ -1969,11 +2003,15 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
     }
   }
   if (!pair && drpb != nullptr && dq != nullptr && dtype == NA_F32 && A.n_rows > 0) {
-    const int32_t nblk = (A.n_rows + rpb_block(A) - 1) / rpb_block(A);
+    // the staged gather's blocks, or the phase-major one's
+    const int32_t nblk = r1_bias_gather_lds(A) != 0
+                             ? (A.n_rows + rpb_block(A) - 1) / rpb_block(A)
+                             : (A.n_rows + kPhBlock - 1) / kPhBlock;
+    int used = 0;
     if (nblk <= n_chunks &&
         r1_gather(A, dlogits, (const float *)key, (float *)dq, A.has_scale ? A.scale : 1.f,
-                  st, (double *)workspace))
-      n_fused = nblk;
+                  st, (double *)workspace, &used))
+      n_fused = used;
   }
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -2020,8 +2058,12 @@ void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
   bias_chunking(A, &chunk, &n_chunks);
   const int rb = rpb_block(A);
   const int64_t nblk = ((int64_t)A.n_rows + rb - 1) / rb;
-  o->fused_bias = f32 && A.n_rows > 0 && nblk <= n_chunks && r1_bias_gather_lds(A) != 0;
-  o->dq = o->fused_bias ? 1 : kind(false);
+  const int64_t nph = ((int64_t)A.n_rows + kPhBlock - 1) / kPhBlock;
+  const bool staged_bias = r1_bias_gather_lds(A) != 0;
+  const bool phase_bias = !staged_bias && ph_bias_gather_lds(A) != 0;
+  o->fused_bias = f32 && A.n_rows > 0 &&
+                  ((staged_bias && nblk <= n_chunks) || (phase_bias && nph <= n_chunks));
+  o->dq = o->fused_bias ? (staged_bias ? (int)kR1Staged : (int)kR1Phase) : kind(false);
   o->block = o->qk == kR1Phase ? kPhBlock : rb;
 }
 

@@ -183,12 +183,12 @@ def test_config5_full(K, d):
     f32 = torch.float32
     B, L, H, D = 8, 2048, 12, 12
     # the kernels the bench times: staged rank-1 (phase-major at K >= 5,
-    # d = 8), and the dq pass forming the bias partials on the staged ones
+    # d = 8), and the dq pass (either) forming the bias partials
     pp = _lib.make_rpb_params(1, B, H, D, (L,), K, d, False, _lib.NA_F32, 0.288)
     pl = _lib.NaRpbPlan()
     assert _lib.load().na_rpb_kernel_plan(ctypes.byref(pp), ctypes.byref(pl)) == 0
     want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
-    assert (pl.qk, pl.av, pl.dq) == (want,) * 3 and pl.fused_bias == (want == _lib.RPB_STAGED)
+    assert (pl.qk, pl.av, pl.dq) == (want,) * 3 and pl.fused_bias == 1
     q, k, v = (randn((B, L, H, D), f32, s) for s in (40, 41, 42))
     rpb = randn((H, 2 * K - 1), f32, 43, std=0.02)
     qd, kd = _dev(q, k)
