@@ -751,10 +751,10 @@ struct PhRows {
 };
 
 template <int K>
-__device__ __forceinline__ PhRows ph_rows(const RpbProb &A, const PhMap &M) {
+__device__ __forceinline__ PhRows ph_rows(const RpbProb &A, const PhMap &M, int bid) {
   PhRows R;
   const int nthr = (int)blockDim.x;
-  R.row0 = (int)blockIdx.x * nthr;
+  R.row0 = bid * nthr;
   R.rows = min(nthr, A.n_rows - R.row0);
   const PhPos f = ph_pos(A, M, (int)fdiv((uint32_t)R.row0, A.fH));
   const PhPos l = ph_pos(A, M, (int)fdiv((uint32_t)(R.row0 + R.rows - 1), A.fH));
@@ -777,13 +777,14 @@ struct PhUnits {
 };
 
 template <int K, int NC>
-__global__ void __launch_bounds__(512)
-    k_r1p_dot(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ x,
-              const float *__restrict__ y, const float *__restrict__ rpb,
-              float *__restrict__ out, int scale_x) {
+__device__ __forceinline__ void r1p_dot_body(int bid, const RpbProb &A, const PhMap &M,
+                                             const PhUnits &U, const float *__restrict__ x,
+                                             const float *__restrict__ y,
+                                             const float *__restrict__ rpb,
+                                             float *__restrict__ out, int scale_x) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
-  const PhRows R = ph_rows<K>(A, M);
+  const PhRows R = ph_rows<K>(A, M, bid);
   float *so = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   constexpr int R0 = 2 * K - 1;
@@ -831,18 +832,28 @@ __global__ void __launch_bounds__(512)
                  reinterpret_cast<uint4 *>(so), R.row0 * K / 4, R.rows * K / 4);
 }
 
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_dot(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ x,
+              const float *__restrict__ y, const float *__restrict__ rpb,
+              float *__restrict__ out, int scale_x) {
+  r1p_dot_body<K, NC>((int)blockIdx.x, A, M, U, x, y, rpb, out, scale_x);
+}
+
 // bpart (the QK backward's dq pass): also the bias gradient's float64
 // partials, one per (cell, block), as the contiguous staged gather forms
 // them (the block's rows are (position, head) rows, heads innermost, in
 // phase-major order; the reduction adds blocks in order).
 template <int K, int NC>
-__global__ void __launch_bounds__(512)
-    k_r1p_gather(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ wgt,
-                 const float *__restrict__ y, float *__restrict__ out, float post,
-                 double *__restrict__ bpart) {
+__device__ __forceinline__ void r1p_gather_body(int bid, int nblk, const RpbProb &A,
+                                                const PhMap &M, const PhUnits &U,
+                                                const float *__restrict__ wgt,
+                                                const float *__restrict__ y,
+                                                float *__restrict__ out, float post,
+                                                double *__restrict__ bpart) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
-  const PhRows R = ph_rows<K>(A, M);
+  const PhRows R = ph_rows<K>(A, M, bid);
   float *sw = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   int *spb = reinterpret_cast<int *>(win + (nthr + 2 * r1_halo(K, 1, A.H)) * NC);
@@ -884,7 +895,7 @@ __global__ void __launch_bounds__(512)
         const int k = c - spb[j];
         if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
       }
-      bpart[(int64_t)tid * gridDim.x + blockIdx.x] = acc_b;
+      bpart[(int64_t)tid * nblk + bid] = acc_b;
     }
   }
   __syncthreads();
@@ -902,6 +913,14 @@ __global__ void __launch_bounds__(512)
                  reinterpret_cast<uint4 *>(sm4), R.row0 * NC, R.rows * NC);
 }
 
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_gather(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ wgt,
+                 const float *__restrict__ y, float *__restrict__ out, float post,
+                 double *__restrict__ bpart) {
+  r1p_gather_body<K, NC>((int)blockIdx.x, (int)gridDim.x, A, M, U, wgt, y, out, post, bpart);
+}
+
 // dk / dv on the phase-major rows (d > 1): one thread per key row in the
 // order (sample, phase, index m, head).  In phase units the queries whose
 // windows hold key m are [m <= K-1 ? 0 : m - K/2, m >= plen-K ? plen-1 :
@@ -913,13 +932,13 @@ __global__ void __launch_bounds__(512)
 // of one phase the K candidates m + t, |t| <= K/2, take slot K/2 - t with no
 // window test (the interior rule of the contiguous inverse in phase units).
 template <int K, int NC>
-__global__ void __launch_bounds__(512)
-    k_r1p_inverse(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ w,
-                  const float *__restrict__ x, float *__restrict__ out, float post,
-                  int cap) {
+__device__ __forceinline__ void r1p_inverse_body(int bid, const RpbProb &A, const PhMap &M,
+                                                 const PhUnits &U, const float *__restrict__ w,
+                                                 const float *__restrict__ x,
+                                                 float *__restrict__ out, float post, int cap) {
   extern __shared__ __align__(16) float4 sm4[];
   const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
-  const int row0 = (int)blockIdx.x * nthr;
+  const int row0 = bid * nthr;
   const int rows = min(nthr, A.n_rows - row0);
   const PhPos f = ph_pos(A, M, (int)fdiv((uint32_t)row0, A.fH));
   const PhPos l = ph_pos(A, M, (int)fdiv((uint32_t)(row0 + rows - 1), A.fH));
@@ -981,6 +1000,43 @@ __global__ void __launch_bounds__(512)
   __syncthreads();
   ph_copy<false, false>(A, M, U.ry, U.fry, nullptr, reinterpret_cast<uint4 *>(out),
                         reinterpret_cast<uint4 *>(sm4), row0 * NC, rows * NC);
+}
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_inverse(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ w,
+                  const float *__restrict__ x, float *__restrict__ out, float post,
+                  int cap) {
+  r1p_inverse_body<K, NC>((int)blockIdx.x, A, M, U, w, x, out, post, cap);
+}
+
+// A backward's two passes on the phase-major rows in one launch: blocks
+// [0, n0) the first pass (QK: dq by the gather over dlogits, with the bias
+// partials when bpart is set; AV: dattn by the dot of dout with the
+// values), the others the inverse (dk or dv).
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_qkb(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ dl,
+              const float *__restrict__ q, const float *__restrict__ key,
+              float *__restrict__ dq, float *__restrict__ dk, float post,
+              double *__restrict__ bpart, int n0, int cap) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    r1p_gather_body<K, NC>(bid, n0, A, M, U, dl, key, dq, post, bpart);
+  else
+    r1p_inverse_body<K, NC>(bid - n0, A, M, U, dl, q, dk, post, cap);
+}
+
+template <int K, int NC>
+__global__ void __launch_bounds__(512)
+    k_r1p_avb(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ attn,
+              const float *__restrict__ v, const float *__restrict__ dout,
+              float *__restrict__ dattn, float *__restrict__ dv, int n0, int cap) {
+  const int bid = (int)blockIdx.x;
+  if (bid < n0)
+    r1p_dot_body<K, NC>(bid, A, M, U, dout, v, nullptr, dattn, 0);
+  else
+    r1p_inverse_body<K, NC>(bid - n0, A, M, U, attn, dout, dv, 1.f, cap);
 }
 
 // dk / dv: out[j] = post * sum over the queries i whose window holds key j
@@ -1459,28 +1515,42 @@ size_t window_bytes(const RpbProb &A, int lgG, size_t slot_bytes, int rb) {
 // 2^31 (larger problems take the generic kernels, whose row offsets are
 // 64-bit).
 // NATTEN_AMD_RPB_PAIR=0 keeps the backward's two passes in two launches
-// (A/B checks of k_r1_qkb / k_r1_avb).
+// (A/B checks of k_r1_qkb / k_r1_avb / k_r1p_qkb / k_r1p_avb; read per
+// call).
 bool pair_launch_off() {
-  static const bool off = [] {
-    const char *e = std::getenv("NATTEN_AMD_RPB_PAIR");
-    return e != nullptr && e[0] == '0';
-  }();
-  return off;
+  const char *e = std::getenv("NATTEN_AMD_RPB_PAIR");
+  return e != nullptr && e[0] == '0';
 }
 
-// Whether dk (qk: the QK backward) or dv takes the phase-major inverse
-// before the contiguous staged inverse and its paired launch, where both
-// apply (d > 1).  The QK backward's dk does where the contiguous inverse's
-// halo is wide, (K - 1) d >= 12 with K >= 5 (config 5: K=7 d=2 23.7 -> 21.1
-// us, K=7 d=4 25.5 -> 22.0, K=5 d=4 20.5 -> 19.9, though its dq then runs
-// as a launch of its own); the AV backward keeps its pair (K=7 d=2 11.0 us
-// paired, 12.9 phase-major) and K = 3 both.  NATTEN_AMD_RPB_PHINV=1 / 0
-// forces / forbids it (A/B checks; read per call).
+// Whether dk (qk: the QK backward) or dv, as a launch of its own (the
+// paired launches off or not applicable), takes the phase-major inverse
+// before the contiguous staged inverse, where both apply (d > 1).  The QK
+// backward's dk does where the contiguous inverse's halo is wide,
+// (K - 1) d >= 12 with K >= 5 (config 5, dq a launch of its own: K=7 d=2
+// 23.7 -> 21.1 us, K=7 d=4 25.5 -> 22.0, K=5 d=4 20.5 -> 19.9); the AV
+// backward's dv and K = 3 keep the staged inverse.  NATTEN_AMD_RPB_PHINV=1
+// / 0 forces / forbids it (A/B checks; read per call).
 bool phase_inverse_first(const RpbProb &A, bool qk) {
   if (A.d0 < 2) return false;
   const char *e = std::getenv("NATTEN_AMD_RPB_PHINV");
   if (e != nullptr && (e[0] == '1' || e[0] == '0')) return e[0] == '1';
   return qk && A.K0 >= 5 && (A.K0 - 1) * A.d0 >= 12;
+}
+
+// Whether the backward's phase-major pair (k_r1p_qkb / k_r1p_avb) goes
+// before the staged kernels where both apply: the QK backward's where
+// (K - 1) d >= 8, the AV backward's where K >= 5 and (K - 1) d >= 12
+// (config 5 qk / av backward, staged -> phase-major pair: K=5 d=2 qk 16.1
+// -> 14.6 us, K=3 d=8 qk 15.0 -> 13.6, K=7 d=4 22.0 -> 17.9 and av 13.25 ->
+// 10.25, K=7 d=2 av 11.2 -> 10.2; K=3 d=2 qk 11.4 -> 13.2 and K=3 av
+// 7.0-8.0 -> 8.6-8.9 stay staged).  NATTEN_AMD_RPB_PHPAIR=1 / 0 forces /
+// forbids it (A/B checks; read per call).
+bool phase_pair_first(const RpbProb &A, bool qk) {
+  if (A.d0 < 2) return false;
+  const char *e = std::getenv("NATTEN_AMD_RPB_PHPAIR");
+  if (e != nullptr && (e[0] == '1' || e[0] == '0')) return e[0] == '1';
+  const int span = (A.K0 - 1) * A.d0;
+  return qk ? span >= 8 : A.K0 >= 5 && span >= 12;
 }
 
 bool r1_offsets_fit(const RpbProb &A) {
@@ -1791,7 +1861,9 @@ size_t ph_inverse_lds(const RpbProb &A, int *cap);
 bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const float *key,
                      float *dq, float *dk, double *bpart, hipStream_t st) {
   if (pair_launch_off()) return false;
-  if (phase_inverse_first(A, true) && ph_inverse_lds(A, nullptr) != 0) return false;
+  if ((phase_inverse_first(A, true) || phase_pair_first(A, true)) &&
+      ph_inverse_lds(A, nullptr) != 0)
+    return false;
   const size_t lg = bpart != nullptr ? r1_bias_gather_lds(A) : r1_lds(A, rpb_block(A), false);
   const size_t li = r1_inverse_lds(A);
   // the pair shares one LDS size: an inverse above 64 KB would hold the
@@ -1827,7 +1899,9 @@ bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const fl
 
 bool r1_av_bwd_fused(const RpbProb &A, const float *attn, const float *v, const float *dout,
                      float *dattn, float *dv, hipStream_t st) {
-  if (phase_inverse_first(A, false) && ph_inverse_lds(A, nullptr) != 0) return false;
+  if ((phase_inverse_first(A, false) || phase_pair_first(A, false)) &&
+      ph_inverse_lds(A, nullptr) != 0)
+    return false;
   if (pair_launch_off()) return false;
   const int rb = rpb_block(A);
   const size_t ld = r1_lds(A, rb, false);
@@ -1855,6 +1929,77 @@ bool r1_av_bwd_fused(const RpbProb &A, const float *attn, const float *v, const 
   R1_KD(A.K0, AVB_NC);
 #undef AVB_NC
 #undef AVB_
+  return true;
+}
+
+// The same pairs on the phase-major kernels (k_r1p_qkb / k_r1p_avb): where
+// the first pass (dq's gather, dattn's dot) is phase-major, because the
+// staged one does not apply, and the inverse is phase-major too.  Both
+// halves run kPhBlock-row blocks, so the launch is two equal halves.
+bool r1p_pair_lds(const RpbProb &A, bool qk, size_t first, size_t *lds, int *cap) {
+  if (pair_launch_off() || first == 0) return false;
+  const bool phase_inv =
+      phase_pair_first(A, qk) || phase_inverse_first(A, qk) || r1_inverse_lds(A) == 0;
+  const size_t li = ph_inverse_lds(A, cap);
+  if (!phase_inv || li == 0) return false;
+  *lds = std::max(first, li);
+  return true;
+}
+
+bool r1p_qk_bwd_pair(const RpbProb &A, const float *dl, const float *q, const float *key,
+                     float *dq, float *dk, double *bpart, hipStream_t st) {
+  const bool staged = bpart != nullptr ? r1_bias_gather_lds(A) != 0
+                                       : r1_lds(A, rpb_block(A), false) != 0;
+  if (staged && !phase_pair_first(A, true)) return false;
+  size_t lds = 0;
+  int cap = 0;
+  if (!r1p_pair_lds(A, true, bpart != nullptr ? ph_bias_gather_lds(A) : ph_lds(A, false),
+                    &lds, &cap))
+    return false;
+  PhMap M;
+  PhUnits U;
+  ph_maps(A, &M, &U);
+  const int n0 = (A.n_rows + kPhBlock - 1) / kPhBlock;
+  const float post = A.has_scale ? A.scale : 1.f;
+#define QKP_(KK, NC)                                                                    \
+  hipLaunchKernelGGL((k_r1p_qkb<KK, NC>), dim3((unsigned)(2 * n0)), dim3(kPhBlock), lds, \
+                     st, A, M, U, dl, q, key, dq, dk, post, bpart, n0, cap)
+#define QKP_NC(KK)                \
+  do {                            \
+    if (A.D == 4) QKP_(KK, 1);    \
+    else if (A.D == 8) QKP_(KK, 2); \
+    else if (A.D == 12) QKP_(KK, 3); \
+    else QKP_(KK, 4);             \
+  } while (0)
+  R1_KD(A.K0, QKP_NC);
+#undef QKP_NC
+#undef QKP_
+  return true;
+}
+
+bool r1p_av_bwd_pair(const RpbProb &A, const float *attn, const float *v, const float *dout,
+                     float *dattn, float *dv, hipStream_t st) {
+  if (r1_lds(A, rpb_block(A), false) != 0 && !phase_pair_first(A, false)) return false;
+  size_t lds = 0;
+  int cap = 0;
+  if (!r1p_pair_lds(A, false, ph_lds(A, false), &lds, &cap)) return false;
+  PhMap M;
+  PhUnits U;
+  ph_maps(A, &M, &U);
+  const int n0 = (A.n_rows + kPhBlock - 1) / kPhBlock;
+#define AVP_(KK, NC)                                                                    \
+  hipLaunchKernelGGL((k_r1p_avb<KK, NC>), dim3((unsigned)(2 * n0)), dim3(kPhBlock), lds, \
+                     st, A, M, U, attn, v, dout, dattn, dv, n0, cap)
+#define AVP_NC(KK)                \
+  do {                            \
+    if (A.D == 4) AVP_(KK, 1);    \
+    else if (A.D == 8) AVP_(KK, 2); \
+    else if (A.D == 12) AVP_(KK, 3); \
+    else AVP_(KK, 4);             \
+  } while (0)
+  R1_KD(A.K0, AVP_NC);
+#undef AVP_NC
+#undef AVP_
   return true;
 }
 #undef R1_KD
@@ -2001,6 +2146,14 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
       pair = true;
       if (bias) n_fused = nblk;
     }
+    const int32_t nph = (A.n_rows + kPhBlock - 1) / kPhBlock;
+    const bool pbias = drpb != nullptr && nph <= n_chunks;
+    if (!pair && (drpb == nullptr || pbias) &&
+        r1p_qk_bwd_pair(A, dlogits, (const float *)q, (const float *)key, (float *)dq,
+                        (float *)dk, pbias ? (double *)workspace : nullptr, st)) {
+      pair = true;
+      if (pbias) n_fused = nph;
+    }
   }
   if (!pair && drpb != nullptr && dq != nullptr && dtype == NA_F32 && A.n_rows > 0) {
     // the staged gather's blocks, or the phase-major one's
@@ -2046,8 +2199,10 @@ void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
   o->av = kind(false);
   o->dattn = kind(false);
   const bool phinv = f32 && ph_inverse_lds(A, nullptr) != 0;
+  const bool pairs = !pair_launch_off();
   auto inv_kind = [&](bool qk) {
-    return phinv && phase_inverse_first(A, qk) ? (int)kR1Phase
+    return phinv && (phase_inverse_first(A, qk) || (pairs && phase_pair_first(A, qk)))
+               ? (int)kR1Phase
            : f32 && r1_inverse_lds(A) != 0     ? (int)kR1Staged
            : phinv                             ? (int)kR1Phase
                                                : 0;
@@ -2059,7 +2214,13 @@ void rpb_plan(const RpbProb &A, int dtype, RpbPlanInfo *o) {
   const int rb = rpb_block(A);
   const int64_t nblk = ((int64_t)A.n_rows + rb - 1) / rb;
   const int64_t nph = ((int64_t)A.n_rows + kPhBlock - 1) / kPhBlock;
-  const bool staged_bias = r1_bias_gather_lds(A) != 0;
+  // the QK backward's phase-major pair takes dq (and the partials) where it
+  // goes first
+  const bool ppair = f32 && phinv && pairs && phase_pair_first(A, true) &&
+                     ph_bias_gather_lds(A) != 0 && nph <= n_chunks;
+  if (f32 && phinv && pairs && phase_pair_first(A, false) && ph_lds(A, false) != 0)
+    o->dattn = (int)kR1Phase;  // the AV backward's phase-major pair
+  const bool staged_bias = !ppair && r1_bias_gather_lds(A) != 0;
   const bool phase_bias = !staged_bias && ph_bias_gather_lds(A) != 0;
   o->fused_bias = f32 && A.n_rows > 0 &&
                   ((staged_bias && nblk <= n_chunks) || (phase_bias && nph <= n_chunks));
@@ -2072,8 +2233,10 @@ void rpb_av_bwd(const RpbProb &A, int dtype, int out_dtype, const float *attn,
                 hipStream_t st) {
   // fp32 (dout fp32 whatever out_dtype): dattn and dv in one launch
   if (dtype == NA_F32 && dattn != nullptr && dvalue != nullptr && A.n_rows > 0 &&
-      r1_av_bwd_fused(A, attn, (const float *)value, (const float *)dout, dattn,
-                      (float *)dvalue, st))
+      (r1_av_bwd_fused(A, attn, (const float *)value, (const float *)dout, dattn,
+                       (float *)dvalue, st) ||
+       r1p_av_bwd_pair(A, attn, (const float *)value, (const float *)dout, dattn,
+                       (float *)dvalue, st)))
     return;
   with_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);

@@ -246,3 +246,31 @@ def test_allin1_1d_low_precision_dilated(dtype):
     q, k, v = (randn((B, L, H, D), dtype, s) for s in (61, 62, 63))
     rpb = randn((H, 2 * K - 1), torch.float32, 64, std=0.02)
     _check_qk_av(q, k, v, rpb, K, d, 0.288, dtype, f"1d {dtype} K{K} d{d}")
+
+
+@pytest.mark.parametrize("B,L,H,D,K,d", PHASE_1D[:2] + [(2, 2048, 12, 8, 7, 8)])
+def test_allin1_backward_pairs_match_separate_launches(B, L, H, D, K, d, monkeypatch):
+    """The backward's paired launches (dq with dk and the bias partials,
+    dattn with dv) against the same passes as separate launches
+    (NATTEN_AMD_RPB_PAIR=0): bit for bit."""
+    from natten_amd.extras.allin1 import na1d_av_fused, na1d_qk_rpb
+
+    _say(f"[case] allin1 pairs B={B} L={L} H={H} D={D} K={K} d={d}")
+    q, k, v = (randn((B, L, H, D), torch.float32, s).to(DEV) for s in (71, 72, 73))
+    rpb = randn((H, 2 * K - 1), torch.float32, 74, std=0.02).to(DEV)
+    g = randn((B, L, H, K), torch.float32, 75).to(DEV)
+    attn = torch.softmax(randn((B, L, H, K), torch.float32, 76), -1).to(DEV)
+    go = randn((B, L, H, D), torch.float32, 77).to(DEV)
+
+    def run():
+        ts = [t.detach().clone().requires_grad_(True) for t in (q, k, rpb)]
+        gq = torch.autograd.grad(na1d_qk_rpb(ts[0], ts[1], ts[2], K, d, scale=0.3), ts, g)
+        a_, v_ = (t.detach().clone().requires_grad_(True) for t in (attn, v))
+        ga = torch.autograd.grad(na1d_av_fused(a_, v_, K, d), (a_, v_), go)
+        return [*gq, *ga]
+
+    paired = run()
+    monkeypatch.setenv("NATTEN_AMD_RPB_PAIR", "0")
+    apart = run()
+    for a, b, n in zip(paired, apart, ("dq", "dk", "drpb", "dattn", "dv")):
+        assert torch.equal(a, b), n

@@ -23,6 +23,8 @@ fp16 / bf16 2e-2 absolute (or one ulp of the dtype).
 
 import sys
 
+import os
+
 import pytest
 import torch
 
@@ -183,12 +185,16 @@ def test_config5_full(K, d):
     f32 = torch.float32
     B, L, H, D = 8, 2048, 12, 12
     # the kernels the bench times: staged rank-1 (phase-major at K >= 5,
-    # d = 8), and the dq pass (either) forming the bias partials
+    # d = 8), and the dq pass (either; phase-major in the QK backward's
+    # phase-major pair) forming the bias partials
     pp = _lib.make_rpb_params(1, B, H, D, (L,), K, d, False, _lib.NA_F32, 0.288)
     pl = _lib.NaRpbPlan()
     assert _lib.load().na_rpb_kernel_plan(ctypes.byref(pp), ctypes.byref(pl)) == 0
     want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
-    assert (pl.qk, pl.av, pl.dq) == (want,) * 3 and pl.fused_bias == 1
+    qk_pair = d > 1 and (K - 1) * d >= 8
+    assert (pl.qk, pl.av) == (want,) * 2 and pl.fused_bias == 1
+    if "NATTEN_AMD_RPB_PHPAIR" not in os.environ:  # the default rule
+        assert pl.dq == (_lib.RPB_PHASE if qk_pair else want)
     q, k, v = (randn((B, L, H, D), f32, s) for s in (40, 41, 42))
     rpb = randn((H, 2 * K - 1), f32, 43, std=0.02)
     qd, kd = _dev(q, k)

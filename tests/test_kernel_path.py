@@ -176,28 +176,24 @@ def test_config5_allin1_kernels():
     """Config 5 ([8, 2048, 12, 12] fp32): the staged rank-1 kernels for
     every K x d except K = 5 and 7 at d = 8, whose contiguous halos are too
     wide and which run phase-major; the dq pass (staged or phase-major)
-    forms the bias partials."""
+    forms the bias partials; the backward's pairs run phase-major where
+    the dilated span is wide."""
     from natten_amd._core import _lib
 
     for K in (3, 5, 7):
         for d in (1, 2, 4, 8):
             pl = _rpb_plan(8, 2048, 12, 12, K, d)
             want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
-            assert pl["qk"] == want and pl["av"] == want and pl["dattn"] == want, (K, d, pl)
+            assert pl["qk"] == want and pl["av"] == want, (K, d, pl)
             assert pl["fused_bias"], (K, d, pl)  # staged or phase-major dq pass
-            assert pl["dq"] == want, (K, d, pl)
-    # staged dk / dv wherever their staged rows fit LDS, else phase-major
-    assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dk"] == _lib.RPB_STAGED
-    assert _rpb_plan(8, 2048, 12, 12, 7, 1)["dv"] == _lib.RPB_STAGED
-    for K in (5, 7):
-        pl = _rpb_plan(8, 2048, 12, 12, K, 8)
-        assert pl["dk"] == _lib.RPB_PHASE and pl["dv"] == _lib.RPB_PHASE, (K, pl)
-    # the QK backward's dk on the phase-major inverse where the contiguous
-    # halo is wide ((K - 1) d >= 12, K >= 5); dv keeps the staged pair
-    for K, d, dk in ((7, 2, _lib.RPB_PHASE), (7, 4, _lib.RPB_PHASE), (5, 4, _lib.RPB_PHASE),
-                     (5, 2, _lib.RPB_STAGED), (3, 8, _lib.RPB_STAGED)):
-        pl = _rpb_plan(8, 2048, 12, 12, K, d)
-        assert pl["dk"] == dk and pl["dv"] == _lib.RPB_STAGED, (K, d, pl)
+            # the backward's phase-major pairs: dq with dk where
+            # (K - 1) d >= 8, dattn with dv where K >= 5 and (K - 1) d >= 12
+            qk_pair = d > 1 and (K - 1) * d >= 8
+            av_pair = d > 1 and K >= 5 and (K - 1) * d >= 12
+            assert pl["dq"] == (_lib.RPB_PHASE if qk_pair else want), (K, d, pl)
+            assert pl["dk"] == (_lib.RPB_PHASE if qk_pair else _lib.RPB_STAGED), (K, d, pl)
+            assert pl["dattn"] == (_lib.RPB_PHASE if av_pair else want), (K, d, pl)
+            assert pl["dv"] == (_lib.RPB_PHASE if av_pair else _lib.RPB_STAGED), (K, d, pl)
 
 
 def test_allin1_low_precision_takes_generic_kernels():
