@@ -6,6 +6,8 @@
 // host-side choice of wave tile, workgroup and LDS layout.
 #pragma once
 
+#include <cstring>
+
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -680,7 +682,7 @@ int box_max(const Axis &x, int t, bool inverse) {
 // box per wave whose box fits the LDS budget.  For the backward the boxes
 // also cover the inverse windows (query boxes of key tiles) and the LDS
 // holds a (lse, delta) pair per staged row.
-LChoice lean_choice(const Prob &P, LMode mode) {
+LChoice lean_choice_compute(const Prob &P, LMode mode) {
   const int R = P.rank, lead = 3 - R;
   LChoice best{};
   best.ok = false;
@@ -807,6 +809,46 @@ LChoice lean_choice(const Prob &P, LMode mode) {
       }
   }
   return best;
+}
+
+// lean_choice, cached: a training loop plans the same few problems on every
+// call, and the enumeration above costs microseconds of host time each time
+// (several times per call: eligibility, workspace size, launch).  The key
+// is every input the choice reads (the environment overrides it also reads
+// are fixed for the process); the cache is per host thread, so it needs no
+// lock, and keeps the last kPlanCache problems.
+constexpr int kPlanCache = 8;
+struct LChoiceKey {
+  int32_t v[20];
+};
+LChoice lean_choice(const Prob &P, LMode mode) {
+  LChoiceKey key{};
+  int n = 0;
+  key.v[n++] = (int32_t)mode;
+  key.v[n++] = P.rank;
+  key.v[n++] = P.D;
+  key.v[n++] = P.kprod;
+  key.v[n++] = P.n_extra;
+  key.v[n++] = P.sample_extent != nullptr ? 1 : 0;
+  key.v[n++] = P.B;
+  key.v[n++] = P.Hkv;
+  for (int a = 0; a < 3; ++a) {
+    key.v[n++] = P.ax[a].L;
+    key.v[n++] = P.ax[a].K;
+    key.v[n++] = P.ax[a].d;
+    key.v[n++] = P.ax[a].causal;
+  }
+  thread_local LChoiceKey keys[kPlanCache];
+  thread_local LChoice vals[kPlanCache];
+  thread_local int used = 0, next = 0;
+  for (int i = 0; i < used; ++i)
+    if (std::memcmp(&keys[i], &key, sizeof key) == 0) return vals[i];
+  const LChoice c = lean_choice_compute(P, mode);
+  keys[next] = key;
+  vals[next] = c;
+  next = (next + 1) % kPlanCache;
+  used = std::min(used + 1, kPlanCache);
+  return c;
 }
 
 LProb make_lprob(const Prob &P, const LChoice &C) {

@@ -218,3 +218,31 @@ def test_allin1_32bit_offset_limit():
     assert ok["qk"] == _lib.RPB_STAGED and ok["dk"] == _lib.RPB_STAGED
     # the phase-major kernels obey the same limit
     assert _rpb_plan(1, 15_000_000, 12, 12, 7, 8)["qk"] == _lib.RPB_GENERIC
+
+
+def test_plan_cache_returns_the_computed_plans():
+    """The host planner caches its launch choice per problem (a few per
+    thread): plans of more problems than the cache holds, asked for in
+    interleaved order, equal the plans computed first, forward and
+    backward, and two problems that differ only in batch or key/value
+    heads get their own plans."""
+    probs = [((b, 56, 56, 4, 32), 4, (7, 7), (d, d), (False, False))
+             for b in (1, 2, 4) for d in (1, 2, 4)]
+    probs += [((2, 300, 8, 64), 2, (9,), (2,), (False,)),
+              ((1, 16, 32, 32, 8, 64), 8, (3, 7, 7), (1, 1, 1), (True, False, False)),
+              ((8, 4096, 16, 64), 4, (63,), (2,), (False,))]
+    first = {}
+    for rep in range(3):
+        order = probs if rep % 2 == 0 else probs[::-1]
+        for pr in order:
+            for bwd in (False, True):
+                got = _plan(*pr, backward=bwd)
+                key = (pr, bwd)
+                if key in first:
+                    assert got == first[key], (pr, bwd)
+                else:
+                    first[key] = got
+    # batch and kv heads enter the backward's rank-2 wave rule
+    a = _plan((4, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False), backward=True)
+    b = _plan((1, 56, 56, 4, 32), 4, (7, 7), (1, 1), (False, False), backward=True)
+    assert a["workgroups"] != b["workgroups"]
