@@ -547,7 +547,10 @@ int na_qk_fwd(const na_params *p, const void *q, const void *k, void *logits,
   if (P.B == 0) return NA_OK;
   if (q == nullptr || k == nullptr || logits == nullptr)
     return fail(NA_ERR_INVALID, "q/k/logits must be non-NULL");
-  if (use_lsplit(p, P))
+  if (use_lsplit(p, P) && na::vsplit_on() &&
+      na::vsplit_qk(P, p->dtype, q, k, logits, P.scale, as_stream(stream)))
+    ;
+  else if (use_lsplit(p, P))
     na::lsplit_qk(P, p->dtype, q, k, logits, P.scale, -INFINITY,
                   as_stream(stream));
   else if (use_msplit(p, P))

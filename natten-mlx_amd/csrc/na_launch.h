@@ -122,6 +122,11 @@ void lean_bwd(const Prob &P, int dtype, const void *q, const void *k,
 // lsplit_inv: z_key = scale * sum over queries q holding the key (all query
 // heads of its group) of a[q, slot(q, key)] * x_q.
 bool lsplit_eligible(const Prob &P, int dtype);
+// Vector-ALU gather alternative to lsplit_qk (na_vsplit.hip; rank 2,
+// non-causal, same odd K <= 7 on both axes): false where it does not apply.
+bool vsplit_on();
+bool vsplit_qk(const Prob &P, int dtype, const void *x, const void *y, void *out,
+               float scale, hipStream_t st);
 void lsplit_qk(const Prob &P, int dtype, const void *x, const void *y,
                void *out, float scale, float fill, hipStream_t st);
 void lsplit_av(const Prob &P, int dtype, const void *a, const void *y,

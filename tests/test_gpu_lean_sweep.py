@@ -332,3 +332,29 @@ def test_split_backward_pair_matches_separate_launches(case, monkeypatch):
     separate = run()
     for a, b in zip(paired, separate):
         assert torch.equal(a, b)
+
+
+VQK_CASES = [
+    # (B, spatial, H, D, K, dilation, dtype)
+    (4, (56, 56), 4, 32, 7, (1, 1), torch.bfloat16),
+    (4, (56, 56), 4, 32, 7, (4, 4), torch.bfloat16),
+    (2, (19, 23), 2, 64, 5, (3, 2), torch.float16),
+    (1, (9, 12), 8, 32, 3, (1, 3), torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", VQK_CASES, ids=[f"v{i}" for i in range(len(VQK_CASES))])
+def test_valu_split_qk_against_oracle(case, monkeypatch):
+    """The vector-ALU gather kernel for the split QK (k_vqk, opt-in with
+    NATTEN_AMD_VSPLIT=1; the matrix-core k_lqh is the default) against the
+    oracle, with partial tiles, both dilated axes and head_dim 64."""
+    import natten_amd
+
+    B, sp, H, D, K, dil, dtype = case
+    _say(f"[case] valu split qk {case}")
+    monkeypatch.setenv("NATTEN_AMD_VSPLIT", "1")
+    q = randn((B, *sp, H, D), dtype, 81)
+    k = randn((B, *sp, H, D), dtype, 82)
+    ref = O.na_qk(q, k, (K, K), 1, dil, (False, False), 0.3)
+    got = natten_amd.na2d_qk(q.to(DEV), k.to(DEV), K, dil, scale=0.3)
+    assert_close(got, ref, dtype, "valu qk logits")
