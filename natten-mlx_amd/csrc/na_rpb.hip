@@ -1465,12 +1465,18 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias);
 // d in {1..8}: K=7 d=1 qk / av 5.27 / 5.81 us at 512 rows, 5.01 / 5.29-5.35
 // at 256; K=7 d=2 5.93 / 6.20 at 512, 5.74 / 5.79 at 384.
 // NATTEN_AMD_RPB_BLOCK overrides it (tuning).
-int rpb_block(const RpbProb &A) {
+// NATTEN_AMD_RPB_BLOCK (64 to 512) forces the rows per block (tuning).
+int block_forced() {
   static const int forced = [] {
     const char *e = std::getenv("NATTEN_AMD_RPB_BLOCK");
     const int v = e != nullptr ? std::atoi(e) : 0;
     return v == 64 || v == 128 || v == 256 || v == 384 || v == 512 ? v : 0;
   }();
+  return forced;
+}
+
+int rpb_block(const RpbProb &A) {
+  const int forced = block_forced();
   if (forced > 0) return forced;
   if (A.rank != 1 || A.K0 * A.d0 < 7) return 256;
   const int rb = A.d0 == 1 ? 256 : 384;
@@ -1659,13 +1665,26 @@ size_t r1_bias_gather_lds(const RpbProb &A) {
 // to 80 KB (two blocks per CU): the candidate queries' rows of dilated
 // windows (K = 7 at d = 4 takes 73 KB for 384 keys).
 constexpr size_t kR1InvLds = 80 * 1024;
-size_t r1_inverse_lds(const RpbProb &A) {
-  const int rb = rpb_block(A);
+size_t r1_inverse_lds(const RpbProb &A, int rb) {
   if (r1_lds(A, rb, false) == 0) return 0;
   const int step = A.heads_first ? 1 : A.H;
   const size_t cap = (size_t)rb + 2 * (size_t)r1_halo(A.K0, A.d0, step);
   const size_t lds = cap * (A.D / 4) * 16 + (cap * A.K0 + 4) * sizeof(float);
   return lds <= kR1InvLds ? lds : 0;
+}
+size_t r1_inverse_lds(const RpbProb &A) { return r1_inverse_lds(A, rpb_block(A)); }
+
+// Rows per block of the AV backward's staged pair (k_r1_avb): 512 where
+// K d >= 5 and its LDS fits, else the forward's (config 5 av backward,
+// 256 -> 512 rows: K=7 d=1 8.1 -> 7.0 us, K=5 d=1 6.4 -> 6.3, K=5 d=2 9.0 ->
+// 8.1, K=3 d=2 6.6 -> 6.1; K=3 d=1 5.6 -> 5.9 keeps 256).  The QK pair
+// gains nothing from 512 rows (K=3 / 5 d=1 slower), so it keeps
+// rpb_block's.
+int avb_block(const RpbProb &A) {
+  const int rb = rpb_block(A);
+  if (block_forced() || A.K0 * A.d0 < 5 || rb >= 512) return rb;
+  const size_t li = r1_inverse_lds(A, 512);
+  return r1_lds(A, 512, false) != 0 && li != 0 && li <= 65536 ? 512 : rb;
 }
 
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
@@ -1903,9 +1922,9 @@ bool r1_av_bwd_fused(const RpbProb &A, const float *attn, const float *v, const 
       ph_inverse_lds(A, nullptr) != 0)
     return false;
   if (pair_launch_off()) return false;
-  const int rb = rpb_block(A);
+  const int rb = avb_block(A);
   const size_t ld = r1_lds(A, rb, false);
-  const size_t li = r1_inverse_lds(A);
+  const size_t li = r1_inverse_lds(A, rb);
   if (ld == 0 || li == 0) return false;
   const int n0 = (A.n_rows + rb - 1) / rb;
   const dim3 grid((unsigned)(2 * n0)), block(rb);
