@@ -626,6 +626,20 @@ __device__ __forceinline__ void r1_gather_body(int bid, int nblk, const RpbProb 
       acc[c].w = fmaf(wk, t.w, acc[c].w);
     }
   }
+  // the block's output rows are one contiguous range: write them through
+  // LDS (over the window, once every thread has read its rows) as
+  // consecutive 16-byte units rather than one strided row per lane; the
+  // bias partials run after, with the accumulators already stored
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float4 o = acc[c];
+    o.x *= post;
+    o.y *= post;
+    o.z *= post;
+    o.w *= post;
+    win[tid * NC + c] = o;
+  }
   if (bpart != nullptr) {
     // thread (h, c) of the H (2K - 1) bias cells adds, in row order and in
     // float64, the block's weights w[r, k] of head h with pb(r) + k = c
@@ -636,30 +650,40 @@ __device__ __forceinline__ void r1_gather_body(int bid, int nblk, const RpbProb 
       const int h = tid / R0, c = tid - h * R0;
       const int row0 = bid * nthr;
       const int h0 = row0 - (int)fdiv((uint32_t)row0, A.fH) * A.H;
+      // a block of one sequence whose first and last positions have
+      // unclamped windows (pb = K/2, which holds exactly on the interior
+      // interval) has pb = K/2 on every row: slot c - K/2 of each row, no
+      // per-row test (the same terms in the same order as the general loop)
+      const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)(row0 + b.rows - 1));
+      const int nh = K / 2;
+      const bool inner = pf.b == pl.b && pf.i0 >= nh * A.d0 && pl.i0 + nh * A.d0 < A.L0;
       double acc_b = 0.0;
-      for (int j = h >= h0 ? h - h0 : h - h0 + A.H; j < b.rows; j += A.H) {
-        const int k = c - spb[j];
-        if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
+      int j = h >= h0 ? h - h0 : h - h0 + A.H;
+      if (inner) {
+        const int k = c - nh;
+        if ((unsigned)k < (unsigned)K) {
+          for (; j + 3 * A.H < b.rows; j += 4 * A.H) {
+            const float t0 = sw[j * K + k], t1 = sw[(j + A.H) * K + k];
+            const float t2 = sw[(j + 2 * A.H) * K + k], t3 = sw[(j + 3 * A.H) * K + k];
+            acc_b += (double)t0;
+            acc_b += (double)t1;
+            acc_b += (double)t2;
+            acc_b += (double)t3;
+          }
+          for (; j < b.rows; j += A.H) acc_b += (double)sw[j * K + k];
+        }
+      } else {
+        for (; j < b.rows; j += A.H) {
+          const int k = c - spb[j];
+          if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
+        }
       }
       bpart[(int64_t)tid * nblk + bid] = acc_b;
     }
   }
-  // the block's output rows are one contiguous range: write them through
-  // LDS (over the weights and window, once every thread has read them) as
-  // consecutive 16-byte units rather than one strided row per lane
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    float4 o = acc[c];
-    o.x *= post;
-    o.y *= post;
-    o.z *= post;
-    o.w *= post;
-    sm4[tid * NC + c] = o;
-  }
   __syncthreads();
   block_copy16<true>(reinterpret_cast<uint4 *>(out) + (int64_t)bid * nthr * NC,
-               reinterpret_cast<const uint4 *>(sm4), (int64_t)b.rows * NC);
+               reinterpret_cast<const uint4 *>(win), (int64_t)b.rows * NC);
 }
 
 template <int K, int NC>
@@ -883,21 +907,8 @@ __device__ __forceinline__ void r1p_gather_body(int bid, int nblk, const RpbProb
       acc[c].w = fmaf(wk, t.w, acc[c].w);
     }
   }
-  if (bpart != nullptr) {
-    // thread (h, c) of the H (2K - 1) bias cells adds, in row order and in
-    // float64, the block's weights w[r, k] of head h with pb(r) + k = c
-    constexpr int R0 = 2 * K - 1;
-    if (tid < A.H * R0) {
-      const int h = tid / R0, c = tid - h * R0;
-      const int h0 = R.row0 - (int)fdiv((uint32_t)R.row0, A.fH) * A.H;
-      double acc_b = 0.0;
-      for (int j = h >= h0 ? h - h0 : h - h0 + A.H; j < R.rows; j += A.H) {
-        const int k = c - spb[j];
-        if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
-      }
-      bpart[(int64_t)tid * nblk + bid] = acc_b;
-    }
-  }
+  // the output rows over the window (once every thread has read its
+  // rows), then the bias partials with the accumulators already stored
   __syncthreads();
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -906,11 +917,49 @@ __device__ __forceinline__ void r1p_gather_body(int bid, int nblk, const RpbProb
     o.y *= post;
     o.z *= post;
     o.w *= post;
-    sm4[tid * NC + c] = o;
+    win[tid * NC + c] = o;
+  }
+  if (bpart != nullptr) {
+    // thread (h, c) of the H (2K - 1) bias cells adds, in row order and in
+    // float64, the block's weights w[r, k] of head h with pb(r) + k = c
+    constexpr int R0 = 2 * K - 1;
+    if (tid < A.H * R0) {
+      const int h = tid / R0, c = tid - h * R0;
+      const int h0 = R.row0 - (int)fdiv((uint32_t)R.row0, A.fH) * A.H;
+      // a block inside one phase of one sample whose first and last indices
+      // have unclamped windows (K/2 <= m <= plen - 1 - K/2, where pb = K/2)
+      // has pb = K/2 on every row, as in the staged gather
+      const int nh = K / 2;
+      const PhPos f = ph_pos(A, M, (int)fdiv((uint32_t)R.row0, A.fH));
+      const PhPos l = ph_pos(A, M, (int)fdiv((uint32_t)(R.row0 + R.rows - 1), A.fH));
+      const bool inner = f.b == l.b && f.r == l.r && f.m >= nh && l.m + nh < l.plen;
+      double acc_b = 0.0;
+      int j = h >= h0 ? h - h0 : h - h0 + A.H;
+      if (inner) {
+        const int k = c - nh;
+        if ((unsigned)k < (unsigned)K) {
+          for (; j + 3 * A.H < R.rows; j += 4 * A.H) {
+            const float t0 = sw[j * K + k], t1 = sw[(j + A.H) * K + k];
+            const float t2 = sw[(j + 2 * A.H) * K + k], t3 = sw[(j + 3 * A.H) * K + k];
+            acc_b += (double)t0;
+            acc_b += (double)t1;
+            acc_b += (double)t2;
+            acc_b += (double)t3;
+          }
+          for (; j < R.rows; j += A.H) acc_b += (double)sw[j * K + k];
+        }
+      } else {
+        for (; j < R.rows; j += A.H) {
+          const int k = c - spb[j];
+          if ((unsigned)k < (unsigned)K) acc_b += (double)sw[j * K + k];
+        }
+      }
+      bpart[(int64_t)tid * nblk + bid] = acc_b;
+    }
   }
   __syncthreads();
   ph_copy<false>(A, M, U.ry, U.fry, nullptr, reinterpret_cast<uint4 *>(out),
-                 reinterpret_cast<uint4 *>(sm4), R.row0 * NC, R.rows * NC);
+                 reinterpret_cast<uint4 *>(win), R.row0 * NC, R.rows * NC);
 }
 
 template <int K, int NC>
