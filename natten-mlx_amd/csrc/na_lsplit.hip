@@ -693,7 +693,13 @@ __device__ __forceinline__ void linv_body(int bid, const LProb &Pin, const T *__
   typedef typename M::v4 v4;
   typedef typename M::e E;
   constexpr int NDB = D / 16;
-  constexpr int NP = 4;  // chunk pairs whose gathers are issued together
+  // chunk pairs whose gathers are issued together: one.  Each gathered
+  // element carries its own address, so more pairs in flight cost
+  // registers: at four the backward pairs (k_lqkb / k_lavb) took 108 VGPRs,
+  // four waves per SIMD and 1.5 rounds of workgroups at config 2 (qk / av
+  // backward 12.05 / 11.79 us), at two 76 (10.97 / 10.70 us), at one 60 /
+  // 71 (10.74 / 10.13 us).
+  constexpr int NP = 1;
   constexpr int RS = lds_y(D);
   extern __shared__ __align__(16) char smem[];
 
