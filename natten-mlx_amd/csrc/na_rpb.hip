@@ -1703,13 +1703,13 @@ R1Kind r1_kind(const RpbProb &A, bool bias) {
 // The staged gather that also forms the bias gradient's partials:
 // spatial-first rows, one thread per bias cell, each row's first bias cell
 // in LDS.
-size_t r1_bias_gather_lds(const RpbProb &A) {
-  const int rb = rpb_block(A);
+size_t r1_bias_gather_lds(const RpbProb &A, int rb) {
   const size_t lds = r1_lds(A, rb, false);
   if (lds == 0 || A.heads_first || A.H * A.R0 > rb) return 0;
   const size_t b = lds + (size_t)rb * sizeof(int);
   return b <= 65536 ? b : 0;
 }
+size_t r1_bias_gather_lds(const RpbProb &A) { return r1_bias_gather_lds(A, rpb_block(A)); }
 // LDS of the staged inverse (dk / dv), or 0 where it does not apply.  Up
 // to 80 KB (two blocks per CU): the candidate queries' rows of dilated
 // windows (K = 7 at d = 4 takes 73 KB for 384 keys).
@@ -1734,6 +1734,17 @@ int avb_block(const RpbProb &A) {
   if (block_forced() || A.K0 * A.d0 < 5 || rb >= 512) return rb;
   const size_t li = r1_inverse_lds(A, 512);
   return r1_lds(A, 512, false) != 0 && li != 0 && li <= 65536 ? 512 : rb;
+}
+
+// Rows per block of the QK backward's staged pair (k_r1_qkb): 512 where
+// (K - 1) d >= 6 and its LDS fits, else the forward's (config 5 qk
+// backward, 256 -> 512 rows: K=7 d=1 15.1 -> 13.1 us; K=3 d=1 10.1 -> 11.8,
+// K=5 d=1 11.5 -> 12.8 and K=3 d=2 11.1 -> 11.6 keep 256).
+int qkb_block(const RpbProb &A) {
+  const int rb = rpb_block(A);
+  if (block_forced() || (A.K0 - 1) * A.d0 < 6 || rb >= 512) return rb;
+  const size_t li = r1_inverse_lds(A, 512);
+  return r1_bias_gather_lds(A, 512) != 0 && li != 0 && li <= 65536 ? 512 : rb;
 }
 
 bool r1_dot(const RpbProb &A, const float *x, const float *y, const float *rpb,
@@ -1932,13 +1943,13 @@ bool r1_qk_bwd_fused(const RpbProb &A, const float *dl, const float *q, const fl
   if ((phase_inverse_first(A, true) || phase_pair_first(A, true)) &&
       ph_inverse_lds(A, nullptr) != 0)
     return false;
-  const size_t lg = bpart != nullptr ? r1_bias_gather_lds(A) : r1_lds(A, rpb_block(A), false);
-  const size_t li = r1_inverse_lds(A);
+  const int rb = qkb_block(A);
+  const size_t lg = bpart != nullptr ? r1_bias_gather_lds(A, rb) : r1_lds(A, rb, false);
+  const size_t li = r1_inverse_lds(A, rb);
   // the pair shares one LDS size: an inverse above 64 KB would hold the
   // gather's blocks to two per CU too (K = 7, d = 4: 26.4 us as two
   // launches, 29.9 us as one)
   if (lg == 0 || li == 0 || li > 65536) return false;
-  const int rb = rpb_block(A);
   const int n0 = (A.n_rows + rb - 1) / rb;
   const dim3 grid((unsigned)(2 * n0)), block(rb);
   const size_t lds = std::max(lg, li);
@@ -2206,7 +2217,7 @@ void rpb_qk_bwd(const RpbProb &A, int dtype, const void *q, const void *key,
   int32_t n_fused = 0;
   bool pair = false;  // dq and dk in one launch
   if (dq != nullptr && dk != nullptr && dtype == NA_F32 && A.n_rows > 0) {
-    const int32_t nblk = (A.n_rows + rpb_block(A) - 1) / rpb_block(A);
+    const int32_t nblk = (A.n_rows + qkb_block(A) - 1) / qkb_block(A);
     const bool bias = drpb != nullptr && nblk <= n_chunks;
     if ((drpb == nullptr || bias) &&
         r1_qk_bwd_fused(A, dlogits, (const float *)q, (const float *)key, (float *)dq,
