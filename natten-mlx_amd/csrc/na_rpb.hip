@@ -461,9 +461,17 @@ __device__ __forceinline__ R1Rows r1_rows(const RpbProb &A, int step, int bid) {
     o.lo = row0 - hf + (wf.s - pf.i0) * step;
     o.hi = rl - hl + (wl.s + K - 1 - pl.i0) * step + step;
   } else {
+    // a block of one sequence whose first and last positions have centred
+    // windows (K/2 d <= i < L - K/2 d, the interval where no window is
+    // pinned) covers [first - K/2 d, last + K/2 d]; other blocks take
+    // their rows widened by (K - 1) d positions per side
+    const int rl = row0 + o.rows - 1;
+    const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)rl);
+    const int nhd = (K / 2) * A.d0;
+    const bool inner = !A.heads_first && pf.b == pl.b && pf.i0 >= nhd && pl.i0 + nhd < A.L0;
     const int reach = (K - 1) * A.d0 * step;
-    o.lo = max(0, row0 - reach);
-    o.hi = min(A.n_rows, row0 + o.rows + reach);
+    o.lo = inner ? row0 - pf.h - nhd * step : max(0, row0 - reach);
+    o.hi = inner ? rl - pl.h + (nhd + 1) * step : min(A.n_rows, row0 + o.rows + reach);
   }
   return o;
 }
