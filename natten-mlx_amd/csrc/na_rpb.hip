@@ -1114,7 +1114,22 @@ __device__ __forceinline__ void r1_inverse_body(int bid, const RpbProb &A,
   const int row0 = bid * nthr;
   const int rows = min(nthr, A.n_rows - row0);
   const int r = row0 + min(tid, rows - 1);
-  const int reach = (K - 1) * A.d0 * step;
+  // every key of the block at a position j in [K d, L - 1 - K d] of one
+  // sequence (block-uniform): j's phase index m and the phase indices m + t,
+  // |t| <= K/2, of the queries j + t d lie at least K from both ends of the
+  // phase, so those queries' windows are unclamped ([m + t - K/2, m + t +
+  // K/2], holding j at slot K/2 - t) and every other query's window (of the
+  // same phase: unclamped and more than K/2 away, or clamped to the first
+  // or last K indices) misses j; the K candidates need no window test, and
+  // the block stages only the rows K/2 d positions either side of its own
+  bool interior;
+  {
+    const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)(row0 + rows - 1));
+    const int kd = K * A.d0;
+    interior = pf.b == pl.b && pf.h == (A.heads_first ? pl.h : pf.h) && pf.i0 >= kd &&
+               pl.i0 <= A.L0 - 1 - kd;
+  }
+  const int reach = (interior ? K / 2 : K - 1) * A.d0 * step;
   const int lo = max(0, row0 - reach), hi = min(A.n_rows, row0 + rows + reach);
   const int cap = nthr + 2 * r1_halo(K, A.d0, step);  // staged rows, at most
   float4 *xs = sm4;
@@ -1164,20 +1179,6 @@ __device__ __forceinline__ void r1_inverse_body(int bid, const RpbProb &A,
       acc[c].w = fmaf(wk, v.w, acc[c].w);
     }
   };
-  // every key of the block at a position j in [K d, L - 1 - K d] of one
-  // sequence (block-uniform): j's phase index m and the phase indices m + t,
-  // |t| <= K/2, of the queries j + t d lie at least K from both ends of the
-  // phase, so those queries' windows are unclamped ([m + t - K/2, m + t +
-  // K/2], holding j at slot K/2 - t) and every other query's window (of the
-  // same phase: unclamped and more than K/2 away, or clamped to the first
-  // or last K indices) misses j; the K candidates need no window test
-  bool interior;
-  {
-    const RPos pf = rpos(A, (uint32_t)row0), pl = rpos(A, (uint32_t)(row0 + rows - 1));
-    const int kd = K * A.d0;
-    interior = pf.b == pl.b && pf.h == (A.heads_first ? pl.h : pf.h) && pf.i0 >= kd &&
-               pl.i0 <= A.L0 - 1 - kd;
-  }
   if (interior) {
 #pragma unroll
     for (int t = -(K / 2); t <= K / 2; ++t) {
