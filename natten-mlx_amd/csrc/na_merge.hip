@@ -51,15 +51,27 @@ __device__ __forceinline__ float merge_weights(const MergeIn &S, int n,
   return L;
 }
 
-// One thread per VEC consecutive elements of a row (VEC divides D).
-template <typename T, int VEC>
+// One thread per VEC consecutive elements of a row (VEC divides D).  P2:
+// D / VEC is 2^lg and the whole tensor has fewer than 2^31 such units, so
+// the row index is a 32-bit shift (a 64-bit division by a runtime value is
+// a long instruction sequence here, most of the kernel's work).
+template <typename T, int VEC, bool P2>
 __global__ void __launch_bounds__(256)
-    k_merge_fwd(MergeIn S, int n, int64_t rows, int D, T *__restrict__ out,
+    k_merge_fwd(MergeIn S, int n, int64_t rows, int D, int lg, T *__restrict__ out,
                 float *__restrict__ lse) {
-  const int64_t per_row = D / VEC;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * per_row) return;
-  const int64_t r = idx / per_row;
+  int64_t idx, r, per_row;
+  if constexpr (P2) {
+    const uint32_t i32 = blockIdx.x * blockDim.x + threadIdx.x;
+    if ((int64_t)i32 >= (rows << lg)) return;
+    idx = i32;
+    r = i32 >> lg;
+    per_row = (int64_t)1 << lg;
+  } else {
+    per_row = D / VEC;
+    idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    r = idx / per_row;
+  }
   const int64_t e0 = idx * VEC;  // == r * D + (idx - r * per_row) * VEC
   float w[kMergeMaxParts];
   const float L = merge_weights(S, n, r, w);
@@ -122,13 +134,21 @@ void merge_fwd_t(const MergeIn &S, int n, int64_t rows, int D, void *out,
                  float *lse, hipStream_t st) {
   constexpr int V = 16 / (int)sizeof(T);
   if (D % V == 0) {
-    const int64_t threads = rows * (D / V);
-    hipLaunchKernelGGL((k_merge_fwd<T, V>), dim3((unsigned)((threads + 255) / 256)),
-                       dim3(256), 0, st, S, n, rows, D, (T *)out, lse);
+    const int pr = D / V;
+    const int64_t threads = rows * pr;
+    int lg = 0;
+    while ((1 << lg) < pr) ++lg;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if ((1 << lg) == pr && threads + 255 < ((int64_t)1 << 31))
+      hipLaunchKernelGGL((k_merge_fwd<T, V, true>), grid, dim3(256), 0, st, S, n, rows, D,
+                         lg, (T *)out, lse);
+    else
+      hipLaunchKernelGGL((k_merge_fwd<T, V, false>), grid, dim3(256), 0, st, S, n, rows, D,
+                         0, (T *)out, lse);
   } else {
     const int64_t threads = rows * D;
-    hipLaunchKernelGGL((k_merge_fwd<T, 1>), dim3((unsigned)((threads + 255) / 256)),
-                       dim3(256), 0, st, S, n, rows, D, (T *)out, lse);
+    hipLaunchKernelGGL((k_merge_fwd<T, 1, false>), dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, st, S, n, rows, D, 0, (T *)out, lse);
   }
 }
 
