@@ -1602,19 +1602,19 @@ bool phase_inverse_first(const RpbProb &A, bool qk) {
 }
 
 // Whether the backward's phase-major pair (k_r1p_qkb / k_r1p_avb) goes
-// before the staged kernels where both apply: the QK backward's where
-// (K - 1) d >= 8, the AV backward's where K >= 5 and (K - 1) d >= 12
-// (config 5 qk / av backward, staged -> phase-major pair: K=5 d=2 qk 16.1
-// -> 14.6 us, K=3 d=8 qk 15.0 -> 13.6, K=7 d=4 22.0 -> 17.9 and av 13.25 ->
-// 10.25, K=7 d=2 av 11.2 -> 10.2; K=3 d=2 qk 11.4 -> 13.2 and K=3 av
-// 7.0-8.0 -> 8.6-8.9 stay staged).  NATTEN_AMD_RPB_PHPAIR=1 / 0 forces /
-// forbids it (A/B checks; read per call).
+// before the staged kernels where both apply: where K >= 5 and
+// (K - 1) d >= 12, for both backward calls (config 5, phase-major pair
+// against the staged one: qk K=5 d=4 13.7 vs 15.1 us, K=7 d=2 15.7 vs 16.8,
+// av K=7 d=4 10.0 vs 11.7; the staged pair is faster at K=3 d=4 / 8 (12.6 /
+// 13.2 vs 13.0 / 13.6 us) and K=5 d=2 (13.0 vs 13.7)).
+// NATTEN_AMD_RPB_PHPAIR=1 / 0 forces / forbids it (A/B checks; read per
+// call).
 bool phase_pair_first(const RpbProb &A, bool qk) {
   if (A.d0 < 2) return false;
   const char *e = std::getenv("NATTEN_AMD_RPB_PHPAIR");
   if (e != nullptr && (e[0] == '1' || e[0] == '0')) return e[0] == '1';
-  const int span = (A.K0 - 1) * A.d0;
-  return qk ? span >= 8 : A.K0 >= 5 && span >= 12;
+  (void)qk;
+  return A.K0 >= 5 && (A.K0 - 1) * A.d0 >= 12;
 }
 
 bool r1_offsets_fit(const RpbProb &A) {

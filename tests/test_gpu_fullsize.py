@@ -191,7 +191,7 @@ def test_config5_full(K, d):
     pl = _lib.NaRpbPlan()
     assert _lib.load().na_rpb_kernel_plan(ctypes.byref(pp), ctypes.byref(pl)) == 0
     want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
-    qk_pair = d > 1 and (K - 1) * d >= 8
+    qk_pair = d > 1 and K >= 5 and (K - 1) * d >= 12
     assert (pl.qk, pl.av) == (want,) * 2 and pl.fused_bias == 1
     if "NATTEN_AMD_RPB_PHPAIR" not in os.environ:  # the default rule
         assert pl.dq == (_lib.RPB_PHASE if qk_pair else want)

@@ -186,10 +186,9 @@ def test_config5_allin1_kernels():
             want = _lib.RPB_PHASE if (K >= 5 and d == 8) else _lib.RPB_STAGED
             assert pl["qk"] == want and pl["av"] == want, (K, d, pl)
             assert pl["fused_bias"], (K, d, pl)  # staged or phase-major dq pass
-            # the backward's phase-major pairs: dq with dk where
-            # (K - 1) d >= 8, dattn with dv where K >= 5 and (K - 1) d >= 12
-            qk_pair = d > 1 and (K - 1) * d >= 8
-            av_pair = d > 1 and K >= 5 and (K - 1) * d >= 12
+            # the backward's phase-major pairs (dq with dk, dattn with dv)
+            # where K >= 5 and (K - 1) d >= 12
+            qk_pair = av_pair = d > 1 and K >= 5 and (K - 1) * d >= 12
             assert pl["dq"] == (_lib.RPB_PHASE if qk_pair else want), (K, d, pl)
             assert pl["dk"] == (_lib.RPB_PHASE if qk_pair else _lib.RPB_STAGED), (K, d, pl)
             assert pl["dattn"] == (_lib.RPB_PHASE if av_pair else want), (K, d, pl)
