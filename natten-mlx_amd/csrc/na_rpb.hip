@@ -417,6 +417,15 @@ __global__ void __launch_bounds__(512)
 }
 
 // ---- rank 1, fp32, head_dim 4 NC <= 16, window side K fixed ----------------
+// Row block of dispatch index bid in a launch of nb blocks.  Workgroups are
+// dealt to the 8 XCDs in turn (bid mod 8), each XCD with its own L2: here
+// XCD x runs one contiguous run of row blocks, so the halo rows that a
+// block stages with its neighbours are mostly fetched once per run.
+__device__ __forceinline__ int xcd_block(int bid, int nb) {
+  const int x = bid & 7, s = bid >> 3, per = nb >> 3, rem = nb & 7;
+  return x * per + min(x, rem) + s;
+}
+
 // The DiNAT 1-D shapes (fp32 rows of a few 16-byte units, K in 3..13) with
 // the neighbor window staged: one thread per row, the slot loop unrolled
 // over K with each slot row read from LDS at a constant stride from the
@@ -568,7 +577,7 @@ __global__ void __launch_bounds__(512)
     k_r1_dot(RpbProb A, const float *__restrict__ x, const float *__restrict__ y,
              const float *__restrict__ rpb, float *__restrict__ out,
              int scale_x) {
-  r1_dot_body<K, NC>((int)blockIdx.x, A, x, y, rpb, out, scale_x);
+  r1_dot_body<K, NC>(xcd_block((int)blockIdx.x, (int)gridDim.x), A, x, y, rpb, out, scale_x);
 }
 
 // AV / dq: out[r] = post * sum_k w[r, k] * y[nbr(r, k)] over valid slots.
@@ -699,7 +708,8 @@ __global__ void __launch_bounds__(512)
     k_r1_gather(RpbProb A, const float *__restrict__ wgt,
                 const float *__restrict__ y, float *__restrict__ out,
                 float post, double *__restrict__ bpart) {
-  r1_gather_body<K, NC>((int)blockIdx.x, (int)gridDim.x, A, wgt, y, out, post, bpart);
+  r1_gather_body<K, NC>(xcd_block((int)blockIdx.x, (int)gridDim.x), (int)gridDim.x, A, wgt, y,
+                        out, post, bpart);
 }
 
 // ---- rank 1, spatial-first, dilation d > 1: rows in phase-major order ----
@@ -869,7 +879,8 @@ __global__ void __launch_bounds__(512)
     k_r1p_dot(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ x,
               const float *__restrict__ y, const float *__restrict__ rpb,
               float *__restrict__ out, int scale_x) {
-  r1p_dot_body<K, NC>((int)blockIdx.x, A, M, U, x, y, rpb, out, scale_x);
+  r1p_dot_body<K, NC>(xcd_block((int)blockIdx.x, (int)gridDim.x), A, M, U, x, y, rpb, out,
+                      scale_x);
 }
 
 // bpart (the QK backward's dq pass): also the bias gradient's float64
@@ -975,7 +986,8 @@ __global__ void __launch_bounds__(512)
     k_r1p_gather(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ wgt,
                  const float *__restrict__ y, float *__restrict__ out, float post,
                  double *__restrict__ bpart) {
-  r1p_gather_body<K, NC>((int)blockIdx.x, (int)gridDim.x, A, M, U, wgt, y, out, post, bpart);
+  r1p_gather_body<K, NC>(xcd_block((int)blockIdx.x, (int)gridDim.x), (int)gridDim.x, A, M, U,
+                         wgt, y, out, post, bpart);
 }
 
 // dk / dv on the phase-major rows (d > 1): one thread per key row in the
@@ -1064,13 +1076,15 @@ __global__ void __launch_bounds__(512)
     k_r1p_inverse(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ w,
                   const float *__restrict__ x, float *__restrict__ out, float post,
                   int cap) {
-  r1p_inverse_body<K, NC>((int)blockIdx.x, A, M, U, w, x, out, post, cap);
+  r1p_inverse_body<K, NC>(xcd_block((int)blockIdx.x, (int)gridDim.x), A, M, U, w, x, out, post,
+                          cap);
 }
 
 // A backward's two passes on the phase-major rows in one launch: blocks
 // [0, n0) the first pass (QK: dq by the gather over dlogits, with the bias
 // partials when bpart is set; AV: dattn by the dot of dout with the
-// values), the others the inverse (dk or dv).
+// values), the others the inverse (dk or dv); each pass's row blocks in
+// contiguous runs per XCD as in k_r1_qkb.
 template <int K, int NC>
 __global__ void __launch_bounds__(512)
     k_r1p_qkb(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ dl,
@@ -1079,9 +1093,9 @@ __global__ void __launch_bounds__(512)
               double *__restrict__ bpart, int n0, int cap) {
   const int bid = (int)blockIdx.x;
   if (bid < n0)
-    r1p_gather_body<K, NC>(bid, n0, A, M, U, dl, key, dq, post, bpart);
+    r1p_gather_body<K, NC>(xcd_block(bid, n0), n0, A, M, U, dl, key, dq, post, bpart);
   else
-    r1p_inverse_body<K, NC>(bid - n0, A, M, U, dl, q, dk, post, cap);
+    r1p_inverse_body<K, NC>(xcd_block(bid - n0, n0), A, M, U, dl, q, dk, post, cap);
 }
 
 template <int K, int NC>
@@ -1091,9 +1105,9 @@ __global__ void __launch_bounds__(512)
               float *__restrict__ dattn, float *__restrict__ dv, int n0, int cap) {
   const int bid = (int)blockIdx.x;
   if (bid < n0)
-    r1p_dot_body<K, NC>(bid, A, M, U, dout, v, nullptr, dattn, 0);
+    r1p_dot_body<K, NC>(xcd_block(bid, n0), A, M, U, dout, v, nullptr, dattn, 0);
   else
-    r1p_inverse_body<K, NC>(bid - n0, A, M, U, attn, dout, dv, 1.f, cap);
+    r1p_inverse_body<K, NC>(xcd_block(bid - n0, n0), A, M, U, attn, dout, dv, 1.f, cap);
 }
 
 // dk / dv: out[j] = post * sum over the queries i whose window holds key j
@@ -1227,14 +1241,17 @@ template <int K, int NC, bool D1>
 __global__ void __launch_bounds__(512)
     k_r1_inverse(RpbProb A, const float *__restrict__ w,
                  const float *__restrict__ x, float *__restrict__ out, float post) {
-  r1_inverse_body<K, NC, D1>((int)blockIdx.x, A, w, x, out, post);
+  r1_inverse_body<K, NC, D1>(xcd_block((int)blockIdx.x, (int)gridDim.x), A, w, x, out, post);
 }
 
 // The two passes of a backward in one launch (they are independent): blocks
 // [0, n0) run the first pass, the others the inverse (dk or dv).  QK
 // backward: dq by the gather over dlogits (with the bias partials when bpart
 // is set) and dk; AV backward: dattn by the dot of dout with the values and
-// dv.
+// dv.  Each pass deals its row blocks to the XCDs in contiguous runs
+// (xcd_block), the two passes' dispatch ranges kept apart: interleaving the
+// passes block by block in one run per XCD was slower (config 5 K=7 d=1
+// QK backward 13.0 -> 13.8 us; the passes apart 12.7 us).
 template <int K, int NC, bool D1>
 __global__ void __launch_bounds__(512)
     k_r1_qkb(RpbProb A, const float *__restrict__ dl, const float *__restrict__ q,
@@ -1242,9 +1259,9 @@ __global__ void __launch_bounds__(512)
              float *__restrict__ dk, float post, double *__restrict__ bpart, int n0) {
   const int bid = (int)blockIdx.x;
   if (bid < n0)
-    r1_gather_body<K, NC>(bid, n0, A, dl, key, dq, post, bpart);
+    r1_gather_body<K, NC>(xcd_block(bid, n0), n0, A, dl, key, dq, post, bpart);
   else
-    r1_inverse_body<K, NC, D1>(bid - n0, A, dl, q, dk, post);
+    r1_inverse_body<K, NC, D1>(xcd_block(bid - n0, n0), A, dl, q, dk, post);
 }
 
 template <int K, int NC, bool D1>
@@ -1254,9 +1271,9 @@ __global__ void __launch_bounds__(512)
              float *__restrict__ dv, int n0) {
   const int bid = (int)blockIdx.x;
   if (bid < n0)
-    r1_dot_body<K, NC>(bid, A, dout, v, nullptr, dattn, 0);
+    r1_dot_body<K, NC>(xcd_block(bid, n0), A, dout, v, nullptr, dattn, 0);
   else
-    r1_inverse_body<K, NC, D1>(bid - n0, A, attn, dout, dv, 1.f);
+    r1_inverse_body<K, NC, D1>(xcd_block(bid - n0, n0), A, attn, dout, dv, 1.f);
 }
 
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
