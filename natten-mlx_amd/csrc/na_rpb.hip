@@ -1533,12 +1533,15 @@ size_t r1_lds(const RpbProb &A, int rb, bool bias);
 
 // Threads per block of the forward gathers (k_rpb_dot / k_rpb_gather and
 // the staged rank-1 kernels).  Rank 1 with a window reach K0 * d0 of at
-// least 7: 256 rows for d0 = 1 (a block stages exactly its windows' rows),
-// 384 for larger dilations, where the staged kernels take that block
-// (with a bias table), else 512 (the halo weighs on smaller blocks);
-// everything else 256.  Measured at D = 12, K in {3, 5, 7},
-// d in {1..8}: K=7 d=1 qk / av 5.27 / 5.81 us at 512 rows, 5.01 / 5.29-5.35
-// at 256; K=7 d=2 5.93 / 6.20 at 512, 5.74 / 5.79 at 384.
+// least 7: 256 rows for d0 = 1 (a block stages exactly its windows' rows);
+// for larger dilations 256 where a window reaches (K0/2) d0 >= 6 positions
+// either side and the staged kernels take that block (with a bias table),
+// else 384 where they take it, else 512; everything else 256.  Measured at
+// D = 12, K in {3, 5, 7}, d in {1..8}, with each launch's row blocks in
+// contiguous runs per XCD: K=7 d=1 qk / av 4.99 / 5.25 us at 512 rows,
+// 4.64 / 4.69 at 256; K=7 d=2 5.31 / 5.36 at 384, 5.08 / 5.09 at 256; K=5
+// d=4 4.95 / 5.17 at 384, 4.84 / 4.91 at 256; K=3 d=4 4.30 / 4.79 at 384,
+// 4.43 / 4.69 at 256.
 // NATTEN_AMD_RPB_BLOCK overrides it (tuning).
 // NATTEN_AMD_RPB_BLOCK (64 to 512) forces the rows per block (tuning).
 int block_forced() {
@@ -1554,8 +1557,9 @@ int rpb_block(const RpbProb &A) {
   const int forced = block_forced();
   if (forced > 0) return forced;
   if (A.rank != 1 || A.K0 * A.d0 < 7) return 256;
-  const int rb = A.d0 == 1 ? 256 : 384;
-  return r1_lds(A, rb, true) != 0 ? rb : 512;
+  if (A.d0 == 1 || ((A.K0 / 2) * A.d0 >= 6 && r1_lds(A, 256, true) != 0))
+    return r1_lds(A, 256, true) != 0 ? 256 : 512;
+  return r1_lds(A, 384, true) != 0 ? 384 : 512;
 }
 
 template <typename A_, typename B_>
@@ -1750,25 +1754,26 @@ size_t r1_inverse_lds(const RpbProb &A, int rb) {
 size_t r1_inverse_lds(const RpbProb &A) { return r1_inverse_lds(A, rpb_block(A)); }
 
 // Rows per block of the AV backward's staged pair (k_r1_avb): 512 where
-// K d >= 5 and its LDS fits, else the forward's (config 5 av backward,
-// 256 -> 512 rows: K=7 d=1 8.1 -> 7.0 us, K=5 d=1 6.4 -> 6.3, K=5 d=2 9.0 ->
-// 8.1, K=3 d=2 6.6 -> 6.1; K=3 d=1 5.6 -> 5.9 keeps 256).  The QK pair
-// gains nothing from 512 rows (K=3 / 5 d=1 slower), so it keeps
-// rpb_block's.
+// 6 <= K d <= 16 and its LDS fits, else the forward's (config 5 av
+// backward, the forward's rows -> 512: K=7 d=1 7.70 -> 7.01 us, K=5 d=2
+// 8.44 -> 7.81, K=3 d=4 7.29 -> 6.91; K=5 d=1 6.25 -> 6.41 and K=3 d=8
+// 7.50 -> 8.04 keep 256; K=3 d=1 keeps 256).
 int avb_block(const RpbProb &A) {
   const int rb = rpb_block(A);
-  if (block_forced() || A.K0 * A.d0 < 5 || rb >= 512) return rb;
+  if (block_forced() || A.K0 * A.d0 < 6 || A.K0 * A.d0 > 16 || rb >= 512) return rb;
   const size_t li = r1_inverse_lds(A, 512);
   return r1_lds(A, 512, false) != 0 && li != 0 && li <= 65536 ? 512 : rb;
 }
 
 // Rows per block of the QK backward's staged pair (k_r1_qkb): 512 where
-// (K - 1) d >= 6 and its LDS fits, else the forward's (config 5 qk
-// backward, 256 -> 512 rows: K=7 d=1 15.1 -> 13.1 us; K=3 d=1 10.1 -> 11.8,
-// K=5 d=1 11.5 -> 12.8 and K=3 d=2 11.1 -> 11.6 keep 256).
+// K >= 5, (K - 1) d >= 6 and its LDS fits, else the forward's (config 5 qk
+// backward, 256 -> 512 rows: K=7 d=1 15.1 -> 13.1 us before the XCD runs,
+// 12.6 either way after; K=3 d=1 10.1 -> 11.8, K=5 d=1 11.5 -> 12.8 and
+// K=3 d=2 11.1 -> 11.6 keep 256; K=3 d=4 11.5 at 384 rows, 12.4 at 512,
+// and K=3 d=8 11.6 at 256, 12.4 at 512, keep the forward's).
 int qkb_block(const RpbProb &A) {
   const int rb = rpb_block(A);
-  if (block_forced() || (A.K0 - 1) * A.d0 < 6 || rb >= 512) return rb;
+  if (block_forced() || A.K0 < 5 || (A.K0 - 1) * A.d0 < 6 || rb >= 512) return rb;
   const size_t li = r1_inverse_lds(A, 512);
   return r1_bias_gather_lds(A, 512) != 0 && li != 0 && li <= 65536 ? 512 : rb;
 }
