@@ -783,6 +783,49 @@ __device__ __forceinline__ void ph_copy(const RpbProb &A, const PhMap &M, int ru
   }
 }
 
+// The first round of a LOAD ph_copy (four units per thread) split into its
+// loads and its LDS stores, so that a kernel staging two ranges issues both
+// ranges' first loads before it waits on either (one load round trip for
+// the common block instead of two); ph_copy stages any units past the first
+// round (units [4 nthr, n), copied by the caller).
+struct PhRound {
+  u32x4 r[4];
+  int ix[4];
+  __device__ __forceinline__ void load(const RpbProb &A, const PhMap &M, int ru, FastDiv fru,
+                                       const uint4 *gsrc, int g0, int n) {
+    const int nt = (int)blockDim.x, tid = (int)threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ix[j] = min(j * nt + tid, n - 1);
+      const int g = g0 + ix[j];
+      const int pos = (int)fdiv((uint32_t)g, fru);
+      const PhPos o = ph_pos(A, M, pos);
+      const int mu = (o.b * A.L0 + o.r + A.d0 * o.m) * ru + (g - pos * ru);
+      r[j] = reinterpret_cast<const u32x4 *>(gsrc)[mu];
+    }
+  }
+  __device__ __forceinline__ void store(uint4 *lds) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) reinterpret_cast<u32x4 *>(lds)[ix[j]] = r[j];
+  }
+};
+
+// Two LOAD copies (n0, n1 >= 1 units) with their first rounds' loads in
+// flight together.
+__device__ __forceinline__ void ph_copy2(const RpbProb &A, const PhMap &M, int ru0,
+                                         FastDiv fru0, const uint4 *src0, uint4 *lds0,
+                                         int g0, int n0, int ru1, FastDiv fru1,
+                                         const uint4 *src1, uint4 *lds1, int g1, int n1) {
+  const int kr = 4 * (int)blockDim.x;
+  PhRound a, b;
+  a.load(A, M, ru0, fru0, src0, g0, n0);
+  b.load(A, M, ru1, fru1, src1, g1, n1);
+  a.store(lds0);
+  b.store(lds1);
+  ph_copy<true>(A, M, ru0, fru0, src0, nullptr, lds0 + kr, g0 + kr, n0 - kr);
+  ph_copy<true>(A, M, ru1, fru1, src1, nullptr, lds1 + kr, g1 + kr, n1 - kr);
+}
+
 // The block's rows [row0, row0 + rows) and the virtual positions [lo, hi)
 // of their windows; the thread's row: virtual position, head, phase place.
 struct PhRows {
@@ -900,10 +943,10 @@ __device__ __forceinline__ void r1p_gather_body(int bid, int nblk, const RpbProb
   float *sw = reinterpret_cast<float *>(sm4);
   float4 *win = sm4 + (nthr * K + 3) / 4;
   int *spb = reinterpret_cast<int *>(win + (nthr + 2 * r1_halo(K, 1, A.H)) * NC);
-  ph_copy<true>(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(wgt), nullptr,
-                reinterpret_cast<uint4 *>(sw), R.row0 * K / 4, R.rows * K / 4);
-  ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(y), nullptr,
-                reinterpret_cast<uint4 *>(win), R.lo * U.ry, (R.hi - R.lo) * U.ry);
+  ph_copy2(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(wgt),
+           reinterpret_cast<uint4 *>(sw), R.row0 * K / 4, R.rows * K / 4, U.ry, U.fry,
+           reinterpret_cast<const uint4 *>(y), reinterpret_cast<uint4 *>(win), R.lo * U.ry,
+           (R.hi - R.lo) * U.ry);
   if (bpart != nullptr)
     spb[tid] = rwin_axis(K, A.d0, A.fd0, R.o.r + A.d0 * R.o.m, A.L0).pb;
   __syncthreads();
@@ -1015,10 +1058,10 @@ __device__ __forceinline__ void r1p_inverse_body(int bid, const RpbProb &A, cons
   const int hi = l.b * A.L0 + l.pstart + (l.m >= l.plen - K ? l.plen - 1 : l.m + K / 2) + 1;
   float4 *xs = sm4;                                     // cap rows of NC units
   float *ws = reinterpret_cast<float *>(sm4 + cap * NC);  // cap rows of K floats
-  ph_copy<true>(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(x), nullptr,
-                reinterpret_cast<uint4 *>(xs), lo * U.ry, (hi - lo) * U.ry);
-  ph_copy<true>(A, M, U.rk, U.frk, reinterpret_cast<const uint4 *>(w), nullptr,
-                reinterpret_cast<uint4 *>(ws), lo * U.rk, (hi - lo) * U.rk);
+  ph_copy2(A, M, U.ry, U.fry, reinterpret_cast<const uint4 *>(x),
+           reinterpret_cast<uint4 *>(xs), lo * U.ry, (hi - lo) * U.ry, U.rk, U.frk,
+           reinterpret_cast<const uint4 *>(w), reinterpret_cast<uint4 *>(ws), lo * U.rk,
+           (hi - lo) * U.rk);
   const int v = row0 + min(tid, rows - 1);
   const int vpos = (int)fdiv((uint32_t)v, A.fH);
   const int h = v - vpos * A.H;
