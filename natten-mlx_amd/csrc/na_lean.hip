@@ -367,33 +367,34 @@ __global__ void __launch_bounds__(512)
 // ---------------------------------------------------------------------------
 // Backward.
 
-// Stage the dK/dV role's query box: Q and dO rows to LDS (layout as
-// stage_box) and per row the pair (lse * log2(e), rowsum(dO * O) - dlse),
-// the row sum reduced over the D/8 consecutive lanes holding one row.
-template <typename T, int D, int R>
-__device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
-                                           const T *__restrict__ q,
-                                           const T *__restrict__ dout,
-                                           const T *__restrict__ out,
-                                           const float *__restrict__ lse,
-                                           const float *__restrict__ dlse,
-                                           typename L16<T>::e *qs,
-                                           typename L16<T>::e *os, int tid,
-                                           int nthr, int s0) {
+// One round of the dK/dV role's query-box staging: each lane's NU units of
+// Q and dO rows (layout as stage_box) and per row the pair (lse * log2(e),
+// rowsum(dO * O) - dlse), the row sum reduced over the D/8 consecutive
+// lanes holding one row.  load() only reads memory into registers, so a
+// wave may issue it before the barrier that ends the other waves' reads of
+// the LDS it will overwrite; store() writes the LDS.  NU: units per lane
+// in flight, by default two for the wider rank-1 heads, whose backward
+// keeps four waves per SIMD (its dK / dV accumulators and the key's own
+// rows stay live across the staging), else four.
+template <typename T, int D, int R, int NU_ = (R == 1 && D >= 64 ? 2 : 4)>
+struct QboxRound {
   typedef typename L16<T>::v8 v8;
-  constexpr int OCT = D / 8;
-  constexpr int RSE = lds_row(D);
-  // units per lane in flight: two for the wider rank-1 heads, whose
-  // backward keeps four waves per SIMD (its dK / dV accumulators and the
-  // key's own rows stay live across the staging)
-  constexpr int NU = R == 1 && D >= 64 ? 2 : 4;
-  const int nun = P.ebox * OCT;
-  const int o = tid % OCT;  // the lane's unit in each of its rows
-  for (int u0 = 0; u0 < nun; u0 += NU * nthr) {
-    v8 qr[NU], dr[NU], orr[NU];
-    float lr[NU], dl[NU];
-    int g[NU], la[NU];
+  typedef typename L16<T>::e E;
+  static constexpr int OCT = D / 8;
+  static constexpr int RSE = lds_row(D);
+  static constexpr int NU = NU_;
+  v8 qr[NU], dr[NU], orr[NU];
+  float lr[NU], dl[NU];
+  int la[NU];
+  __device__ __forceinline__ void load(const LProb &P, const LTile &t,
+                                       const T *__restrict__ q, const T *__restrict__ dout,
+                                       const T *__restrict__ out,
+                                       const float *__restrict__ lse,
+                                       const float *__restrict__ dlse, int u0, int tid,
+                                       int nthr, int s0) {
+    int g[NU];
     unit_walk<R, OCT, RSE, NU, false>(P, t, u0, tid, nthr, s0, g, la);
+    const int o = tid % OCT;  // the lane's unit in each of its rows
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
       // element offsets are non-negative: an unsigned division is a shift
@@ -404,6 +405,9 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
       lr[j] = ldf(lse, row);
       dl[j] = dlse != nullptr ? ldf(dlse, row) : 0.f;
     }
+  }
+  __device__ __forceinline__ void store(E *qs, E *os, int tid) const {
+    const int o = tid % OCT;
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
       *reinterpret_cast<v8 *>(qs + la[j]) = qr[j];
@@ -423,6 +427,27 @@ __device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
         *reinterpret_cast<float2 *>(qs + la[j] + D) =
             make_float2(lr[j] * kLog2e, dl[j] - part);
     }
+  }
+};
+
+// Stage the dK/dV role's query box from unit u_begin on (the rounds before
+// it staged by the caller), then clear the slack rows.
+template <typename T, int D, int R>
+__device__ __forceinline__ void stage_qbox(const LProb &P, const LTile &t,
+                                           const T *__restrict__ q,
+                                           const T *__restrict__ dout,
+                                           const T *__restrict__ out,
+                                           const float *__restrict__ lse,
+                                           const float *__restrict__ dlse,
+                                           typename L16<T>::e *qs,
+                                           typename L16<T>::e *os, int tid,
+                                           int nthr, int s0, int u_begin) {
+  typedef QboxRound<T, D, R> QR;
+  const int nun = P.ebox * QR::OCT;
+  for (int u0 = u_begin; u0 < nun; u0 += QR::NU * nthr) {
+    QR r;
+    r.load(P, t, q, dout, out, lse, dlse, u0, tid, nthr, s0);
+    r.store(qs, os, tid);
   }
   zero_slack<T, D>(P, qs, tid, nthr);
 }
@@ -817,12 +842,28 @@ __global__ void __launch_bounds__(512)
   const int qbase0 = t.kbase;  // query box rows of head hk * rep
   const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
   const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
+  // rank 1 and 2 (without the slab prefetch): the first query box's first
+  // round (three units per lane, two for the wider rank-1 heads) is loaded
+  // before the barrier that ends the dQ half's reads of the K/V box, so a
+  // wave that is done with dQ has those loads in flight while the others
+  // finish (rank 3 keeps its registers for the slabs)
+  constexpr bool PRE = R <= 2 && !PFS;
+  typedef QboxRound<T, D, R, (R == 1 && D >= 64 ? 2 : 3)> QP;
   for (int hr = 0; hr < P.rep; ++hr) {
     t.kbase = qbase0 + hr * D;  // query head hk * rep + hr
     for (int si = 0; si < nsl; ++si) {
     const int s0 = si * P.sl;
-    __syncthreads();  // the LDS reads of the previous box or slab are done
-    stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr, s0);
+    if (PRE && hr == 0 && si == 0) {
+      QP pre;
+      pre.load(P, t, q, dout, out, lse, dlse, 0, tid, nthr, s0);
+      __syncthreads();
+      pre.store(xs, ys, tid);
+      stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr, s0,
+                          QP::NU * nthr);
+    } else {
+      __syncthreads();  // the LDS reads of the previous box or slab are done
+      stage_qbox<T, D, R>(P, t, q, dout, out, lse, dlse, xs, ys, tid, nthr, s0, 0);
+    }
     __syncthreads();
     if (!ws.any) continue;
     const int a0 = R == 3 ? max(ws.ws[0], s0) : 0;
