@@ -842,18 +842,19 @@ __global__ void __launch_bounds__(512)
   const int qbase0 = t.kbase;  // query box rows of head hk * rep
   const int nsl = R == 3 ? (t.E[0] + P.sl - 1) / P.sl : 1;
   const int rows1 = R > 1 ? ws.we[1] - ws.ws[1] : 1;
-  // rank 1 and 2 (without the slab prefetch): the first query box's first
-  // round (three units per lane, two for the wider rank-1 heads) is loaded
-  // before the barrier that ends the dQ half's reads of the K/V box, so a
-  // wave that is done with dQ has those loads in flight while the others
-  // finish (rank 3 keeps its registers for the slabs)
+  // rank 1 and 2 (without the slab prefetch): each query box's first round
+  // (three units per lane, two for the wider rank-1 heads) is loaded before
+  // the barrier that ends the reads of the LDS it replaces (the dQ half's
+  // K/V box, or the previous query head's box), so a wave that is done
+  // with its chunks has those loads in flight while the others finish
+  // (rank 3 keeps its registers for the slabs)
   constexpr bool PRE = R <= 2 && !PFS;
   typedef QboxRound<T, D, R, (R == 1 && D >= 64 ? 2 : 3)> QP;
   for (int hr = 0; hr < P.rep; ++hr) {
     t.kbase = qbase0 + hr * D;  // query head hk * rep + hr
     for (int si = 0; si < nsl; ++si) {
     const int s0 = si * P.sl;
-    if (PRE && hr == 0 && si == 0) {
+    if (PRE) {
       QP pre;
       pre.load(P, t, q, dout, out, lse, dlse, 0, tid, nthr, s0);
       __syncthreads();
