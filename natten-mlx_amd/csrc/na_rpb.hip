@@ -1123,11 +1123,11 @@ __global__ void __launch_bounds__(512)
                           cap);
 }
 
-// A backward's two passes on the phase-major rows in one launch: blocks
-// [0, n0) the first pass (QK: dq by the gather over dlogits, with the bias
-// partials when bpart is set; AV: dattn by the dot of dout with the
-// values), the others the inverse (dk or dv); each pass's row blocks in
-// contiguous runs per XCD as in k_r1_qkb.
+// A backward's two passes on the phase-major rows in one launch, n0 blocks
+// each: QK, dq by the gather over dlogits (with the bias partials when
+// bpart is set) in blocks [0, n0), then dk; AV, dv first, then dattn by the
+// dot of dout with the values; each pass's row blocks in contiguous runs
+// per XCD as in k_r1_qkb.
 template <int K, int NC>
 __global__ void __launch_bounds__(512)
     k_r1p_qkb(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ dl,
@@ -1146,11 +1146,12 @@ __global__ void __launch_bounds__(512)
     k_r1p_avb(RpbProb A, PhMap M, PhUnits U, const float *__restrict__ attn,
               const float *__restrict__ v, const float *__restrict__ dout,
               float *__restrict__ dattn, float *__restrict__ dv, int n0, int cap) {
+  // the dv pass's blocks first, as in k_r1_avb
   const int bid = (int)blockIdx.x;
-  if (bid < n0)
-    r1p_dot_body<K, NC>(xcd_block(bid, n0), A, M, U, dout, v, nullptr, dattn, 0);
+  if (bid >= n0)
+    r1p_dot_body<K, NC>(xcd_block(bid - n0, n0), A, M, U, dout, v, nullptr, dattn, 0);
   else
-    r1p_inverse_body<K, NC>(xcd_block(bid - n0, n0), A, M, U, attn, dout, dv, 1.f, cap);
+    r1p_inverse_body<K, NC>(xcd_block(bid, n0), A, M, U, attn, dout, dv, 1.f, cap);
 }
 
 // dk / dv: out[j] = post * sum over the queries i whose window holds key j
@@ -1287,12 +1288,12 @@ __global__ void __launch_bounds__(512)
   r1_inverse_body<K, NC, D1>(xcd_block((int)blockIdx.x, (int)gridDim.x), A, w, x, out, post);
 }
 
-// The two passes of a backward in one launch (they are independent): blocks
-// [0, n0) run the first pass, the others the inverse (dk or dv).  QK
-// backward: dq by the gather over dlogits (with the bias partials when bpart
-// is set) and dk; AV backward: dattn by the dot of dout with the values and
-// dv.  Each pass deals its row blocks to the XCDs in contiguous runs
-// (xcd_block), the two passes' dispatch ranges kept apart: interleaving the
+// The two passes of a backward in one launch (they are independent), n0
+// blocks each.  QK backward: dq by the gather over dlogits (with the bias
+// partials when bpart is set), blocks [0, n0), then dk; AV backward: dv
+// first, then dattn by the dot of dout with the values.  Each pass deals
+// its row blocks to the XCDs in contiguous runs (xcd_block), the two
+// passes' dispatch ranges kept apart: interleaving the
 // passes block by block in one run per XCD was slower (config 5 K=7 d=1
 // QK backward 13.0 -> 13.8 us; the passes apart 12.7 us).
 template <int K, int NC, bool D1>
@@ -1312,11 +1313,15 @@ __global__ void __launch_bounds__(512)
     k_r1_avb(RpbProb A, const float *__restrict__ attn, const float *__restrict__ v,
              const float *__restrict__ dout, float *__restrict__ dattn,
              float *__restrict__ dv, int n0) {
+  // the dv pass's blocks are dispatched first here, the dq pass's in
+  // k_r1_qkb (config 5 AV backward, dattn pass first -> dv pass first:
+  // K=7 d=1 7.12 -> 6.77 us, K=3 d=8 7.62 -> 6.53, K=5 d=1 6.31 -> 5.60;
+  // the QK pairs the other way round: K=7 d=1 12.7 -> 13.5 us)
   const int bid = (int)blockIdx.x;
-  if (bid < n0)
-    r1_dot_body<K, NC>(xcd_block(bid, n0), A, dout, v, nullptr, dattn, 0);
+  if (bid >= n0)
+    r1_dot_body<K, NC>(xcd_block(bid - n0, n0), A, dout, v, nullptr, dattn, 0);
   else
-    r1_inverse_body<K, NC, D1>(xcd_block(bid - n0, n0), A, attn, dout, dv, 1.f);
+    r1_inverse_body<K, NC, D1>(xcd_block(bid, n0), A, attn, dout, dv, 1.f);
 }
 
 // out[j] = sum over (r, n) with nbr(r, n) == j of w[r, n] * x'[r]: the
