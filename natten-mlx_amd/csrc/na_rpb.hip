@@ -1801,16 +1801,19 @@ size_t r1_inverse_lds(const RpbProb &A, int rb) {
 }
 size_t r1_inverse_lds(const RpbProb &A) { return r1_inverse_lds(A, rpb_block(A)); }
 
-// Rows per block of the AV backward's staged pair (k_r1_avb): 512 where
-// 6 <= K d <= 16 and its LDS fits, else the forward's (config 5 av
-// backward, the forward's rows -> 512: K=7 d=1 7.70 -> 7.01 us, K=5 d=2
-// 8.44 -> 7.81, K=3 d=4 7.29 -> 6.91; K=5 d=1 6.25 -> 6.41 and K=3 d=8
-// 7.50 -> 8.04 keep 256; K=3 d=1 keeps 256).
+// Rows per block of the AV backward's staged pair (k_r1_avb), with the dv
+// blocks dispatched first: 512 at d = 1 from K = 7, 256 at larger
+// dilations, where the staged kernels take them (config 5 av backward:
+// K=7 d=1 6.80 at 256 rows, 6.64 at 512; K=5 d=1 5.53 / 6.03; K=3 d=2
+// 5.54 / 5.89; K=3 d=4 6.12 at 256, 6.28 at 384, 6.52 at 512; K=5 d=2
+// 6.77 / 6.88 / 7.36 us).
 int avb_block(const RpbProb &A) {
   const int rb = rpb_block(A);
-  if (block_forced() || A.K0 * A.d0 < 6 || A.K0 * A.d0 > 16 || rb >= 512) return rb;
-  const size_t li = r1_inverse_lds(A, 512);
-  return r1_lds(A, 512, false) != 0 && li != 0 && li <= 65536 ? 512 : rb;
+  if (block_forced()) return rb;
+  const int want = A.d0 == 1 && A.K0 >= 7 ? 512 : A.d0 > 1 ? 256 : rb;
+  if (want == rb) return rb;
+  const size_t li = r1_inverse_lds(A, want);
+  return r1_lds(A, want, false) != 0 && li != 0 && li <= 65536 ? want : rb;
 }
 
 // Rows per block of the QK backward's staged pair (k_r1_qkb): 512 where
